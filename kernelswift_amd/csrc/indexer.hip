@@ -1,0 +1,109 @@
+// Fused indexer entry: RoPE (q at start_pos + s, k at t) -> row statistics -> exact scores -> exact top-k.
+//
+// Semantics of baseline/indexer.py:161-206 after the two projections (which stay in the caller):
+// RoPE on the configured segment of q (and k), score = sum_h w_h * relu(bf16(q_h . k)), causal mask,
+// sorted top-k with lowest-index ties, -1 / +offset post-processing.  Replaces the reference's three-op
+// sequence rope_inplace -> fused_qk_reduce -> topk_mask (optimized/indexer_project/indexer.py:197-222).
+// All intermediates live in the caller's workspace; inputs are never modified.
+#include "common.h"
+#include "indexer_common.h"
+
+namespace {
+
+struct IndexerWs {
+  uint16_t *q_rot;
+  uint16_t *k_rot;
+  float *q_norm;
+  int32_t *q_span;
+  float *k_norm;
+  int32_t *k_span;
+  float *scores;
+  size_t bytes;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+IndexerWs carve(void *base, int64_t B, int64_t S, int64_t H, int64_t D, int64_t T) {
+  IndexerWs w{};
+  size_t off = 0;
+  auto take = [&](size_t n) {
+    char *p = base ? static_cast<char *>(base) + off : nullptr;
+    off += align256(n);
+    return p;
+  };
+  w.q_rot = reinterpret_cast<uint16_t *>(take(size_t(B * S * H * D) * 2));
+  w.k_rot = reinterpret_cast<uint16_t *>(take(size_t(B * T * D) * 2));
+  w.q_norm = reinterpret_cast<float *>(take(size_t(B * S * H) * 4));
+  w.q_span = reinterpret_cast<int32_t *>(take(size_t(B * S * H) * 4));
+  w.k_norm = reinterpret_cast<float *>(take(size_t(B * T) * 4));
+  w.k_span = reinterpret_cast<int32_t *>(take(size_t(B * T) * 4));
+  w.scores = reinterpret_cast<float *>(take(size_t(B * S * T) * 4));
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace
+
+extern "C" size_t ks_indexer_workspace_size(int64_t B, int64_t S, int64_t H, int64_t D, int64_t T) {
+  if (B < 0 || S < 0 || H < 0 || D < 0 || T < 0) return 0;
+  return carve(nullptr, B, S, H, D, T).bytes;
+}
+
+extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,
+                          int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
+                          int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out,
+                          int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D, int64_t T,
+                          int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(D == 128, "ks_indexer: D=%lld, the kernels are built for head_dim 128", (long long)D);
+  KS_CHECK_ARG(H == 16 || H == 32 || H == 64, "ks_indexer: H=%lld must be 16, 32 or 64", (long long)H);
+  KS_CHECK_ARG(B >= 0 && S >= 0, "ks_indexer: negative B or S");
+  KS_CHECK_ARG(T >= 1 && T <= 65536, "ks_indexer: T=%lld must be in [1, 65536]", (long long)T);
+  KS_CHECK_ARG(k_batch_stride >= T, "ks_indexer: k_batch_stride < T");
+  KS_CHECK_ARG(ratio >= 1 && start_pos >= 0, "ks_indexer: ratio must be >= 1 and start_pos >= 0");
+  KS_CHECK_ARG(k_top >= 1, "ks_indexer: k_top must be >= 1");
+  KS_CHECK_ARG(rope_dim >= 0 && rope_dim % 8 == 0 && rope_start >= 0 && rope_start % 8 == 0 &&
+                   rope_start + rope_dim <= D,
+               "ks_indexer: rotated segment must be 8-aligned and inside the head");
+  if (rope_dim > 0) {
+    KS_CHECK_ARG(freqs != nullptr, "ks_indexer: freqs is null");
+    KS_CHECK_ARG(start_pos + S <= freq_rows, "ks_indexer: query positions exceed freqs rows");
+    KS_CHECK_ARG(!rope_k || T <= freq_rows, "ks_indexer: key positions exceed freqs rows");
+  }
+  const int64_t kk = k_top < T ? k_top : T;
+  KS_CHECK_ARG(kk <= 4096, "ks_indexer: min(k_top, T)=%lld exceeds 4096", (long long)kk);
+  if (B * S == 0) return KS_OK;
+  KS_CHECK_ARG(q && k && w && out, "ks_indexer: null pointer");
+  KS_CHECK_ARG(ks::aligned(q, 16) && ks::aligned(k, 16), "ks_indexer: q and k must be 16-byte aligned");
+  const IndexerWs ws = carve(workspace, B, S, H, D, T);
+  KS_CHECK_ARG(workspace != nullptr && workspace_bytes >= ws.bytes,
+               "ks_indexer: workspace of %zu bytes required, %zu given", ws.bytes, workspace_bytes);
+  KS_CHECK_ARG(ks::aligned(workspace, 256), "ks_indexer: workspace must be 256-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rs = static_cast<int>(rope_start), rd = static_cast<int>(rope_dim);
+
+  // q: rotate at positions start_pos + s into the workspace copy, with row statistics
+  int rc = ks::launch_rope_rows(q, ws.q_rot, freqs, B * S * H, 128, static_cast<int>(H), S, start_pos, rs, rd,
+                                ws.q_norm, ws.q_span, st);
+  if (rc != KS_OK) return rc;
+  // k: rotate at positions t (or copy) per batch, with row statistics
+  const int rdk = rope_k ? rd : 0;
+  for (int64_t b = 0; b < B; ++b) {
+    rc = ks::launch_rope_rows(k + b * k_batch_stride * D, ws.k_rot + b * T * D, freqs, T, 128, 1, T, 0, rs, rdk,
+                              ws.k_norm + b * T, ws.k_span + b * T, st);
+    if (rc != KS_OK) return rc;
+    if (k_batch_stride == T) {  // contiguous batches: the first launch may cover all of them
+      if (b == 0 && B > 1) {
+        rc = ks::launch_rope_rows(k + T * D, ws.k_rot + T * D, freqs, (B - 1) * T, 128, 1, T, 0, rs, rdk,
+                                  ws.k_norm + T, ws.k_span + T, st);
+        if (rc != KS_OK) return rc;
+      }
+      break;
+    }
+  }
+  rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, w_bf16 ? 1 : 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span,
+                                 ws.scores, B, S, H, T, T, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC,
+                                 nullptr, st);
+  if (rc != KS_OK) return rc;
+  return ks_indexer_topk(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, stream);
+}

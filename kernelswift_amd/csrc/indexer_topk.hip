@@ -1,0 +1,251 @@
+// Exact sorted top-k per score row with the reference's -1 / +offset post-processing (gfx950).
+//
+// Semantics: index_score.topk(k) + post-processing (baseline/indexer.py:195-206), with the tie order
+// of a stable descending sort (equal scores keep ascending column order; -inf sorts last) that the
+// reference TopK kernel reproduces (optimized/indexer_project/design.md:99-105,
+// optimized/indexer_project/op_kernel/indexer_topk.asc:219-246).
+//
+// One 1024-lane workgroup per row.  The row is read once into registers (column j*1024 + lane),
+// converted to order-preserving uint32 keys.  A 3-pass LDS radix select (11 + 11 + 10 bits) finds the
+// k-th largest key K*; keys > K* are collected unordered, keys == K* are collected in column order
+// (ordered block scan) only when more of them exist than are needed; the k winners are then bitonic
+// sorted in LDS on the 64-bit composite (key, ~column), which is exactly (score desc, column asc).
+//
+// Causal rows: columns >= limit = (start_pos + s + 1) / ratio are -inf by definition of the masked
+// scores (baseline/indexer.py:185-193), so they are never read: the valid prefix is selected and, when
+// it holds fewer than k columns, the remaining slots are the masked columns in ascending order, which
+// post-processing turns into -1 (the reference's prefix pruning, indexer_topk.asc:96-152).
+#include "common.h"
+
+namespace ks {
+namespace {
+
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkWaves = kTopkThreads / 64;
+constexpr int kTopkMaxK = 4096;
+
+// fp32 -> uint32 whose unsigned order equals the float order; -0 is canonicalised to +0.
+// Key 0 is reserved for "absent" (it would be a negative NaN, which is outside the contract).
+__device__ __forceinline__ uint32_t score_key(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) == 0) u = 0;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inclusive prefix sum over the 1024 lanes of the block (lane order).  `wsum` is kTopkWaves ints of LDS.
+__device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t *wsum) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  if (lane == 63) wsum[wave] = v;
+  __syncthreads();
+  uint32_t base = 0;
+  for (int w = 0; w < wave; ++w) base += wsum[w];
+  __syncthreads();
+  return v + base;
+}
+
+struct SelShared {
+  uint32_t hist[2048];
+  uint32_t wsum[kTopkWaves];
+  uint32_t digit;
+  uint32_t k_rem;
+  uint32_t bucket_count;
+  uint32_t n_gt;
+};
+
+// One radix pass: histogram of digit (key >> shift) & (nbins-1) among keys whose bits above the
+// digit equal `prefix` under `mask`; then locate the bucket holding the k_rem-th largest.
+template <int KPT>
+__device__ __forceinline__ void radix_pass(const uint32_t (&key)[KPT], uint32_t prefix, uint32_t mask, int shift,
+                                           int nbins, SelShared &sh) {
+  // k_rem must be read before the barrier that precedes this pass's single update of it
+  const uint32_t k_rem = sh.k_rem;
+  for (int i = threadIdx.x; i < 2048; i += kTopkThreads) sh.hist[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const uint32_t kk = key[j];
+    if (kk != 0 && (kk & mask) == prefix) atomicAdd(&sh.hist[(kk >> shift) & (nbins - 1)], 1u);
+  }
+  __syncthreads();
+  // Lane t owns bins hi = nbins-1-2t and lo = hi-1 (two bins per lane for 2048, one for 1024):
+  // an inclusive lane-order scan is then a suffix sum over bins from the top.
+  const int per = nbins / kTopkThreads;  // 2 or 1
+  const int hi = nbins - 1 - per * static_cast<int>(threadIdx.x);
+  const uint32_t c_hi = sh.hist[hi];
+  const uint32_t c_lo = per == 2 ? sh.hist[hi - 1] : 0u;
+  const uint32_t mine = c_hi + c_lo;
+  const uint32_t incl = block_inclusive_scan(mine, sh.wsum);
+  const uint32_t excl = incl - mine;
+  if (excl < k_rem && incl >= k_rem) {
+    if (excl + c_hi >= k_rem) {
+      sh.digit = static_cast<uint32_t>(hi);
+      sh.bucket_count = c_hi;
+      sh.k_rem = k_rem - excl;
+    } else {
+      sh.digit = static_cast<uint32_t>(hi - 1);
+      sh.bucket_count = c_lo;
+      sh.k_rem = k_rem - excl - c_hi;
+    }
+  }
+  __syncthreads();
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__restrict__ scores, int64_t ld,
+                                                                int64_t S, int T, int k, int causal,
+                                                                int64_t start_pos, int ratio, int64_t offset,
+                                                                void *__restrict__ out, int out_i64, int P) {
+  extern __shared__ uint64_t cand[];  // P composites
+  __shared__ SelShared sh;
+  const int64_t row = blockIdx.x;
+  const int64_t s = row % S;
+  const int tid = threadIdx.x;
+  int64_t limit = INT64_MAX;
+  int n_valid = T;
+  if (causal) {
+    limit = (start_pos + s + 1) / ratio;
+    n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
+  }
+  const int k_sel = k < n_valid ? k : n_valid;
+  const float *src = scores + row * ld;
+
+  uint32_t key[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int col = j * kTopkThreads + tid;
+    key[j] = col < n_valid ? score_key(src[col]) : 0u;
+  }
+  for (int i = tid; i < P; i += kTopkThreads) cand[i] = 0ull;
+  if (tid == 0) {
+    sh.k_rem = static_cast<uint32_t>(k_sel);
+    sh.n_gt = 0;
+  }
+  __syncthreads();
+
+  if (k_sel > 0) {
+    // ---- radix select of the k_sel-th largest key
+    radix_pass<KPT>(key, 0u, 0u, 21, 2048, sh);
+    const uint32_t d1 = sh.digit;
+    radix_pass<KPT>(key, d1 << 21, 0xFFE00000u, 10, 2048, sh);
+    const uint32_t d2 = sh.digit;
+    radix_pass<KPT>(key, (d1 << 21) | (d2 << 10), 0xFFFFFC00u, 0, 1024, sh);
+    const uint32_t kstar = (d1 << 21) | (d2 << 10) | sh.digit;
+    const uint32_t take_eq = sh.k_rem;          // how many keys == K* are selected (>= 1)
+    const uint32_t eq_total = sh.bucket_count;  // how many keys == K* exist
+    const uint32_t n_gt = static_cast<uint32_t>(k_sel) - take_eq;
+
+    // ---- collect keys > K* (unordered) and, if all of them are taken, keys == K*
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const uint32_t kk = key[j];
+      const bool take = kk > kstar || (kk == kstar && take_eq == eq_total);
+      if (take) {
+        const uint32_t pos = atomicAdd(&sh.n_gt, 1u);
+        const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
+        cand[pos] = (static_cast<uint64_t>(kk) << 32) | static_cast<uint64_t>(~col);
+      }
+    }
+    // ---- ties at K*: the take_eq lowest columns, found with an ordered scan (column = j*1024 + lane)
+    if (take_eq != eq_total) {
+      uint32_t base = 0;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const uint32_t f = key[j] == kstar ? 1u : 0u;
+        const uint32_t incl = block_inclusive_scan(f, sh.wsum);
+        const uint32_t rank = base + incl - f;
+        if (f && rank < take_eq) {
+          const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
+          cand[n_gt + rank] = (static_cast<uint64_t>(kstar) << 32) | static_cast<uint64_t>(~col);
+        }
+        // block total of this slice = sum of the per-wave totals left in wsum by the scan
+        uint32_t tot = 0;
+        for (int w = 0; w < kTopkWaves; ++w) tot += sh.wsum[w];
+        base += tot;
+        __syncthreads();  // wsum is rewritten by the next slice's scan
+      }
+    }
+    __syncthreads();
+
+    // ---- bitonic sort of P composites, descending
+    for (int size = 2; size <= P; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < (P >> 1); i += kTopkThreads) {
+          const int a = 2 * stride * (i / stride) + (i % stride);
+          const int b = a + stride;
+          const uint64_t va = cand[a], vb = cand[b];
+          const bool desc = (a & size) == 0;
+          if (desc ? (va < vb) : (va > vb)) {
+            cand[a] = vb;
+            cand[b] = va;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- post-processing and store (baseline/indexer.py:198-206)
+  for (int j = tid; j < k; j += kTopkThreads) {
+    int64_t col;
+    if (j < k_sel) {
+      col = static_cast<int64_t>(~static_cast<uint32_t>(cand[j] & 0xFFFFFFFFull));
+    } else {
+      col = static_cast<int64_t>(n_valid) + (j - k_sel);  // masked columns, ascending (-inf ties)
+    }
+    const int64_t v = (causal && col >= limit) ? int64_t(-1) : col + offset;
+    if (out_i64) {
+      static_cast<int64_t *>(out)[row * k + j] = v;
+    } else {
+      static_cast<int32_t *>(out)[row * k + j] = static_cast<int32_t>(v);
+    }
+  }
+}
+
+template <int KPT>
+int launch_topk(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal, int64_t start_pos,
+                int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream) {
+  int P = 1;
+  while (P < k) P <<= 1;
+  if (P < 2) P = 2;
+  const size_t shmem = static_cast<size_t>(P) * sizeof(uint64_t);
+  hipLaunchKernelGGL(topk_rows_kernel<KPT>, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, stream,
+                     scores, ld, S, T, k, causal, start_pos, ratio, offset, out, out_i64, P);
+  KS_CHECK_LAUNCH("topk_rows_kernel");
+  return KS_OK;
+}
+
+}  // namespace
+}  // namespace ks
+
+extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
+                               int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out,
+                               int32_t out_i64, void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(B >= 0 && S >= 0, "ks_indexer_topk: negative B or S");
+  KS_CHECK_ARG(T >= 1 && T <= 65536, "ks_indexer_topk: T=%lld must be in [1, 65536]", (long long)T);
+  KS_CHECK_ARG(k >= 1 && k <= T && k <= ks::kTopkMaxK, "ks_indexer_topk: k=%lld must be in [1, min(T, %d)]",
+               (long long)k, ks::kTopkMaxK);
+  KS_CHECK_ARG(ld >= T, "ks_indexer_topk: ld=%lld < T=%lld", (long long)ld, (long long)T);
+  KS_CHECK_ARG(ratio >= 1, "ks_indexer_topk: ratio=%d must be >= 1", ratio);
+  KS_CHECK_ARG(start_pos >= 0, "ks_indexer_topk: start_pos must be >= 0");
+  const int64_t rows = B * S;
+  if (rows == 0) return KS_OK;
+  KS_CHECK_ARG(rows < (int64_t(1) << 31), "ks_indexer_topk: too many rows");
+  KS_CHECK_ARG(scores != nullptr && out != nullptr, "ks_indexer_topk: null pointer");
+  KS_CHECK_ARG(ks::aligned(scores, 4) && ks::aligned(out, out_i64 ? 8 : 4), "ks_indexer_topk: misaligned pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
+  const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
+  if (T <= 1024) return ks::launch_topk<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+  if (T <= 2048) return ks::launch_topk<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+  if (T <= 4096) return ks::launch_topk<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+  if (T <= 8192) return ks::launch_topk<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+  if (T <= 16384) return ks::launch_topk<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+  if (T <= 32768) return ks::launch_topk<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+  return ks::launch_topk<64>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+}

@@ -1,0 +1,218 @@
+"""Torch-facing operators over the C ABI of libkswift_amd.so.
+
+Each function mirrors one op of the reference's torch extensions (same name or
+the reference name in the docstring, same argument meaning, RuntimeError on
+invalid input like TORCH_CHECK) and launches the gfx950 kernels on the current
+HIP stream without synchronising.  PyTorch only provides device memory and the
+stream; there is no CPU or torch fallback: a tensor on the wrong device, a
+missing library or an unsupported shape raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "sinkhorn", "rope_inplace", "indexer_row_stats", "indexer_scores", "topk_mask", "indexer",
+    "indexer_workspace_size", "sparse_attn", "sparse_attn_workspace_size", "copy_bytes",
+]
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _on_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        _check(t.is_cuda, "tensors must be on the GPU (there is no CPU path)")
+        _check(t.is_contiguous(), "tensors must be contiguous")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _p(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------- Sinkhorn
+def sinkhorn(x: torch.Tensor, repeat: int = 10, eps: float = 1e-6) -> torch.Tensor:
+    """sinkhorn_torch(x, repeat, eps) (optimized/sinkhorn_project/op_extension/sinkhorn_torch.cpp:18).
+
+    x: float32 [..., 4, 4] (any leading dims; the reference required 4-D and <= 2560 matrices).
+    Returns a new tensor (out-of-place, like the reference's empty_like output)."""
+    _check(x.dtype == torch.float32, "x must be float32")
+    _on_gpu(x)
+    _check(x.dim() >= 2 and x.shape[-1] == 4 and x.shape[-2] == 4, "x must be [..., 4, 4]")
+    _check(repeat >= 1, "repeat must be >= 1")
+    out = torch.empty_like(x)
+    n = x.numel() // 16
+    _lib.check(_lib.load().ks_sinkhorn(_p(x), _p(out), n, int(repeat), float(eps), _stream(x)), "sinkhorn")
+    return out
+
+
+# ---------------------------------------------------------------- indexer
+def rope_inplace(x: torch.Tensor, freqs: torch.Tensor, rope_start: Optional[int] = None, rope_dim: Optional[int] = None,
+                 pos0: int = 0) -> None:
+    """rope_inplace(q, freqs) (optimized/indexer_project/op_extension/indexer_torch.cpp:174).
+
+    x: bf16 [B, S, H, D] or [B, S, D], rotated in place.  freqs: float32 [rows, P, 2] (cos, sin), the real
+    view of freqs_cis.  Default segment = the trailing 2P dims (the reference op's choice); pass
+    rope_start=0 for the leading dims.  Token s uses freqs row pos0 + s."""
+    _check(x.dtype == torch.bfloat16, "x must be bfloat16")
+    _check(freqs.dtype == torch.float32 and freqs.dim() == 3 and freqs.shape[2] == 2, "freqs must be float32 [s, p, 2]")
+    _on_gpu(x, freqs)
+    _check(x.dim() in (3, 4), "x must be [b, s, h, d] or [b, s, d]")
+    B, S = x.shape[0], x.shape[1]
+    H = x.shape[2] if x.dim() == 4 else 1
+    D = x.shape[-1]
+    P = freqs.shape[1]
+    rd = 2 * P if rope_dim is None else rope_dim
+    _check(rd == 2 * P, "rope_dim must equal 2 * freqs.shape[1]")
+    rs = D - rd if rope_start is None else rope_start
+    _lib.check(_lib.load().ks_rope_inplace(_p(x), _p(freqs), B, S, H, D, rs, rd, pos0, freqs.shape[0], _stream(x)),
+               "rope_inplace")
+
+
+def indexer_row_stats(x: torch.Tensor):
+    """Row statistics (norm upper bound, span) of bf16 rows of length 128 for indexer_scores."""
+    _check(x.dtype == torch.bfloat16 and x.shape[-1] == 128, "x must be bfloat16 [..., 128]")
+    _on_gpu(x)
+    rows = x.numel() // 128
+    norm = torch.empty(rows, dtype=torch.float32, device=x.device)
+    span = torch.empty(rows, dtype=torch.int32, device=x.device)
+    _lib.check(_lib.load().ks_indexer_row_stats(_p(x), rows, 128, _p(norm), _p(span), _stream(x)), "indexer_row_stats")
+    return norm, span
+
+
+def indexer_scores(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, causal: bool, start_pos: int = 0,
+                   ratio: int = 1, T: Optional[int] = None, stats=None) -> torch.Tensor:
+    """fused_qk_reduce(q, kvT, weights, causal, ratio) (indexer_torch.cpp:100), generalised.
+
+    q: bf16 [B, S, H, 128] (already rotated); k: bf16 [B, Tk, 128] (untransposed, first T rows used);
+    weights: float32 or bf16 [B, S, H].  Returns float32 scores [B, S, T] with -inf where masked.
+    stats: optional ((q_norm, q_span), (k_norm, k_span)) from indexer_row_stats."""
+    _check(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16, "q and k must be bfloat16")
+    _check(weights.dtype in (torch.float32, torch.bfloat16), "weights must be float32 or bfloat16")
+    _on_gpu(q, k, weights)
+    _check(q.dim() == 4 and k.dim() == 3 and weights.dim() == 3, "q [b,s,h,d], k [b,t,d], weights [b,s,h]")
+    B, S, H, D = q.shape
+    _check(k.shape[0] == B and k.shape[2] == D, "k shape mismatch")
+    _check(tuple(weights.shape) == (B, S, H), "weights shape mismatch")
+    Tk = k.shape[1]
+    T = Tk if T is None else T
+    if stats is None:
+        stats = (indexer_row_stats(q), indexer_row_stats(k))
+    (qn, qs), (kn, ks_) = stats
+    out = torch.empty((B, S, T), dtype=torch.float32, device=q.device)
+    _lib.check(_lib.load().ks_indexer_scores(_p(q), _p(k), _p(weights), 1 if weights.dtype == torch.bfloat16 else 0,
+                                             _p(qn), _p(qs), _p(kn), _p(ks_), _p(out), B, S, H, D, T, Tk,
+                                             1 if causal else 0, start_pos, ratio, _stream(q)), "indexer_scores")
+    return out
+
+
+def topk_mask(scores: torch.Tensor, causal: bool, ratio: int, actual_t: int, offset: int, k: int = 128,
+              start_pos: int = 0, out_dtype: torch.dtype = torch.int64) -> torch.Tensor:
+    """topk_mask(scores, causal, ratio, actualT, offset) (indexer_torch.cpp:232), generalised.
+
+    scores: float32 [B, S, ld] (first actual_t columns used).  Returns [B, S, min(k, actual_t)] indices
+    sorted by (score desc, column asc); causal: column >= (start_pos+s+1)//ratio -> -1, else +offset."""
+    _check(scores.dtype == torch.float32, "scores must be float32")
+    _on_gpu(scores)
+    _check(scores.dim() == 3, "scores must be [b, s, t]")
+    _check(out_dtype in (torch.int32, torch.int64), "out_dtype must be int32 or int64")
+    B, S, ld = scores.shape
+    kk = min(k, actual_t)
+    out = torch.empty((B, S, kk), dtype=out_dtype, device=scores.device)
+    _lib.check(_lib.load().ks_indexer_topk(_p(scores), ld, B, S, actual_t, kk, 1 if causal else 0, start_pos, ratio,
+                                           offset, _p(out), 1 if out_dtype == torch.int64 else 0, _stream(scores)),
+               "topk_mask")
+    return out
+
+
+def indexer_workspace_size(B: int, S: int, H: int, D: int, T: int) -> int:
+    return int(_lib.load().ks_indexer_workspace_size(B, S, H, D, T))
+
+
+def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Optional[torch.Tensor], k_top: int,
+            causal: bool, start_pos: int, ratio: int = 1, offset: int = 0, rope_start: int = 0, rope_dim: int = 64,
+            rope_k: bool = True, out_dtype: torch.dtype = torch.int32,
+            workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Fused RoPE -> exact scores -> exact top-k (the reference wrapper's three-op sequence,
+    optimized/indexer_project/indexer.py:197-222).  Inputs are not modified.
+
+    q: bf16 [B, S, H, 128]; k: bf16 [B, T, 128]; weights float32/bf16 [B, S, H];
+    freqs: float32 [rows, rope_dim/2, 2].  Returns [B, S, min(k_top, T)] int32 (default) or int64."""
+    _check(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16, "q and k must be bfloat16")
+    _check(weights.dtype in (torch.float32, torch.bfloat16), "weights must be float32 or bfloat16")
+    _on_gpu(q, k, weights)
+    B, S, H, D = q.shape
+    T = k.shape[1]
+    if rope_dim > 0:
+        _check(freqs is not None and freqs.dtype == torch.float32 and freqs.shape[1] * 2 == rope_dim,
+               "freqs must be float32 [rows, rope_dim/2, 2]")
+        _on_gpu(freqs)
+    need = indexer_workspace_size(B, S, H, D, T)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    kk = min(k_top, T)
+    out = torch.empty((B, S, kk), dtype=out_dtype, device=q.device)
+    fr = freqs.shape[0] if freqs is not None else 0
+    _lib.check(_lib.load().ks_indexer(_p(q), _p(k), _p(weights), 1 if weights.dtype == torch.bfloat16 else 0,
+                                      _p(freqs), fr, rope_start, rope_dim, 1 if rope_k else 0, k_top,
+                                      1 if causal else 0, start_pos, ratio, offset, _p(out),
+                                      1 if out_dtype == torch.int64 else 0, B, S, H, D, T, T, _p(workspace),
+                                      workspace.numel(), _stream(q)), "indexer")
+    return out
+
+
+# ---------------------------------------------------------------- sparse attention
+def sparse_attn_workspace_size(B: int, M: int, H: int, Dqk: int, Dv: int, K: int) -> int:
+    return int(_lib.load().ks_sparse_attn_workspace_size(B, M, H, Dqk, Dv, K))
+
+
+def sparse_attn(q: torch.Tensor, kv: torch.Tensor, attn_sink: torch.Tensor, topk_idxs: torch.Tensor,
+                softmax_scale: float, dv: Optional[int] = None,
+                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sparse_attn_megakernel_basic(q, kv, attn_sink, topk_idxs, softmax_scale)
+    (optimized/sparse_attention/op_extension/register.cpp:9-10), plus dv (V = kv[..., :dv]).
+
+    q: bf16 [B, M, H, Dqk]; kv: bf16 [B, N, Dqk]; attn_sink: float32 [H]; topk_idxs: int32 [B, M, K]
+    (negative = invalid).  Returns bf16 [B, M, H, dv]."""
+    _check(q.dtype == torch.bfloat16, "q must be bfloat16")
+    _check(kv.dtype == torch.bfloat16, "kv must be bfloat16")
+    _check(attn_sink.dtype == torch.float32, "attn_sink must be float32")
+    _check(topk_idxs.dtype == torch.int32, "topk_idxs must be int32")
+    _on_gpu(q, kv, attn_sink, topk_idxs)
+    _check(q.dim() == 4 and kv.dim() == 3 and attn_sink.dim() == 1 and topk_idxs.dim() == 3,
+           "q [b,m,h,d], kv [b,n,d], attn_sink [h], topk_idxs [b,m,topk]")
+    B, M, H, D = q.shape
+    N = kv.shape[1]
+    K = topk_idxs.shape[2]
+    _check(kv.shape[0] == B and kv.shape[2] == D, "kv shape mismatch")
+    _check(attn_sink.shape[0] == H, "attn_sink shape mismatch")
+    _check(topk_idxs.shape[0] == B and topk_idxs.shape[1] == M, "topk_idxs shape mismatch")
+    dv = D if dv is None else dv
+    out = torch.empty((B, M, H, dv), dtype=torch.bfloat16, device=q.device)
+    need = sparse_attn_workspace_size(B, M, H, D, dv, K)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    wsz = 0 if workspace is None else workspace.numel()
+    _lib.check(_lib.load().ks_sparse_attn(_p(q), _p(kv), _p(attn_sink), _p(topk_idxs), _p(out), B, M, H, D, dv, N, K,
+                                          float(softmax_scale), _p(workspace) if need else None, wsz, _stream(q)),
+               "sparse_attn")
+    return out
+
+
+def copy_bytes(src: torch.Tensor, dst: torch.Tensor) -> None:
+    """Streaming copy kernel used to calibrate HBM traffic counters."""
+    _on_gpu(src, dst)
+    n = src.numel() * src.element_size()
+    _check(dst.numel() * dst.element_size() >= n, "dst too small")
+    _lib.check(_lib.load().ks_copy_bytes(_p(src), _p(dst), n, _stream(src)), "copy_bytes")

@@ -1,0 +1,199 @@
+"""GPU parity: indexer RoPE, exact scores and fused top-k vs the canonical CPU oracle (bit-exact).
+
+Scores are compared bit for bit (float32 patterns), indices exactly, at the BASELINE.json shapes
+(configs 2 and 4) and on small shapes that stress the exact-rounding path (integer-valued inputs whose
+dots land exactly on bf16 midpoints, heavy-tailed data, wide dynamic range)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kernelswift_amd import ops, workloads
+from kernelswift_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+bits = workloads.bf16_bits
+
+
+def _u16(t):
+    return bits(t)
+
+
+def test_rope_bit_exact_first_and_last_segments(device):
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(2, 33, 4, 128, generator=g).bfloat16()
+    tab = workloads.freqs_table(64, 4096)
+    for rs, pos0 in [(0, 0), (64, 1000), (32, 7)]:
+        print(f"[case] rope rope_start={rs} pos0={pos0}", flush=True)
+        x = q.to(device)
+        ops.rope_inplace(x, tab.to(device), rope_start=rs, pos0=pos0)
+        torch.cuda.synchronize()
+        want = oracle.rope_bf16(_u16(q), tab.numpy(), rs, 64, pos0)
+        np.testing.assert_array_equal(_u16(x), want)
+
+
+def test_row_stats(device):
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(300, 128, generator=g).bfloat16()
+    x[5] = 0
+    x[7, :100] = 0
+    x[9, 3] = 1e-30
+    print("[case] row stats", flush=True)
+    n, s = ops.indexer_row_stats(x.to(device))
+    n, s = n.cpu().numpy(), s.cpu().numpy()
+    xf = oracle.bf16_to_f32(_u16(x)).astype(np.float64)
+    true_n = np.sqrt((xf ** 2).sum(1))
+    assert np.all(n >= true_n) and np.all(n <= true_n * (1 + 2 ** -10) + 1e-38)
+    assert n[5] == 0 and s[5] == 0
+    lsb = np.array([min([oracle_lsb(v) for v in _u16(x)[r] if v & 0x7FFF] or [0]) for r in range(300)])
+    top = np.array([int(np.frexp(v)[1]) if v > 0 else 0 for v in n])
+    np.testing.assert_array_equal(s[n > 0], (top - lsb)[n > 0])
+
+
+def oracle_lsb(b):
+    e = (int(b) >> 7) & 0xFF
+    return -133 if e == 0 else e - 134
+
+
+def _scores_gpu(q, k, w, causal, start_pos, ratio=1, bound_c=None):
+    """Exact-score kernel through the C ABI; returns (scores, [recomputed, unresolved])."""
+    qd, kd, wd = q.to("cuda"), k.to("cuda"), w.to("cuda")
+    (qn, qs), (kn, ks_) = ops.indexer_row_stats(qd), ops.indexer_row_stats(kd)
+    B, S, H, D = q.shape
+    T = k.shape[1]
+    out = torch.empty(B, S, T, dtype=torch.float32, device="cuda")
+    st = torch.zeros(2, dtype=torch.int32, device="cuda")
+    lib = _lib.load()
+    rc = lib.ks_dbg_indexer_scores(qd.data_ptr(), kd.data_ptr(), wd.data_ptr(), 1 if w.dtype == torch.bfloat16 else 0,
+                                   qn.data_ptr(), qs.data_ptr(), kn.data_ptr(), ks_.data_ptr(), out.data_ptr(),
+                                   B, S, H, D, T, T, 1 if causal else 0, start_pos, ratio,
+                                   3.0 if bound_c is None else bound_c, st.data_ptr(),
+                                   torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "ks_dbg_indexer_scores")
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), st.cpu().numpy()
+
+
+def _oracle_scores(q, k, w, causal, start_pos, ratio=1):
+    wn = _u16(w) if w.dtype == torch.bfloat16 else w.numpy()
+    return oracle.indexer_scores(_u16(q), _u16(k), wn, causal, start_pos, ratio)
+
+
+@pytest.mark.parametrize("H", [16, 32, 64])
+@pytest.mark.parametrize("w_bf16", [False, True])
+def test_scores_small_bit_exact(device, H, w_bf16):
+    g = torch.Generator().manual_seed(H + w_bf16)
+    B, S, T = 2, 9, 300
+    q = torch.randn(B, S, H, 128, generator=g).bfloat16()
+    k = torch.randn(B, T, 128, generator=g).bfloat16()
+    w = torch.randn(B, S, H, generator=g) / 8
+    if w_bf16:
+        w = w.bfloat16()
+    print(f"[case] scores small H={H} w_bf16={w_bf16}", flush=True)
+    got, st = _scores_gpu(q, k, w, True, T - S)
+    want = _oracle_scores(q, k, w, True, T - S)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert st[1] == 0
+
+
+def test_scores_midpoint_ties_exact_path(device):
+    # small-integer inputs: every dot is an integer computed exactly by the MFMA; odd values above 256
+    # sit exactly on bf16 midpoints, so ties-to-even must come from the exact recomputation
+    g = torch.Generator().manual_seed(7)
+    q = torch.randint(-3, 4, (1, 8, 64, 128), generator=g).bfloat16()
+    k = torch.randint(-3, 4, (1, 512, 128), generator=g).bfloat16()
+    w = torch.randn(1, 8, 64, generator=g) / 8
+    print("[case] scores integer midpoints", flush=True)
+    got, st = _scores_gpu(q, k, w, False, 0)
+    want = _oracle_scores(q, k, w, False, 0)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert st[0] > 0 and st[1] == 0
+
+
+@pytest.mark.parametrize("dist", ["heavy", "scaled", "tiny"])
+def test_scores_adversarial_distributions(device, dist):
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(1, 16, 64, 128, generator=g)
+    k = torch.randn(1, 1024, 128, generator=g)
+    if dist == "heavy":  # heavy tails (x^3), tiny values flushed so rows stay inside the exact range
+        q, k = q ** 3, k ** 3
+        q = torch.where(q.abs() < 1e-3, torch.zeros_like(q), q)
+        k = torch.where(k.abs() < 1e-3, torch.zeros_like(k), k)
+    elif dist == "scaled":
+        q = q * torch.exp2(torch.randint(-8, 9, (1, 16, 64, 1), generator=g).float())
+        k = k * torch.exp2(torch.randint(-8, 9, (1, 1024, 1), generator=g).float())
+    else:  # values near 0 mixed with O(1): wide dynamic range inside rows
+        q = q * torch.exp2(torch.randint(-30, 1, q.shape, generator=g).float())
+    q, k = q.bfloat16(), k.bfloat16()
+    w = torch.randn(1, 16, 64, generator=g) / 8
+    print(f"[case] scores adversarial {dist}", flush=True)
+    got, st = _scores_gpu(q, k, w, True, 1024 - 16)
+    want = _oracle_scores(q, k, w, True, 1024 - 16)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert st[1] == 0
+
+
+def test_scores_outside_exact_range_is_reported(device):
+    # x^3 of N(0,1) without flushing: row magnitudes span up to ~2^90, beyond the proven exact range
+    # (span_q + span_k <= 84).  The kernel must count every near-tie dot it could not resolve, and no
+    # score may differ from the oracle unless such a dot was reported.
+    g = torch.Generator().manual_seed(11)
+    q = (torch.randn(1, 16, 64, 128, generator=g) ** 3).bfloat16()
+    k = (torch.randn(1, 1024, 128, generator=g) ** 3).bfloat16()
+    w = torch.randn(1, 16, 64, generator=g) / 8
+    print("[case] scores outside exact range", flush=True)
+    got, st = _scores_gpu(q, k, w, True, 1024 - 16)
+    want = _oracle_scores(q, k, w, True, 1024 - 16)
+    mism = int((got.view(np.uint32) != want.view(np.uint32)).sum())
+    print(f"[info] unresolved near-tie dots {int(st[1])}, mismatching scores {mism}", flush=True)
+    assert mism <= int(st[1])
+
+
+@pytest.mark.parametrize("cfg", [2, 4])
+def test_indexer_config_bit_exact(device, cfg):
+    w = workloads.CONFIGS[cfg]("cpu")
+    t, p = w.tensors, w.params
+    print(f"[case] indexer config {cfg}", flush=True)
+    d = {n: v.to(device) for n, v in t.items()}
+    got = ops.indexer(d["q"], d["k"], d["w"], d["freqs"], p["k_top"], p["causal"], p["start_pos"], p["ratio"],
+                      p["offset"], p["rope_start"], p["rope_dim"], p["rope_k"])
+    torch.cuda.synchronize()
+    want = oracle.indexer(_u16(t["q"]), _u16(t["k"]), t["w"].numpy(), t["freqs"].numpy(), p["k_top"], p["causal"],
+                          p["start_pos"], p["ratio"], p["offset"], p["rope_start"], p["rope_dim"], p["rope_k"])
+    g = got.cpu().numpy().astype(np.int64)
+    assert g.shape == want.shape
+    mism = int((g != want).sum())
+    assert mism == 0, f"{mism} mismatching indices"
+
+
+def test_indexer_scores_config2_bit_exact(device):
+    w = workloads.CONFIGS[2]("cpu")
+    t, p = w.tensors, w.params
+    qr = oracle.rope_bf16(_u16(t["q"]), t["freqs"].numpy(), 0, 64, p["start_pos"])
+    kr = oracle.rope_bf16(_u16(t["k"]).reshape(1, 4096, 1, 128), t["freqs"].numpy(), 0, 64, 0).reshape(1, 4096, 128)
+    q = torch.from_numpy(qr.view(np.int16)).view(torch.bfloat16)
+    k = torch.from_numpy(kr.view(np.int16)).view(torch.bfloat16)
+    print("[case] scores config 2", flush=True)
+    got, st = _scores_gpu(q, k, t["w"], True, p["start_pos"])
+    want = oracle.indexer_scores(qr, kr, t["w"].numpy(), True, p["start_pos"])
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    print(f"[info] exact recomputations: {int(st[0])} of {128 * 64 * 4096} dots", flush=True)
+    assert st[1] == 0
+
+
+def test_indexer_baseline_semantics_ratio4_bf16_weights(device):
+    # the reference's own example semantics: start_pos = 0 masking with compress ratio 4, bf16 weights,
+    # RoPE on the trailing dims of q only, int64 output with -1 and offset
+    g = torch.Generator().manual_seed(5)
+    B, S, H, T = 2, 64, 16, 16
+    q = torch.randn(B, S, H, 128, generator=g).bfloat16()
+    k = torch.randn(B, T, 128, generator=g).bfloat16()
+    w = (torch.randn(B, S, H, generator=g) * 0.1).bfloat16()
+    tab = workloads.freqs_table(32, 256)
+    print("[case] indexer baseline semantics", flush=True)
+    got = ops.indexer(q.to(device), k.to(device), w.to(device), tab.to(device), 128, True, 0, 4, 9, 96, 32, False,
+                      out_dtype=torch.int64)
+    torch.cuda.synchronize()
+    want = oracle.indexer(_u16(q), _u16(k), _u16(w), tab.numpy(), 128, True, 0, 4, 9, 96, 32, False)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)

@@ -1,0 +1,97 @@
+"""GPU parity: sparse attention kernel vs the fp64 oracle (atol = rtol = 1e-2, the reference contract
+of benchmarks/ks/auto_bench.py:41-43), at configs 3 and 5, the reference's own example shape, and edge
+cases: invalid (-1 / out-of-range) indices, duplicates, all-invalid rows, nonzero sinks."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from kernelswift_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+bits = workloads.bf16_bits
+TOL = dict(atol=1e-2, rtol=1e-2)
+
+
+def _run(q, kv, sink, idx, scale, dv, tag):
+    print(f"[case] sparse_attn {tag} q={tuple(q.shape)} kv={tuple(kv.shape)} K={idx.shape[-1]} dv={dv}", flush=True)
+    out = ops.sparse_attn(q, kv, sink, idx, scale, dv=dv)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def test_sparse_attn_config3(device):
+    w = workloads.CONFIGS[3]("cpu")
+    t, p = w.tensors, w.params
+    d = {n: v.to(device) for n, v in t.items()}
+    got = _run(d["q"], d["kv"], d["sink"], d["idx"], p["scale"], p["dv"], "config3")
+    want = oracle.sparse_attn(bits(t["q"]), bits(t["kv"]), t["sink"].numpy(), t["idx"].numpy(), p["scale"], p["dv"])
+    np.testing.assert_allclose(got, want, **TOL)
+    print(f"[info] config3 max abs diff {np.max(np.abs(got - want)):.3e}", flush=True)
+
+
+def test_sparse_attn_config5(device):
+    w = workloads.CONFIGS[5](device)
+    t, p = w.tensors, w.params
+    got = _run(t["q"], t["kv"], t["sink"], t["idx"], p["scale"], p["dv"], "config5")
+    # oracle on the gathered rows only (the 2.25 GiB cache never leaves the GPU)
+    B, _, K = t["idx"].shape
+    rows = torch.stack([t["kv"][b, t["idx"][b, 0].long()] for b in range(B)])  # [B, K, 576]
+    local = torch.arange(K, dtype=torch.int32).expand(B, 1, K).contiguous()
+    want = oracle.sparse_attn(bits(t["q"]), bits(rows), t["sink"].cpu().numpy(), local.numpy(), p["scale"], p["dv"])
+    np.testing.assert_allclose(got, want, **TOL)
+    print(f"[info] config5 max abs diff {np.max(np.abs(got - want)):.3e}", flush=True)
+
+
+def test_sparse_attn_reference_example_shape(device):
+    # baseline/sparse_attention.py:101-117: B=8, H=64, N=32, D=128, topk=16 (randint -> duplicates);
+    # M reduced from 2600 to 650 to keep the fp64 oracle fast
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(8, 650, 64, 128, generator=g).bfloat16()
+    kv = torch.randn(8, 32, 128, generator=g).bfloat16()
+    idx = torch.randint(0, 32, (8, 650, 16), generator=g, dtype=torch.int32)
+    sink = torch.zeros(64)
+    got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), 128 ** -0.5, 128, "reference-example")
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), idx.numpy(), 128 ** -0.5, 128)
+    np.testing.assert_allclose(got, want, **TOL)
+
+
+@pytest.mark.parametrize("Dqk,Dv,H", [(128, 128, 16), (128, 128, 64), (576, 512, 128), (576, 512, 32)])
+def test_sparse_attn_edges(device, Dqk, Dv, H):
+    g = torch.Generator().manual_seed(Dqk + H)
+    B, M, N, K = 2, 5, 300, 100
+    q = torch.randn(B, M, H, Dqk, generator=g).bfloat16()
+    kv = torch.randn(B, N, Dqk, generator=g).bfloat16()
+    idx = torch.randint(-20, N + 20, (B, M, K), generator=g, dtype=torch.int32)  # invalid: <0 and >=N
+    idx[0, 0] = -1  # an all-invalid row -> output 0
+    idx[0, 1, :50] = 7  # duplicates count with multiplicity
+    sink = torch.randn(H, generator=g)
+    got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), Dqk ** -0.5, Dv, "edges")
+    ok = (idx >= 0) & (idx < N)
+    idx_o = torch.where(ok, idx, torch.full_like(idx, -1))
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), idx_o.numpy(), Dqk ** -0.5, Dv)
+    np.testing.assert_allclose(got, want, **TOL)
+    assert np.all(got[0, 0] == 0)
+
+
+@pytest.mark.parametrize("K", [1, 31, 33, 2048, 4000])
+def test_sparse_attn_split_counts(device, K):
+    g = torch.Generator().manual_seed(K)
+    B, M, H, N = 1, 3, 16, 5000
+    q = torch.randn(B, M, H, 128, generator=g).bfloat16()
+    kv = torch.randn(B, N, 128, generator=g).bfloat16()
+    idx = torch.randint(0, N, (B, M, K), generator=g, dtype=torch.int32)
+    sink = torch.full((H,), 0.5)
+    got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), 0.3, 128, f"K={K}")
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), idx.numpy(), 0.3, 128)
+    np.testing.assert_allclose(got, want, **TOL)
+
+
+def test_sparse_attn_errors(device):
+    q = torch.zeros(1, 1, 16, 64, dtype=torch.bfloat16, device=device)
+    kv = torch.zeros(1, 8, 64, dtype=torch.bfloat16, device=device)
+    idx = torch.zeros(1, 1, 4, dtype=torch.int32, device=device)
+    with pytest.raises(RuntimeError):
+        ops.sparse_attn(q, kv, torch.zeros(16, device=device), idx, 0.1)  # D=64 unsupported
+    with pytest.raises(RuntimeError):
+        ops.sparse_attn(q.float(), kv, torch.zeros(16, device=device), idx, 0.1)

@@ -1,0 +1,332 @@
+"""Pin the CPU oracle against mathematics that does not share its code.
+
+CPU only (no GPU marker): exact rational arithmetic, brute force on tiny inputs,
+closed forms and invariants.  A plausible oracle mistake (a dropped term, a wrong
+rounding, a transposed operand, a wrong tie order) fails one of these.
+"""
+import itertools
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import torch_ref
+from tests import exact
+
+
+# ------------------------------------------------------------------ exact dot
+def _rand_bf16(rng, n, emin=-20, emax=6, zero_frac=0.0):
+    m = rng.integers(0, 128, n)
+    e = rng.integers(emin, emax, n)
+    s = rng.integers(0, 2, n)
+    bits = ((s << 15) | (((e + 127) & 0xFF) << 7) | m).astype(np.uint16)
+    if zero_frac:
+        bits[rng.random(n) < zero_frac] = 0
+    return bits
+
+
+def _exact_dot_bits(a, b):
+    v = sum((exact.bf16_value(int(x)) * exact.bf16_value(int(y)) for x, y in zip(a, b)), Fraction(0))
+    return exact.to_bf16_bits(exact.round_bf16(v))
+
+
+def test_dot_exact_random_vs_fraction():
+    rng = np.random.default_rng(1)
+    for trial in range(300):
+        n = int(rng.integers(1, 160))
+        a = _rand_bf16(rng, n, zero_frac=0.1)
+        b = _rand_bf16(rng, n, zero_frac=0.1)
+        assert oracle.dot_exact(a, b) == _exact_dot_bits(a, b), trial
+
+
+def test_dot_exact_wide_exponent_spread_big_path():
+    # exponents spread over >96 bits force the multi-limb accumulator
+    rng = np.random.default_rng(2)
+    for trial in range(100):
+        n = int(rng.integers(2, 40))
+        a = _rand_bf16(rng, n, emin=-120, emax=100)
+        b = _rand_bf16(rng, n, emin=-120, emax=20)
+        assert oracle.dot_exact(a, b) == _exact_dot_bits(a, b), trial
+
+
+def test_dot_exact_cancellation_and_ties():
+    f = oracle.f32_to_bf16
+    one = f(np.float32([1.0]))[0]
+    cases = []
+    # 1 + 2^-8: exactly halfway between 1 and 1+2^-7 -> ties to even -> 1
+    cases.append(([1.0, 2.0 ** -8], [1.0, 1.0], 1.0))
+    # 1 + 2^-7 + 2^-8: halfway between 1+2^-7 (odd) and 1+2^-6 (even) -> up
+    cases.append(([1.0, 2.0 ** -7, 2.0 ** -8], [1.0, 1.0, 1.0], 1.0 + 2.0 ** -6))
+    # 1 + 2^-8 + 2^-40: just above the midpoint -> up
+    cases.append(([1.0, 2.0 ** -8, 2.0 ** -20], [1.0, 1.0, 2.0 ** -20], 1.0 + 2.0 ** -7))
+    # catastrophic cancellation: 2^20 - 2^20 + 3*2^-30
+    cases.append(([2.0 ** 20, -(2.0 ** 20), 3.0 * 2 ** -30], [1.0, 1.0, 1.0], 3.0 * 2 ** -30))
+    # exact zero -> +0
+    cases.append(([2.0, -2.0], [3.0, 3.0], 0.0))
+    for av, bv, want in cases:
+        a = f(np.float32(av))
+        b = f(np.float32(bv))
+        got = oracle.bf16_to_f32(np.uint16(oracle.dot_exact(a, b)))
+        assert float(got) == want, (av, bv, float(got), want)
+    assert one == 0x3F80
+    # +0 bits for exact cancellation
+    assert oracle.dot_exact(f(np.float32([2.0, -2.0])), f(np.float32([3.0, 3.0]))) == 0
+
+
+def test_dot_exact_subnormal_results():
+    # products near the bf16 subnormal range: 2^-70 * 2^-62 = 2^-132
+    f = oracle.f32_to_bf16
+    a = f(np.float32([2.0 ** -70, 2.0 ** -70]))
+    b = f(np.float32([2.0 ** -62, 2.0 ** -63]))
+    want = _exact_dot_bits(a, b)
+    assert oracle.dot_exact(a, b) == want
+    assert want & 0x7F80 == 0  # really subnormal
+
+
+def test_dot_matrix_matches_single():
+    rng = np.random.default_rng(3)
+    A = oracle.f32_to_bf16(rng.standard_normal((5, 128)).astype(np.float32))
+    B = oracle.f32_to_bf16(rng.standard_normal((7, 128)).astype(np.float32))
+    M = oracle.dot_matrix(A, B, threads=2)
+    for i in range(5):
+        for j in range(7):
+            assert M[i, j] == _exact_dot_bits(A[i], B[j])
+
+
+# ------------------------------------------------------------------ scores
+def _scores_fraction(q, k, w, causal, start_pos, ratio):
+    """Canonical order recomputed with Fractions and explicit roundings."""
+    B, S, H, D = q.shape
+    T = k.shape[1]
+    out = np.empty((B, S, T), dtype=np.float32)
+    bfw = w.dtype == np.uint16
+    for b in range(B):
+        for s in range(S):
+            lim = (start_pos + s + 1) // ratio
+            for t in range(T):
+                if causal and t >= lim:
+                    out[b, s, t] = -np.inf
+                    continue
+                G = [Fraction(0)] * 4
+                for h in range(H):
+                    d = exact.round_bf16(sum((exact.bf16_value(int(x)) * exact.bf16_value(int(y))
+                                              for x, y in zip(q[b, s, h], k[b, t])), Fraction(0)))
+                    r = d if d > 0 else Fraction(0)
+                    g = (h // 4) % 4
+                    if bfw:
+                        wh = exact.bf16_value(int(w[b, s, h]))
+                        G[g] = exact.round_f32(G[g] + exact.round_bf16(r * wh))
+                    else:
+                        wh = exact.f32_value(float(w[b, s, h]))
+                        G[g] = exact.round_f32(r * wh + G[g])  # one rounding: fma
+                sc = exact.round_f32(exact.round_f32(G[0] + G[1]) + exact.round_f32(G[2] + G[3]))
+                if bfw:
+                    sc = exact.round_bf16(sc)
+                out[b, s, t] = exact.to_f32(sc)
+    return out
+
+
+@pytest.mark.parametrize("w_bf16", [False, True])
+def test_indexer_scores_canonical_order(w_bf16):
+    rng = np.random.default_rng(4)
+    B, S, H, D, T = 1, 3, 16, 8, 6
+    q = oracle.f32_to_bf16(rng.standard_normal((B, S, H, D)).astype(np.float32))
+    k = oracle.f32_to_bf16(rng.standard_normal((B, T, D)).astype(np.float32))
+    wf = (rng.standard_normal((B, S, H)) / 8).astype(np.float32)
+    w = oracle.f32_to_bf16(wf) if w_bf16 else wf
+    got = oracle.indexer_scores(q, k, w, causal=True, start_pos=2, ratio=1)
+    want = _scores_fraction(q, k, w, True, 2, 1)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_indexer_scores_single_head_closed_form():
+    rng = np.random.default_rng(5)
+    q = oracle.f32_to_bf16(rng.standard_normal((1, 4, 1, 32)).astype(np.float32))
+    k = oracle.f32_to_bf16(rng.standard_normal((1, 9, 32)).astype(np.float32))
+    w = (rng.standard_normal((1, 4, 1))).astype(np.float32)
+    got = oracle.indexer_scores(q, k, w, causal=False, start_pos=0)
+    d = oracle.bf16_to_f32(oracle.dot_matrix(q[0, :, 0], k[0]))
+    want = np.maximum(d, np.float32(0)) * w[0, :, 0][:, None]  # one rounding = fma(r, w, +0)
+    np.testing.assert_array_equal(got[0], want.astype(np.float32))
+
+
+def test_indexer_scores_mask_closed_form():
+    rng = np.random.default_rng(6)
+    B, S, H, D, T = 2, 5, 16, 16, 12
+    q = oracle.f32_to_bf16(rng.standard_normal((B, S, H, D)).astype(np.float32))
+    k = oracle.f32_to_bf16(rng.standard_normal((B, T, D)).astype(np.float32))
+    w = rng.standard_normal((B, S, H)).astype(np.float32)
+    for start_pos, ratio in [(0, 1), (7, 1), (0, 4), (40, 4)]:
+        sc = oracle.indexer_scores(q, k, w, True, start_pos, ratio)
+        for s in range(S):
+            lim = (start_pos + s + 1) // ratio
+            assert np.all(np.isneginf(sc[:, s, lim:]))
+            assert np.all(np.isfinite(sc[:, s, :min(lim, T)]))
+    # negative dots vanish under relu: negate k -> only the other half of dots count
+    sc_pos = oracle.indexer_scores(q, k, np.abs(w), False, 0)
+    assert np.all(sc_pos >= 0)
+
+
+# ------------------------------------------------------------------ RoPE
+def test_rope_position_zero_identity_and_unit_vectors():
+    tab = oracle.freqs_table(64, 16)
+    rng = np.random.default_rng(7)
+    x = oracle.f32_to_bf16(rng.standard_normal((1, 1, 3, 128)).astype(np.float32))
+    y = oracle.rope_bf16(x, tab, 0, 64, pos0=0)
+    np.testing.assert_array_equal(x, y)
+    # unit vector (1, 0) at each position p -> (cos, sin) rounded to bf16
+    e = np.zeros((1, 16, 1, 128), dtype=np.float32)
+    e[..., 0:64:2] = 1.0
+    out = oracle.bf16_to_f32(oracle.rope_bf16(oracle.f32_to_bf16(e), tab, 0, 64, pos0=0))
+    np.testing.assert_array_equal(out[0, :, 0, 0:64:2], oracle.bf16_to_f32(oracle.f32_to_bf16(tab[:, :, 0])))
+    np.testing.assert_array_equal(out[0, :, 0, 1:64:2], oracle.bf16_to_f32(oracle.f32_to_bf16(tab[:, :, 1])))
+    # dims outside the rotated segment are untouched
+    np.testing.assert_array_equal(out[..., 64:], 0)
+
+
+def test_rope_matches_complex128_and_inverse():
+    tab = oracle.freqs_table(64, 4096)
+    rng = np.random.default_rng(8)
+    x = oracle.f32_to_bf16(rng.standard_normal((1, 64, 4, 128)).astype(np.float32))
+    y = oracle.rope_bf16(x, tab, 64, 64, pos0=1000)  # rotate the LAST 64 dims, positions 1000..
+    xf = oracle.bf16_to_f32(x).astype(np.float64)
+    z = (xf[..., 64::2] + 1j * xf[..., 65::2]) * (tab[1000:1064, None, :, 0] + 1j * tab[1000:1064, None, :, 1])
+    yf = oracle.bf16_to_f32(y).astype(np.float64)
+    # within one bf16 ulp of the complex128 product
+    tol = np.abs(z) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(yf[..., 64::2] - z.real) <= tol)
+    assert np.all(np.abs(yf[..., 65::2] - z.imag) <= tol)
+    # inverse rotation (conjugate table) composes to ~identity
+    inv = tab.copy()
+    inv[..., 1] = -inv[..., 1]
+    back = oracle.bf16_to_f32(oracle.rope_bf16(y, inv, 64, 64, pos0=1000)).astype(np.float64)
+    assert np.max(np.abs(back - xf)) < 0.05
+
+
+# ------------------------------------------------------------------ TopK
+def _topk_bruteforce(v, k):
+    """Lexicographically greatest k-permutation under key (value, -index) per slot."""
+    best = None
+    for perm in itertools.permutations(range(len(v)), k):
+        key = [(v[i], -i) for i in perm]
+        if best is None or key > best[0]:
+            best = (key, perm)
+    return list(best[1])
+
+
+def test_topk_bruteforce_with_ties_and_neg_inf():
+    rng = np.random.default_rng(9)
+    vals = np.array([-np.inf, -1.0, 0.0, 0.5, 0.5, 2.0], dtype=np.float32)
+    for trial in range(200):
+        n = int(rng.integers(1, 7))
+        k = int(rng.integers(1, n + 1))
+        v = rng.choice(vals, n)
+        got = oracle.topk_stable(v[None, :], k)[0].tolist()
+        assert got == _topk_bruteforce(v.tolist(), k), (v, k, got)
+
+
+def test_topk_all_equal_and_all_masked():
+    v = np.full((2, 10), -np.inf, dtype=np.float32)
+    v[1] = 3.0
+    np.testing.assert_array_equal(oracle.topk_stable(v, 4), [[0, 1, 2, 3], [0, 1, 2, 3]])
+
+
+def test_postprocess_closed_form():
+    idx = np.array([[[0, 1, 2]], [[5, 9, 3]]], dtype=np.int64).reshape(1, 2, 3)
+    # S=2, start_pos=0, ratio=4: limits (0+1)//4=0 and (0+2)//4=0 -> everything -1
+    np.testing.assert_array_equal(oracle.postprocess(idx, True, 0, 4, 100), -np.ones_like(idx))
+    # start_pos=10, ratio=1: limits 11, 12 -> 9,5,3 kept (+100), none invalid
+    np.testing.assert_array_equal(oracle.postprocess(idx, True, 10, 1, 100), idx + 100)
+    # start_pos=3, ratio=1: limits 4 and 5 -> row0 [0,1,2]+100; row1 5->-1, 9->-1, 3->103
+    got = oracle.postprocess(idx, True, 3, 1, 100)
+    np.testing.assert_array_equal(got, [[[100, 101, 102], [-1, -1, 103]]])
+    np.testing.assert_array_equal(oracle.postprocess(idx, False, 3, 1, 7), idx + 7)
+
+
+def test_indexer_end_to_end_vs_torch_cpu_sets():
+    """The canonical oracle and the plain torch-CPU op sequence pick (almost) the same sets."""
+    g = torch.Generator().manual_seed(10)
+    B, S, H, D, T, kt = 1, 8, 16, 128, 256, 32
+    q = torch.randn(B, S, H, D, generator=g).bfloat16()
+    k = torch.randn(B, T, D, generator=g).bfloat16()
+    w = torch.randn(B, S, H, generator=g) / 8
+    tab = oracle.freqs_table(64, 512)
+    cis = torch.view_as_complex(torch.from_numpy(tab).contiguous())
+    sp = T - S
+    a = oracle.indexer(q.view(torch.int16).numpy().view(np.uint16), k.view(torch.int16).numpy().view(np.uint16),
+                       w.numpy(), tab, kt, True, sp, 1, 0)
+    b = torch_ref.indexer(q, k, w, cis, kt, True, sp, 1, 0).numpy()
+    overlap = np.mean([len(set(a[0, s]) & set(b[0, s])) / kt for s in range(S)])
+    assert overlap > 0.97
+
+
+# ------------------------------------------------------------------ Sinkhorn
+def test_sinkhorn_constant_input_closed_form():
+    x = np.zeros((3, 4, 4), dtype=np.float32)
+    y = oracle.sinkhorn(x, repeat=10, eps=1e-6)
+    np.testing.assert_allclose(y, 0.25, atol=1e-5)
+
+
+def test_sinkhorn_invariants_and_equivariance():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((64, 4, 4)).astype(np.float32)
+    y = oracle.sinkhorn(x, 10, 1e-6)
+    assert np.all(y > 0)
+    np.testing.assert_allclose(y.sum(axis=-2), 1.0, atol=1e-5)
+    np.testing.assert_allclose(y.sum(axis=-1), 1.0, atol=2e-3)
+    pr, pc = rng.permutation(4), rng.permutation(4)
+    yp = oracle.sinkhorn(x[:, pr][:, :, pc], 10, 1e-6)
+    np.testing.assert_allclose(yp, y[:, pr][:, :, pc], atol=1e-12)
+    # fp32 torch restatement agrees
+    yt = torch_ref.sinkhorn(torch.from_numpy(x), 10, 1e-6).numpy()
+    np.testing.assert_allclose(yt, y, atol=1e-5, rtol=1e-5)
+
+
+# ------------------------------------------------------------------ sparse attention
+def _bf(a):
+    return oracle.f32_to_bf16(np.asarray(a, dtype=np.float32))
+
+
+def test_sparse_attn_closed_forms():
+    rng = np.random.default_rng(12)
+    B, M, H, D, N, K = 1, 3, 4, 16, 10, 5
+    q = _bf(rng.standard_normal((B, M, H, D)))
+    kv = _bf(rng.standard_normal((B, N, D)))
+    sink = np.zeros(H, dtype=np.float32)
+    # all invalid -> 0
+    idx = -np.ones((B, M, K), dtype=np.int32)
+    np.testing.assert_array_equal(oracle.sparse_attn(q, kv, sink, idx, 0.25), 0.0)
+    # equal scores (q = 0) -> k/(k + e^(sink - 0)) * mean(V)
+    q0 = np.zeros_like(q)
+    idx = rng.integers(0, N, (B, M, K)).astype(np.int32)
+    out = oracle.sparse_attn(q0, kv, sink, idx, 0.25)
+    kvf = oracle.bf16_to_f32(kv).astype(np.float64)
+    for m in range(M):
+        mean = kvf[0, idx[0, m]].mean(axis=0)
+        np.testing.assert_allclose(out[0, m], np.broadcast_to(K / (K + 1.0) * mean, (H, D)), rtol=1e-12, atol=1e-12)
+    # single valid index with sink -> -inf: exactly that row
+    idx = -np.ones((B, M, K), dtype=np.int32)
+    idx[0, :, 2] = [4, 7, 1]
+    out = oracle.sparse_attn(q, kv, np.full(H, -np.inf, dtype=np.float32), idx, 0.25)
+    for m, r in enumerate([4, 7, 1]):
+        np.testing.assert_allclose(out[0, m], np.broadcast_to(kvf[0, r], (H, D)), rtol=0, atol=0)
+    # duplicates count with multiplicity: [r, r, s] == weights 2:1 at equal scores
+    idx = np.array([[[3, 3, 6]]], dtype=np.int32)
+    out = oracle.sparse_attn(np.zeros((1, 1, H, D), np.uint16), kv, sink, idx, 1.0)
+    want = (2 * kvf[0, 3] + kvf[0, 6]) / 4.0
+    np.testing.assert_allclose(out[0, 0], np.broadcast_to(want, (H, D)), rtol=1e-12)
+
+
+def test_sparse_attn_matches_torch_cpu():
+    g = torch.Generator().manual_seed(13)
+    B, M, H, D, N, K = 2, 4, 8, 64, 40, 12
+    q = torch.randn(B, M, H, D, generator=g).bfloat16()
+    kv = torch.randn(B, N, D, generator=g).bfloat16()
+    idx = torch.randint(-3, N, (B, M, K), generator=g, dtype=torch.int32)
+    sink = torch.randn(H, generator=g)
+    a = oracle.sparse_attn(q.view(torch.int16).numpy().view(np.uint16), kv.view(torch.int16).numpy().view(np.uint16),
+                           sink.numpy(), idx.numpy(), D ** -0.5, dv=48)
+    b = torch_ref.sparse_attn(q, kv, sink, idx, D ** -0.5, dv=48).float().numpy()
+    np.testing.assert_allclose(b, a, atol=1e-2, rtol=1e-2)

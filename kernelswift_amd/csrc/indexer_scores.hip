@@ -7,20 +7,24 @@
 // exact real dot product rounded once to bf16; heads are summed in four groups g = (h/4) % 4, each in
 // increasing h with fma (fp32 weights), then (G0 + G1) + (G2 + G3).
 //
-// Work decomposition: a 256-lane workgroup = 4 waves = 4 queries x one block of 256 keys.  The key block
-// (64 KiB bf16) is staged once in LDS with a 16-byte XOR swizzle (chunk c of key r at c ^ (r & 15)), so the
-// 16 lanes that read the same d-chunk of 16 different keys hit 16 distinct bank groups.  Each wave keeps its
-// query's q rows (H heads x 128 d) as MFMA A-fragments in VGPRs and walks the block in 16-key tiles with
-// v_mfma_f32_16x16x32_bf16 (M = 16 heads, N = 16 keys, 4 k-steps).  In the 16x16 output layout lane l holds
-// heads 16m + 4(l/16) + r (r = 0..3) of key l % 16, i.e. exactly the canonical head group g = l/16, so the
-// head sum runs in-lane and two xor-shuffles (16, 32) finish ((G0+G1)+(G2+G3)).
+// Work decomposition: a 512-lane workgroup = 8 waves = 8 queries x a block of 256 keys.  The key block is
+// staged once in LDS (64 KiB, zero rows past T) behind the kernel's only barrier; from there each wave runs
+// independently.  A wave keeps its query's rows in VGPRs as MFMA A-fragments and walks the block in
+// 16-key tiles with v_mfma_f32_16x16x32_bf16 (M = 16 heads, N = 16 keys, 4 k-steps), issuing the next
+// tile's MFMAs before the current tile's epilogue.  LDS rows use a 16-byte XOR swizzle (chunk c of row r
+// at c ^ (r & 15)), so 16 lanes reading one chunk of 16 rows hit 16 distinct bank groups.  In the MFMA
+// output layout lane l holds heads 16m + 4(l/16) + r (r = 0..3) of key l % 16, i.e. exactly the canonical
+// head group g = l/16, so the head sum runs in-lane and two permlane swaps finish ((G0+G1)+(G2+G3)).
 //
 // Exactness: the MFMA fp32 sum A differs from the exact dot by less than
-//   delta = C * 2^-23 * ||q_h|| * ||k_t||       (C = kScoreBoundC, measured error model),
-// so RNE_bf16(A) is the exact answer unless a bf16 rounding boundary lies within delta of A.  Such "risky"
-// dots (and every dot whose bf16 ulp is not >> delta) are recomputed exactly: 16 lanes form the 128 exact
-// products in double precision and reduce them; the per-row spans from the statistics pass prove that every
-// partial sum is representable (span_q + span_k <= 52), or a hi/lo split keeps both halves exact (<= 84).
+//   delta = C * 2^-23 * ||q_h|| * max_t ||k_t||   (C = kScoreBoundC, a measured error model),
+// so the relu'd bf16 value is exact when RNE(A - delta) and RNE(A + delta) agree after the ReLU (one packed
+// convert and one packed max per pair of dots and interval end).  Keys with a disagreeing ("near-tie") dot
+// are deferred: both interval ends of all their head groups go to a per-wave LDS list, and when the list
+// fills (and at the end) the near-tie dots are recomputed exactly, 16 at a time with 4 lanes per dot, and
+// the affected scores rewritten.  Per-row spans from the statistics pass prove every partial sum of the
+// exact dot representable in a double (span_q + span_k <= 52); up to 84 a hi/lo split keeps both halves
+// exact; beyond that the dot keeps the lower interval end and is counted as unresolved.
 #include "common.h"
 #include "indexer_common.h"
 
@@ -28,11 +32,33 @@ namespace ks {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kKB = 256;  // keys per workgroup block
-constexpr int kWaves = 4; // queries per workgroup (one per wave)
 constexpr int kD = 128;
+constexpr int kQW = 8;        // queries (= waves) per workgroup
+constexpr int kThreads = kQW * 64;
+constexpr int kKR = 256;      // keys per workgroup
+constexpr int kEntCap = 36;   // deferred key entries per wave (flushed above kEntCap - 16)
+constexpr int kDotCap = 512;  // near-tie dots listed at a time per wave
+
+// Context of one key whose score depends on a near-tie dot: for the four head groups, the relu'd bf16
+// values of the two interval ends (packed pairs; they differ exactly at the near-tie slots).
+struct alignas(16) KeyEntry {
+  uint32_t pl[4][8];
+  uint32_t ph[4][8];
+  int32_t key;
+  int32_t pad[3];
+};
+
+struct ScoresLds {
+  uint4 k[kKR * 16];                 // swizzled key block of this workgroup (64 KiB)
+  KeyEntry ent[kQW][kEntCap];
+  uint16_t dots[kQW][kDotCap];       // flattened near-tie dots: (pair << 4) | slot, pair = 4 entry + group
+  float red[kQW];
+};
 
 __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
@@ -41,19 +67,45 @@ __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
 
 __device__ __forceinline__ float round_bf16_f(float a) { return bf16_to_f32(f32_to_bf16_rne(a)); }
 
-// RNE to bf16 of the exact value a + b (two doubles).  TwoSum gives s + t == a + b exactly with
-// s = fl(a + b); the bf16 grid is far coarser than the double grid, so RNE(a + b) = RNE(s) except when s
-// is exactly a bf16 midpoint, where the sign of t decides (t == 0: ties to even).
-__device__ uint16_t round2_to_bf16(double a, double b) {
-  const double s = a + b;
-  const double bb = s - a;
-  const double t = (a - (s - bb)) + (b - bb);
+// Packed RNE conversion of two fp32 values and ReLU on the bf16 bit patterns (negative bf16 values are
+// negative int16, so a signed max with 0 clears them to +0).
+__device__ __forceinline__ uint32_t cvt_relu_pk(float lo, float hi) {
+  const bf16x2_t v = __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t);  // one v_cvt_pk_bf16_f32
+  const short2_t s = __builtin_elementwise_max(__builtin_bit_cast(short2_t, v), short2_t{0, 0});
+  return __builtin_bit_cast(uint32_t, s);
+}
+
+__device__ __forceinline__ float unpack_hi(uint32_t p) { return __builtin_bit_cast(float, p & 0xFFFF0000u); }
+__device__ __forceinline__ float unpack_lo(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
+
+__device__ __forceinline__ int frexp_exp(float x) {
+  int e = 0;
+  frexpf(x, &e);
+  return e;
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u), CTRL, 0xF, 0xF, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Sum over the 4 lanes of a quad (quad_perm xor 1, xor 2); exact whenever every partial sum is.
+__device__ __forceinline__ double quad_sum_f64(double v) {
+  v += dpp_f64<0xB1>(v);
+  return v + dpp_f64<0x4E>(v);
+}
+
+// RNE to bf16 of a double value s, with the sign of a residual t (s + t is the exact value, |t| below the
+// double spacing at s) deciding exact bf16 midpoints; t == 0 ties to even.
+__device__ uint16_t round_dir_to_bf16(double s, int tdir) {
   if (s == 0.0) return 0;
   const uint64_t bits = __builtin_bit_cast(uint64_t, s);
   const uint16_t sign = (bits >> 63) ? 0x8000 : 0;
   const uint64_t mag = bits & 0x7FFFFFFFFFFFFFFFull;
   const int e = static_cast<int>(mag >> 52) - 1023;
-  const int tdir = (t == 0.0) ? 0 : (((t > 0.0) == (s > 0.0)) ? 1 : -1);  // residual, in magnitude
   if (e >= -126) {
     uint64_t kept = mag >> 45;
     const uint64_t rem = mag & ((1ull << 45) - 1);
@@ -72,178 +124,345 @@ __device__ uint16_t round2_to_bf16(double a, double b) {
   return sign | static_cast<uint16_t>(ni + (up ? 1u : 0u));  // 128 -> smallest normal, bits 0x0080
 }
 
-// Exact dot of one q row (global) and one key row (LDS, swizzled) by the 16 lanes of a group; lane j
-// forms the products of elements 8j..8j+7.  Returns RNE_bf16(exact) as fp32 in every lane of the group.
-__device__ float exact_dot16(const uint16_t *__restrict__ qrow, const uint4 *kl, int key_local, int j, int span_sum,
-                             int top_sum, bool &ok) {
-  const uint4 qa = *reinterpret_cast<const uint4 *>(qrow + 8 * j);
-  const uint4 kb = kl[key_local * 16 + (j ^ (key_local & 15))];
-  const uint32_t qw[4] = {qa.x, qa.y, qa.z, qa.w};
-  const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w};
-  const bool split = span_sum > 52;
-  const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
-  double hi = 0.0, lo = 0.0;
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const double a = bf16_to_f32(static_cast<uint16_t>(hh ? (qw[p] >> 16) : (qw[p] & 0xFFFFu)));
-      const double b = bf16_to_f32(static_cast<uint16_t>(hh ? (kw[p] >> 16) : (kw[p] & 0xFFFFu)));
-      const double prod = a * b;  // exact: 16 significant bits
-      if (!split || fabs(prod) >= thr) hi += prod; else lo += prod;
-    }
-  }
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    hi += __shfl_xor(hi, m, 64);
-    lo += __shfl_xor(lo, m, 64);
-  }
-  ok = span_sum <= 84;
-  return bf16_to_f32(round2_to_bf16(hi, lo));
+// RNE to bf16 of the exact value a + b (two doubles): TwoSum gives s + t == a + b exactly.
+__device__ uint16_t round2_to_bf16(double a, double b) {
+  const double s = a + b;
+  const double bb = s - a;
+  const double t = (a - (s - bb)) + (b - bb);
+  return round_dir_to_bf16(s, (t == 0.0) ? 0 : (((t > 0.0) == (s > 0.0)) ? 1 : -1));
 }
 
-template <int HT, bool WBF>
-__global__ __launch_bounds__(256, 2) void indexer_scores_kernel(
-    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
-    const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
-    const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
-    int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats) {
-  constexpr int H = HT * 16;
-  __shared__ uint4 kl[kKB * 16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t b = blockIdx.z;
-  const int kb0 = blockIdx.x * kKB;
-  const int64_t s = static_cast<int64_t>(blockIdx.y) * kWaves + wave;
-  const int nk = min(kKB, T - kb0);
-  const int64_t krow0 = b * kbs + kb0;  // first key row of this block (also the stats row)
+// ((G0 + G1) + (G2 + G3)) over the four 16-lane rows of the wave (row g holds head group g), returned in
+// every lane.  v_permlane16_swap exchanges row 1 of its first operand with row 0 of its second (and rows
+// 3 / 2), so with G in both operands every lane ends up holding its row pair's two values; the sum of the
+// two registers is G0 + G1 in rows 0-1 and G2 + G3 in rows 2-3.  v_permlane32_swap does the same across
+// the wave halves.  Written as inline assembly (the builtin form was miscompiled into v + v when both
+// operands carry the same value); the NOPs cover the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ float combine_groups(float G) {
+  float a = G, b = G;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  float c = a + b, d = c;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+  return c + d;
+}
 
-  // ---- stage the key block in LDS (zero rows past T)
-  const uint16_t *kbase = k + krow0 * kD;
-#pragma unroll 4
-  for (int it = 0; it < kKB * 16 / 256; ++it) {
-    const int lin = it * 256 + tid;
-    const int kr = lin >> 4, ch = lin & 15;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (kr < nk) v = *reinterpret_cast<const uint4 *>(kbase + static_cast<int64_t>(kr) * kD + ch * 8);
-    kl[kr * 16 + (ch ^ (kr & 15))] = v;
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
   }
-  __syncthreads();
-  if (s >= S) return;  // no barrier follows
+  return v;
+}
 
-  const int64_t limit = causal ? (start_pos + s + 1) / ratio : INT64_MAX;
-  const int l16 = lane & 15, g = lane >> 4;
-  const int64_t qrow0 = (b * S + s) * H;
+// Near-tie slot bits (16 per head group) of an entry: positions where the two interval ends differ.
+template <int HT>
+__device__ __forceinline__ uint32_t entry_mask(const KeyEntry &en, int gg) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int p = 0; p < 2 * HT; ++p) {
+    const uint32_t x = en.pl[gg][p] ^ en.ph[gg][p];
+    m |= ((x & 0xFFFFu) ? 1u : 0u) << (2 * p);
+    m |= ((x >> 16) ? 1u : 0u) << (2 * p + 1);
+  }
+  return m;
+}
 
-  uint4 qa[HT][4];
-#pragma unroll
-  for (int m = 0; m < HT; ++m)
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      qa[m][kk] = *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * kD + 32 * kk + 8 * g);
-  float wv[HT][4], dq[HT][4];
-#pragma unroll
-  for (int m = 0; m < HT; ++m)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t hrow = qrow0 + 16 * m + 4 * g + r;
-      wv[m][r] = WBF ? bf16_to_f32(static_cast<const uint16_t *>(w)[hrow]) : static_cast<const float *>(w)[hrow];
-      dq[m][r] = bound_c * 0x1p-23f * qn[hrow];
-    }
-  float *orow = scores + (b * S + s) * T;
-
-  for (int n = 0; n < kKB / 16; ++n) {
-    if (16 * n >= nk) break;
-    const int key_local = 16 * n + l16;
-    const int key = kb0 + key_local;
-    const bool kvalid = key < T;
-    if (kb0 + 16 * n >= limit) {  // whole tile masked (wave-uniform)
-      if (g == 0 && kvalid) orow[key] = -INFINITY;
-      continue;
-    }
-    f32x4_t acc[HT];
-#pragma unroll
-    for (int m = 0; m < HT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const uint4 bv = kl[key_local * 16 + ((4 * kk + g) ^ l16)];
-#pragma unroll
-      for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv, acc[m]);
-    }
-    const float knv = kvalid ? kn[krow0 + key_local] : 0.f;
-
-    float dv[HT * 4];
-    uint32_t risky = 0;
-#pragma unroll
-    for (int m = 0; m < HT; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float A = acc[m][r];
-        const float dl = dq[m][r] * knv;
-        const float mid = __builtin_bit_cast(float, (__builtin_bit_cast(uint32_t, A) & 0xFFFF0000u) | 0x8000u);
-        const bool rk = (A > -dl) && (fabsf(A - mid) < dl || fabsf(A) < 1024.f * dl);
-        risky |= rk ? (1u << (4 * m + r)) : 0u;
-        dv[4 * m + r] = round_bf16_f(A);
+// Exact recomputation of the deferred near-tie dots of one wave, then of the affected scores.
+template <int HT, bool WBF>
+__device__ void flush_entries(ScoresLds &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
+                              const float *__restrict__ qn, const int32_t *__restrict__ qsp,
+                              const float *__restrict__ kn, const int32_t *__restrict__ ksp, int64_t qrow0,
+                              int64_t kbrow0, float *orow, int64_t limit, int T, int kb0, const float (&wv)[HT][4],
+                              uint32_t &n_exact, uint32_t &n_unres) {
+  KeyEntry *E = L.ent[wave];
+  uint16_t *D = L.dots[wave];
+  const int g = lane >> 4, l16 = lane & 15;
+  // 1. near-tie masks of the (entry, group) pairs, pair = 4 * entry + group; taken before any patching
+  const int npairs = 4 * nent;
+  const uint32_t m0 = lane < npairs ? entry_mask<HT>(E[lane >> 2], lane & 3) : 0u;
+  const uint32_t m1 = lane + 64 < npairs ? entry_mask<HT>(E[(lane + 64) >> 2], lane & 3) : 0u;
+  const uint32_t c0 = __builtin_popcount(m0), c1 = __builtin_popcount(m1);
+  const uint32_t i0 = wave_incl_scan(c0);
+  const uint32_t t0 = __shfl(i0, 63, 64);
+  const uint32_t i1 = wave_incl_scan(c1);
+  const int ndots = static_cast<int>(t0 + __shfl(i1, 63, 64));
+  n_exact += static_cast<uint32_t>(ndots);
+  // 2. the dot list, kDotCap at a time: exact dots, 16 per pass, 4 lanes per dot (lane quarter `sub` owns
+  //    elements 32 sub .. 32 sub + 31); the exact relu'd value replaces the pl value of its slot
+  for (int base = 0; base < ndots; base += kDotCap) {
+    {
+      uint32_t mm = m0;
+      int pos = static_cast<int>(i0 - c0) - base;
+      while (mm) {
+        const int bit = __builtin_ctz(mm);
+        mm &= mm - 1;
+        if (pos >= 0 && pos < kDotCap) D[pos] = static_cast<uint16_t>((lane << 4) | bit);
+        ++pos;
       }
-
-    if (__ballot(risky != 0) != 0ull) {
+      mm = m1;
+      pos = static_cast<int>(t0 + i1 - c1) - base;
+      while (mm) {
+        const int bit = __builtin_ctz(mm);
+        mm &= mm - 1;
+        if (pos >= 0 && pos < kDotCap) D[pos] = static_cast<uint16_t>(((lane + 64) << 4) | bit);
+        ++pos;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int nd = min(kDotCap, ndots - base);
+    const int dq = lane >> 2, sub = lane & 3;
+    for (int b0 = 0; b0 < nd; b0 += 16) {
+      const int di = min(b0 + dq, nd - 1);  // idle quads repeat the last dot (result identical)
+      const uint32_t de = D[di];
+      const int pr = static_cast<int>(de >> 4), slot = static_cast<int>(de & 15);
+      const int e = pr >> 2, gg = pr & 3;
+      const int h = 16 * (slot >> 2) + 4 * gg + (slot & 3);
+      const int64_t hrow = qrow0 + h;
+      const int key = min(E[e].key, T - 1);  // entries only hold keys < T; clamp defensively
+      const int64_t krow = kbrow0 + key;
+      const int kl = key - kb0;               // row of the key in the LDS block
+      const uint4 *qp = reinterpret_cast<const uint4 *>(q + hrow * kD + 32 * sub);
+      uint4 qa[4], ka[4];
 #pragma unroll
-      for (int i = 0; i < HT * 4; ++i) {
-        uint64_t lm = __ballot((risky >> i) & 1u);
-        while (lm != 0ull) {
-          // up to four risky lanes per pass, one per 16-lane group
-          uint64_t tmp = lm, batch = 0;
-          int sel[4];
+      for (int c = 0; c < 4; ++c) {
+        qa[c] = qp[c];
+        ka[c] = L.k[kl * 16 + ((4 * sub + c) ^ (kl & 15))];
+      }
+      const int span_sum = qsp[hrow] + ksp[krow];
+      uint16_t r;
+      if (__builtin_amdgcn_ballot_w64(span_sum > 52) == 0ull) {
+        // every partial sum is a multiple of the smallest product LSB and below 2^53 of it: exact doubles
+        // in any order
+        double a0 = 0.0, a1 = 0.0;
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            sel[q4] = tmp ? __builtin_ctzll(tmp) : -1;
-            if (tmp) {
-              batch |= 1ull << sel[q4];
-              tmp &= tmp - 1;
-            }
+        for (int c = 0; c < 4; ++c) {
+          const uint32_t qw[4] = {qa[c].x, qa[c].y, qa[c].z, qa[c].w};
+          const uint32_t kw[4] = {ka[c].x, ka[c].y, ka[c].z, ka[c].w};
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            a0 = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), a0);
+            a1 = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), a1);
           }
-          lm = tmp;
-          int L = g == 0 ? sel[0] : g == 1 ? sel[1] : g == 2 ? sel[2] : sel[3];
-          if (L < 0) L = sel[0];  // idle groups repeat group 0's dot (result discarded)
-          const int Lg = L >> 4, Ll = L & 15;
-          const int m = i / 4, r = i % 4;
-          const int64_t hrow = qrow0 + 16 * m + 4 * Lg + r;
-          const int kls = 16 * n + Ll;
-          int topq = 0, topk = 0;
-          frexpf(qn[hrow], &topq);
-          frexpf(kn[krow0 + kls], &topk);
-          bool ok = true;
-          const float ex = exact_dot16(q + hrow * kD, kl, kls, l16, qsp[hrow] + ksp[krow0 + kls], topq + topk, ok);
-          const int rank = __builtin_popcountll(batch & ((1ull << lane) - 1ull));
-          const float got = __shfl(ex, 16 * (rank < 4 ? rank : 3), 64);
-          const bool okg = __shfl(ok ? 1 : 0, 16 * (rank < 4 ? rank : 3), 64) != 0;
-          if ((batch >> lane) & 1ull) {
-            if (okg) dv[i] = got;
-          }
-          if (stats != nullptr && lane == 0) {
-            atomicAdd(&stats[0], static_cast<uint32_t>(__builtin_popcountll(batch)));
-          }
-          if (stats != nullptr && ((batch >> lane) & 1ull) && !okg) atomicAdd(&stats[1], 1u);
+        }
+        r = round_dir_to_bf16(quad_sum_f64(a0 + a1), 0);
+      } else {
+        // wide dynamic range: products above / below 2^(top - 38) accumulate separately, each exactly
+        const int top_sum = frexp_exp(qn[hrow]) + frexp_exp(kn[krow]);
+        const bool split = span_sum > 52;
+        const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
+        double hi = 0.0, lo = 0.0;
+        // rare path, kept register-light: one dword of q and k per step, re-read from memory
+        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qp);
+#pragma unroll 1
+        for (int j = 0; j < 16; ++j) {
+          const uint32_t qw = q32[j];
+          const uint32_t kw =
+              reinterpret_cast<const uint32_t *>(&L.k[kl * 16 + ((4 * sub + (j >> 2)) ^ (kl & 15))])[j & 3];
+          const double p0 = static_cast<double>(unpack_lo(qw)) * static_cast<double>(unpack_lo(kw));
+          const double p1 = static_cast<double>(unpack_hi(qw)) * static_cast<double>(unpack_hi(kw));
+          if (!split || fabs(p0) >= thr) hi += p0; else lo += p0;
+          if (!split || fabs(p1) >= thr) hi += p1; else lo += p1;
+        }
+        r = round2_to_bf16(quad_sum_f64(hi), quad_sum_f64(lo));
+      }
+      const uint32_t rv = (r & 0x8000) ? 0u : r;  // ReLU (also maps -0 to +0)
+      if (sub == 0 && b0 + dq < nd) {
+        if (span_sum <= 84) {
+          uint16_t *half = reinterpret_cast<uint16_t *>(&E[e].pl[gg][slot >> 1]) + (slot & 1);
+          *half = static_cast<uint16_t>(rv);
+        } else {
+          ++n_unres;
         }
       }
     }
-
-    // ---- canonical head sum for this lane's group, then ((G0+G1)+(G2+G3))
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  // 3. scores of the deferred keys from the corrected values: lane (row g, column e) sums group g of entry
+  //    e with this lane's own head weights, the rows combine as in the main loop
+  for (int eb = 0; eb < nent; eb += 16) {
+    const int e = min(eb + l16, nent - 1);
     float G = 0.f;
 #pragma unroll
     for (int m = 0; m < HT; ++m)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float rv = fmaxf(dv[4 * m + r], 0.f);
+        const uint32_t p2 = E[e].pl[g][2 * m + (r >> 1)];
+        const float rv = (r & 1) ? unpack_hi(p2) : unpack_lo(p2);
         if constexpr (WBF) {
           G = G + round_bf16_f(rv * wv[m][r]);
         } else {
           G = __builtin_fmaf(rv, wv[m][r], G);
         }
       }
-    const float s01 = G + __shfl_xor(G, 16, 64);
-    float tot = s01 + __shfl_xor(s01, 32, 64);
-    if constexpr (WBF) tot = round_bf16_f(tot);
-    if (g == 0 && kvalid) orow[key] = (key < limit) ? tot : -INFINITY;
+    const float tot = combine_groups(G);
+    const int key = E[e].key;
+    if (g == 0 && eb + l16 < nent && key < T) orow[key] = (key < limit) ? (WBF ? round_bf16_f(tot) : tot) : -INFINITY;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int HT, bool WBF>
+__global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
+    const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
+    const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
+    int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats) {
+  constexpr int H = HT * 16;
+  __shared__ ScoresLds L;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t b = blockIdx.z;
+  const int kb0 = blockIdx.x * kKR;
+  const int nk = min(kKR, T - kb0);
+  const int64_t s = static_cast<int64_t>(blockIdx.y) * kQW + wave;
+  const bool s_ok = s < S;
+  const int64_t kbrow0 = b * kbs;        // first key row of batch b
+  const int64_t krow0 = kbrow0 + kb0;    // first key row of this workgroup
+
+  // max key norm over this workgroup's range (the error bound uses it for every key)
+  float knm = 0.f;
+  for (int i = tid; i < nk; i += kThreads) knm = fmaxf(knm, kn[krow0 + i]);
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
+  if (lane == 0) L.red[wave] = knm;
+  // query rows as MFMA A-fragments
+  const int64_t qrow0 = (b * S + (s_ok ? s : 0)) * H;
+  uint4 qa[HT][4];
+#pragma unroll
+  for (int m = 0; m < HT; ++m)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      qa[m][kk] = s_ok ? *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * kD + 32 * kk + 8 * g)
+                       : make_uint4(0, 0, 0, 0);
+  // the workgroup's whole key block into LDS (zero rows past T)
+#pragma unroll 4
+  for (int it = 0; it < kKR * 16 / kThreads; ++it) {
+    const int lin = it * kThreads + tid;
+    const int kr = lin >> 4, ch = lin & 15;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (kr < nk) v = *reinterpret_cast<const uint4 *>(k + (krow0 + kr) * kD + ch * 8);
+    L.k[kr * 16 + (ch ^ (kr & 15))] = v;
+  }
+  __syncthreads();  // the only barrier: from here on every wave runs independently
+  knm = L.red[0];
+#pragma unroll
+  for (int i = 1; i < kQW; ++i) knm = fmaxf(knm, L.red[i]);
+  if (!s_ok) return;
+  float wv[HT][4], dl[HT][4];
+#pragma unroll
+  for (int m = 0; m < HT; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t hr = qrow0 + 16 * m + 4 * g + r;
+      wv[m][r] = WBF ? bf16_to_f32(static_cast<const uint16_t *>(w)[hr]) : static_cast<const float *>(w)[hr];
+      dl[m][r] = bound_c * 0x1p-23f * qn[hr] * knm;
+    }
+
+  const int64_t limit = causal ? (start_pos + s + 1) / ratio : INT64_MAX;
+  float *orow = scores + (b * S + s) * T;
+  uint32_t n_exact = 0, n_unres = 0;
+  int nent = 0;
+  // tiles of 16 keys; tiles at or past the causal limit are masked without MFMA work
+  const int ntiles = (nk + 15) / 16;
+  const int64_t lim_rel = limit - kb0;
+  const int nlive = lim_rel <= 0 ? 0 : (lim_rel >= 16 * ntiles ? ntiles : static_cast<int>((lim_rel + 15) / 16));
+
+  auto tile_mfma = [&](int t, f32x4_t(&acc)[HT]) {
+    const int key_l = 16 * t + l16;
+#pragma unroll
+    for (int m = 0; m < HT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint4 bv = L.k[key_l * 16 + ((4 * kk + g) ^ l16)];
+#pragma unroll
+      for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv, acc[m]);
+    }
+  };
+
+  auto tile_epilogue = [&](int t, const f32x4_t(&acc)[HT]) {
+    const int key_l = 16 * t + l16;
+    const int key = kb0 + key_l;
+    const bool kvalid = key_l < nk;
+    // interval test: RNE(A - delta) == RNE(A + delta) (after ReLU) <=> the exact dot rounds to the same
+    // relu'd bf16 value; pl holds that value for the head sum
+    uint32_t pl[2 * HT], ph[2 * HT];
+    uint64_t anyr = 0;
+#pragma unroll
+    for (int m = 0; m < HT; ++m)
+#pragma unroll
+      for (int rp = 0; rp < 2; ++rp) {
+        const float A0 = acc[m][2 * rp], A1 = acc[m][2 * rp + 1];
+        const float d0 = dl[m][2 * rp], d1 = dl[m][2 * rp + 1];
+        pl[2 * m + rp] = cvt_relu_pk(A0 - d0, A1 - d1);
+        ph[2 * m + rp] = cvt_relu_pk(A0 + d0, A1 + d1);
+        anyr |= __builtin_amdgcn_ballot_w64(pl[2 * m + rp] != ph[2 * m + rp]);
+      }
+    // canonical head sum of this lane's group, then ((G0+G1)+(G2+G3)) across the rows
+    float G = 0.f;
+#pragma unroll
+    for (int m = 0; m < HT; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t p2 = pl[2 * m + (r >> 1)];
+        const float rv = (r & 1) ? unpack_hi(p2) : unpack_lo(p2);
+        if constexpr (WBF) {
+          G = G + round_bf16_f(rv * wv[m][r]);
+        } else {
+          G = __builtin_fmaf(rv, wv[m][r], G);
+        }
+      }
+    const float tot = combine_groups(G);
+    const float outv = WBF ? round_bf16_f(tot) : tot;
+    if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
+    anyr &= __builtin_amdgcn_ballot_w64(kvalid);  // keys past T are zero rows, never deferred
+    if (anyr != 0ull) {
+      // defer the keys holding a near-tie dot: save all four groups' interval ends
+      const uint32_t km = static_cast<uint32_t>((anyr | (anyr >> 16) | (anyr >> 32) | (anyr >> 48)) & 0xFFFFull);
+      if ((km >> l16) & 1u) {
+        const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
+        KeyEntry &en = L.ent[wave][e];
+#pragma unroll
+        for (int p = 0; p < 2 * HT; ++p) {
+          en.pl[g][p] = pl[p];
+          en.ph[g][p] = ph[p];
+        }
+        if (g == 0) en.key = key;
+      }
+      nent += __builtin_popcount(km);
+    }
+  };
+
+  // software pipeline: the MFMAs of the next tile are in flight during the current tile's epilogue; the
+  // deferred entries are flushed at one place (when a further tile could overflow them, and at the end)
+  f32x4_t acc[HT], nxt[HT];
+  if (nlive > 0) tile_mfma(0, acc);
+  for (int t = 0; t < nlive; ++t) {
+    if (t + 1 < nlive) tile_mfma(t + 1, nxt);
+    tile_epilogue(t, acc);
+    if (nent > kEntCap - 16 || (t == nlive - 1 && nent > 0)) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      flush_entries<HT, WBF>(L, wave, lane, nent, q, qn, qsp, kn, ksp, qrow0, kbrow0, orow, limit, T, kb0, wv,
+                             n_exact, n_unres);
+      nent = 0;
+    }
+#pragma unroll
+    for (int m = 0; m < HT; ++m) acc[m] = nxt[m];
+  }
+  // masked tiles (at or past the causal limit)
+  for (int t = nlive; t < ntiles; ++t) {
+    const int key_l = 16 * t + l16;
+    if (g == 0 && key_l < nk) orow[kb0 + key_l] = -INFINITY;
+  }
+  if (stats != nullptr) {
+    if (lane == 0 && n_exact) atomicAdd(&stats[0], n_exact);
+    if (n_unres) atomicAdd(&stats[1], n_unres);
   }
 }
 
@@ -252,14 +471,14 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
                      const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                      int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c, uint32_t *stats,
                      hipStream_t stream) {
-  dim3 grid(static_cast<unsigned>(ceil_div(T, kKB)), static_cast<unsigned>(ceil_div(S, kWaves)),
+  dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
   if (w_bf16) {
-    hipLaunchKernelGGL((indexer_scores_kernel<HT, true>), grid, dim3(256), 0, stream, q, k, w, qn, qsp, kn, ksp,
+    hipLaunchKernelGGL((indexer_scores_kernel<HT, true>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn, ksp,
                        scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats);
   } else {
-    hipLaunchKernelGGL((indexer_scores_kernel<HT, false>), grid, dim3(256), 0, stream, q, k, w, qn, qsp, kn, ksp,
-                       scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats);
+    hipLaunchKernelGGL((indexer_scores_kernel<HT, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn,
+                       ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;
@@ -295,6 +514,7 @@ int check_scores_args(const uint16_t *q, const uint16_t *k, const void *w, const
   KS_CHECK_ARG(D == 128, "ks_indexer_scores: D=%lld, the kernel is built for head_dim 128", (long long)D);
   KS_CHECK_ARG(H == 16 || H == 32 || H == 64, "ks_indexer_scores: H=%lld must be 16, 32 or 64", (long long)H);
   KS_CHECK_ARG(B >= 0 && S >= 0, "ks_indexer_scores: negative B or S");
+  KS_CHECK_ARG(B < 65536 && S < (int64_t(1) << 24), "ks_indexer_scores: B or S too large");
   KS_CHECK_ARG(T >= 1 && T < (int64_t(1) << 31), "ks_indexer_scores: T=%lld out of range", (long long)T);
   KS_CHECK_ARG(kbs >= T, "ks_indexer_scores: k_batch_stride=%lld < T=%lld", (long long)kbs, (long long)T);
   KS_CHECK_ARG(ratio >= 1 && start_pos >= 0, "ks_indexer_scores: ratio must be >= 1 and start_pos >= 0");

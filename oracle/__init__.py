@@ -9,7 +9,7 @@ reference computes in floating point with a tolerance contract) or, for the
 bit-exact indexer path, in the canonical arithmetic order implemented by the C
 library ks_oracle.c.  Citations are to /root/reference files.
 
-Pinning (what checks each function beyond restating it; see tests/test_oracle_*.py):
+Pinning (what checks each function beyond restating it; see tests/test_oracle.py):
   sinkhorn        closed forms (constant input -> 1/4), doubly-stochastic invariant,
                   permutation equivariance, fp64-vs-fp32 restatements agree.
   rope_bf16       identity at position 0, unit vectors -> (cos, sin), inverse

@@ -101,8 +101,8 @@ int ks_rope_inplace(uint16_t *x, const float *freqs, int64_t B, int64_t S,
  * q_norm/q_span: [B*S*H] and k_norm/k_span: [B*k_batch_stride] row statistics
  * from ks_indexer_row_stats over the same q and k buffers (they bound the MFMA
  * error and prove the exact recomputation of near-tie dots exact).
- * scores: f32 [B, S, T].  D must be 128 (the only head dim the kernel is built
- * for); H in {16, 32, 64}; T >= 1.
+ * scores: f32 [B, S, T].  D must be 64 or 128 (the head dims the kernel is
+ * built for); H in {16, 32, 64}; T >= 1.
  * Exactness holds for rows whose nonzero magnitudes span less than ~2^40 each
  * (span_q + span_k <= 84, see ks_indexer_row_stats); beyond that a near-tie dot
  * keeps its MFMA rounding.
@@ -115,7 +115,7 @@ int ks_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w,
                       int32_t ratio, void *stream);
 
 /* ------------------------------------------------------------------------
- * Per-row statistics of bf16 rows of length D = 128 for ks_indexer_scores:
+ * Per-row statistics of bf16 rows of length D (64 or 128) for ks_indexer_scores:
  *   norm[r] >= ||x_r||_2 (an upper bound within 2^-11 relative),
  *   span[r]  = ceil(log2 norm[r]) - (exponent of the least significant bit of
  *              the smallest nonzero element), 0 for an all-zero row.
@@ -134,7 +134,9 @@ int ks_indexer_row_stats(const uint16_t *x, int64_t rows, int64_t D, float *norm
  * ks_rope_inplace; inputs are not modified (rotated copies live in the
  * workspace).  out: [B*S, min(k_top, T)] int32 or int64 (out_i64), as
  * ks_indexer_topk.  workspace: ks_indexer_workspace_size(B, S, H, D, T) bytes,
- * 256-byte aligned.
+ * 256-byte aligned.  Shapes as ks_indexer_scores: q bf16 [B, S, H, D] with
+ * D in {64, 128} and H in {16, 32, 64}; batch b's T key rows start at
+ * k + b*k_batch_stride*D; w [B, S, H]; T <= 65536.
  * ---------------------------------------------------------------------- */
 size_t ks_indexer_workspace_size(int64_t B, int64_t S, int64_t H, int64_t D,
                                  int64_t T);

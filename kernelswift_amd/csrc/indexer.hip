@@ -55,7 +55,8 @@ extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, i
                           int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D, int64_t T,
                           int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream) {
   ks::last_error().clear();
-  KS_CHECK_ARG(D == 128, "ks_indexer: D=%lld, the kernels are built for head_dim 128", (long long)D);
+  KS_CHECK_ARG(D == 128 || D == 64, "ks_indexer: D=%lld, the kernels are built for head_dim 64 and 128",
+               (long long)D);
   KS_CHECK_ARG(H == 16 || H == 32 || H == 64, "ks_indexer: H=%lld must be 16, 32 or 64", (long long)H);
   KS_CHECK_ARG(B >= 0 && S >= 0, "ks_indexer: negative B or S");
   KS_CHECK_ARG(T >= 1 && T <= 65536, "ks_indexer: T=%lld must be in [1, 65536]", (long long)T);
@@ -83,18 +84,18 @@ extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, i
   const int rs = static_cast<int>(rope_start), rd = static_cast<int>(rope_dim);
 
   // q: rotate at positions start_pos + s into the workspace copy, with row statistics
-  int rc = ks::launch_rope_rows(q, ws.q_rot, freqs, B * S * H, 128, static_cast<int>(H), S, start_pos, rs, rd,
+  int rc = ks::launch_rope_rows(q, ws.q_rot, freqs, B * S * H, static_cast<int>(D), static_cast<int>(H), S, start_pos, rs, rd,
                                 ws.q_norm, ws.q_span, st);
   if (rc != KS_OK) return rc;
   // k: rotate at positions t (or copy) per batch, with row statistics
   const int rdk = rope_k ? rd : 0;
   for (int64_t b = 0; b < B; ++b) {
-    rc = ks::launch_rope_rows(k + b * k_batch_stride * D, ws.k_rot + b * T * D, freqs, T, 128, 1, T, 0, rs, rdk,
+    rc = ks::launch_rope_rows(k + b * k_batch_stride * D, ws.k_rot + b * T * D, freqs, T, static_cast<int>(D), 1, T, 0, rs, rdk,
                               ws.k_norm + b * T, ws.k_span + b * T, st);
     if (rc != KS_OK) return rc;
     if (k_batch_stride == T) {  // contiguous batches: the first launch may cover all of them
       if (b == 0 && B > 1) {
-        rc = ks::launch_rope_rows(k + T * D, ws.k_rot + T * D, freqs, (B - 1) * T, 128, 1, T, 0, rs, rdk,
+        rc = ks::launch_rope_rows(k + T * D, ws.k_rot + T * D, freqs, (B - 1) * T, static_cast<int>(D), 1, T, 0, rs, rdk,
                                   ws.k_norm + T, ws.k_span + T, st);
         if (rc != KS_OK) return rc;
       }
@@ -102,7 +103,7 @@ extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, i
     }
   }
   rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, w_bf16 ? 1 : 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span,
-                                 ws.scores, B, S, H, T, T, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC,
+                                 ws.scores, B, S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC,
                                  nullptr, st);
   if (rc != KS_OK) return rc;
   return ks_indexer_topk(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, stream);

@@ -21,7 +21,7 @@ int launch_rope_rows(const uint16_t *src, uint16_t *dst, const float *freqs, int
 
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
-                          int64_t S, int64_t H, int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio,
-                          float bound_c, uint32_t *stats, hipStream_t stream);
+                          int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
+                          int ratio, float bound_c, uint32_t *stats, hipStream_t stream);
 
 }  // namespace ks

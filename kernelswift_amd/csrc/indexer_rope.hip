@@ -7,7 +7,7 @@
 // with -ffp-contract=off, so the products are rounded separately, exactly like the CPU oracle).
 //
 // Each lane owns 8 consecutive elements (one 16-byte load and store), so a row of D = 128 is 16 lanes and
-// a wave covers 4 rows with fully coalesced accesses.  In stats mode the 16 lanes of a row also reduce
+// a wave covers 4 rows with fully coalesced accesses.  In stats mode the D/8 lanes of a row also reduce
 // the row's squared norm and its smallest nonzero-element LSB exponent:
 //   norm  >= ||row||_2 (rounded up),   span = ceil(log2 norm) - min_lsb_exponent.
 // The score kernel uses norm for its MFMA error bound and span to prove that a double-precision
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t *__restri
   }
   if (live && dst != nullptr) *reinterpret_cast<uint4 *>(dst + row * D + 8 * j) = v;
   if constexpr (STATS) {
-    // D == 128: the 16 lanes of a row are an aligned 16-lane group of the wave.
+    // D in {64, 128}: the D/8 lanes of a row are an aligned group of the wave.
     float ss = 0.f;
     int lsb = 1 << 20;
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -67,13 +67,12 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t *__restri
         if ((b & 0x7FFFu) != 0) lsb = min(lsb, bf16_lsb_exponent(b));
       }
     }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
+    for (int m = 1; m < chunks_per_row; m <<= 1) {
       ss += __shfl_xor(ss, m, 64);
       lsb = min(lsb, __shfl_xor(lsb, m, 64));
     }
     if (live && j == 0) {
-      // fp32 sum of 128 squares: relative error < 2^-16; sqrt adds < 1 ulp; pad by 2^-12.
+      // fp32 sum of <= 128 squares: relative error < 2^-16; sqrt adds < 1 ulp; pad by 2^-12.
       const float nrm = ss > 0.f ? sqrtf(ss) * (1.0f + 0x1p-12f) : 0.f;
       norm[row] = nrm;
       int top = 0;
@@ -127,11 +126,11 @@ extern "C" int ks_rope_inplace(uint16_t *x, const float *freqs, int64_t B, int64
 extern "C" int ks_indexer_row_stats(const uint16_t *x, int64_t rows, int64_t D, float *norm, int32_t *span,
                                     void *stream) {
   ks::last_error().clear();
-  KS_CHECK_ARG(D == 128, "ks_indexer_row_stats: D=%lld, only 128 is supported", (long long)D);
+  KS_CHECK_ARG(D == 128 || D == 64, "ks_indexer_row_stats: D=%lld, supported: 64 and 128", (long long)D);
   KS_CHECK_ARG(rows >= 0, "ks_indexer_row_stats: rows < 0");
   if (rows == 0) return KS_OK;
   KS_CHECK_ARG(x && norm && span, "ks_indexer_row_stats: null pointer");
   KS_CHECK_ARG(ks::aligned(x, 16), "ks_indexer_row_stats: x must be 16-byte aligned");
-  return ks::launch_rope_rows(x, nullptr, nullptr, rows, 128, 1, 1, 0, 0, 0, norm, span,
+  return ks::launch_rope_rows(x, nullptr, nullptr, rows, static_cast<int>(D), 1, 1, 0, 0, 0, norm, span,
                               static_cast<hipStream_t>(stream));
 }

@@ -37,7 +37,6 @@ typedef short short2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kD = 128;
 constexpr int kQW = 8;        // queries (= waves) per workgroup
 constexpr int kThreads = kQW * 64;
 constexpr int kKR = 256;      // keys per workgroup
@@ -53,8 +52,9 @@ struct alignas(16) KeyEntry {
   int32_t pad[3];
 };
 
+template <int KD>
 struct ScoresLds {
-  uint4 k[kKR * 16];                 // swizzled key block of this workgroup (64 KiB)
+  uint4 k[kKR * KD / 8];             // swizzled key block of this workgroup (KD / 8 16-byte chunks per key)
   KeyEntry ent[kQW][kEntCap];
   uint16_t dots[kQW][kDotCap];       // flattened near-tie dots: (pair << 4) | slot, pair = 4 entry + group
   float red[kQW];
@@ -171,8 +171,8 @@ __device__ __forceinline__ uint32_t entry_mask(const KeyEntry &en, int gg) {
 }
 
 // Exact recomputation of the deferred near-tie dots of one wave, then of the affected scores.
-template <int HT, bool WBF>
-__device__ void flush_entries(ScoresLds &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
+template <int HT, int KD, bool WBF>
+__device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
                               const float *__restrict__ qn, const int32_t *__restrict__ qsp,
                               const float *__restrict__ kn, const int32_t *__restrict__ ksp, int64_t qrow0,
                               int64_t kbrow0, float *orow, int64_t limit, int T, int kb0, const float (&wv)[HT][4],
@@ -191,7 +191,8 @@ __device__ void flush_entries(ScoresLds &L, int wave, int lane, int nent, const 
   const int ndots = static_cast<int>(t0 + __shfl(i1, 63, 64));
   n_exact += static_cast<uint32_t>(ndots);
   // 2. the dot list, kDotCap at a time: exact dots, 16 per pass, 4 lanes per dot (lane quarter `sub` owns
-  //    elements 32 sub .. 32 sub + 31); the exact relu'd value replaces the pl value of its slot
+  //    elements KD/4 sub .. KD/4 (sub + 1) - 1); the exact relu'd value replaces the pl value of its slot
+  constexpr int kC = KD / 8, kLC = KD / 32;  // 16-byte chunks per key row; chunks per lane
   for (int base = 0; base < ndots; base += kDotCap) {
     {
       uint32_t mm = m0;
@@ -225,12 +226,12 @@ __device__ void flush_entries(ScoresLds &L, int wave, int lane, int nent, const 
       const int key = min(E[e].key, T - 1);  // entries only hold keys < T; clamp defensively
       const int64_t krow = kbrow0 + key;
       const int kl = key - kb0;               // row of the key in the LDS block
-      const uint4 *qp = reinterpret_cast<const uint4 *>(q + hrow * kD + 32 * sub);
-      uint4 qa[4], ka[4];
+      const uint4 *qp = reinterpret_cast<const uint4 *>(q + hrow * KD + (KD / 4) * sub);
+      uint4 qa[kLC], ka[kLC];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < kLC; ++c) {
         qa[c] = qp[c];
-        ka[c] = L.k[kl * 16 + ((4 * sub + c) ^ (kl & 15))];
+        ka[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
       }
       const int span_sum = qsp[hrow] + ksp[krow];
       uint16_t r;
@@ -239,7 +240,7 @@ __device__ void flush_entries(ScoresLds &L, int wave, int lane, int nent, const 
         // in any order
         double a0 = 0.0, a1 = 0.0;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < kLC; ++c) {
           const uint32_t qw[4] = {qa[c].x, qa[c].y, qa[c].z, qa[c].w};
           const uint32_t kw[4] = {ka[c].x, ka[c].y, ka[c].z, ka[c].w};
 #pragma unroll
@@ -258,10 +259,10 @@ __device__ void flush_entries(ScoresLds &L, int wave, int lane, int nent, const 
         // rare path, kept register-light: one dword of q and k per step, re-read from memory
         const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qp);
 #pragma unroll 1
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < 4 * kLC; ++j) {
           const uint32_t qw = q32[j];
           const uint32_t kw =
-              reinterpret_cast<const uint32_t *>(&L.k[kl * 16 + ((4 * sub + (j >> 2)) ^ (kl & 15))])[j & 3];
+              reinterpret_cast<const uint32_t *>(&L.k[kl * kC + ((kLC * sub + (j >> 2)) ^ (kl & (kC - 1)))])[j & 3];
           const double p0 = static_cast<double>(unpack_lo(qw)) * static_cast<double>(unpack_lo(kw));
           const double p1 = static_cast<double>(unpack_hi(qw)) * static_cast<double>(unpack_hi(kw));
           if (!split || fabs(p0) >= thr) hi += p0; else lo += p0;
@@ -307,14 +308,15 @@ __device__ void flush_entries(ScoresLds &L, int wave, int lane, int nent, const 
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int HT, bool WBF>
+template <int HT, int KD, bool WBF>
 __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
     const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
     int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats) {
   constexpr int H = HT * 16;
-  __shared__ ScoresLds L;
+  constexpr int kC = KD / 8;  // 16-byte chunks per key row
+  __shared__ ScoresLds<KD> L;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int64_t b = blockIdx.z;
@@ -333,21 +335,21 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   if (lane == 0) L.red[wave] = knm;
   // query rows as MFMA A-fragments
   const int64_t qrow0 = (b * S + (s_ok ? s : 0)) * H;
-  uint4 qa[HT][4];
+  uint4 qa[HT][KD / 32];
 #pragma unroll
   for (int m = 0; m < HT; ++m)
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      qa[m][kk] = s_ok ? *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * kD + 32 * kk + 8 * g)
+    for (int kk = 0; kk < KD / 32; ++kk)
+      qa[m][kk] = s_ok ? *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g)
                        : make_uint4(0, 0, 0, 0);
   // the workgroup's whole key block into LDS (zero rows past T)
 #pragma unroll 4
-  for (int it = 0; it < kKR * 16 / kThreads; ++it) {
+  for (int it = 0; it < kKR * kC / kThreads; ++it) {
     const int lin = it * kThreads + tid;
-    const int kr = lin >> 4, ch = lin & 15;
+    const int kr = lin / kC, ch = lin % kC;
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (kr < nk) v = *reinterpret_cast<const uint4 *>(k + (krow0 + kr) * kD + ch * 8);
-    L.k[kr * 16 + (ch ^ (kr & 15))] = v;
+    if (kr < nk) v = *reinterpret_cast<const uint4 *>(k + (krow0 + kr) * KD + ch * 8);
+    L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = v;
   }
   __syncthreads();  // the only barrier: from here on every wave runs independently
   knm = L.red[0];
@@ -378,8 +380,8 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
 #pragma unroll
     for (int m = 0; m < HT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const uint4 bv = L.k[key_l * 16 + ((4 * kk + g) ^ l16)];
+    for (int kk = 0; kk < KD / 32; ++kk) {
+      const uint4 bv = L.k[key_l * kC + ((4 * kk + g) ^ (key_l & (kC - 1)))];
 #pragma unroll
       for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv, acc[m]);
     }
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     if (nent > kEntCap - 16 || (t == nlive - 1 && nent > 0)) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      flush_entries<HT, WBF>(L, wave, lane, nent, q, qn, qsp, kn, ksp, qrow0, kbrow0, orow, limit, T, kb0, wv,
+      flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qn, qsp, kn, ksp, qrow0, kbrow0, orow, limit, T, kb0, wv,
                              n_exact, n_unres);
       nent = 0;
     }
@@ -466,7 +468,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   }
 }
 
-template <int HT>
+template <int HT, int KD>
 int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                      const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                      int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c, uint32_t *stats,
@@ -474,35 +476,49 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
   dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
   if (w_bf16) {
-    hipLaunchKernelGGL((indexer_scores_kernel<HT, true>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn, ksp,
+    hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn, ksp,
                        scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats);
   } else {
-    hipLaunchKernelGGL((indexer_scores_kernel<HT, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn,
+    hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn,
                        ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;
 }
 
+template <int KD>
+int launch_scores_d(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
+                    const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
+                    int64_t H, int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c,
+                    uint32_t *stats, hipStream_t stream) {
+  switch (H) {
+    case 16:
+      return launch_scores_ht<1, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
+                                     ratio, bound_c, stats, stream);
+    case 32:
+      return launch_scores_ht<2, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
+                                     ratio, bound_c, stats, stream);
+    case 64:
+      return launch_scores_ht<4, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
+                                     ratio, bound_c, stats, stream);
+    default:
+      return fail(KS_ERR_INVALID, "indexer scores: H=%lld, supported: 16, 32, 64", (long long)H);
+  }
+}
+
 }  // namespace
 
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
-                          int64_t S, int64_t H, int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio,
-                          float bound_c, uint32_t *stats, hipStream_t stream) {
-  switch (H) {
-    case 16:
-      return launch_scores_ht<1>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos, ratio,
-                                 bound_c, stats, stream);
-    case 32:
-      return launch_scores_ht<2>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos, ratio,
-                                 bound_c, stats, stream);
-    case 64:
-      return launch_scores_ht<4>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos, ratio,
-                                 bound_c, stats, stream);
-    default:
-      return fail(KS_ERR_INVALID, "indexer scores: H=%lld, supported: 16, 32, 64", (long long)H);
-  }
+                          int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
+                          int ratio, float bound_c, uint32_t *stats, hipStream_t stream) {
+  if (D == 128)
+    return launch_scores_d<128>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
+                                bound_c, stats, stream);
+  if (D == 64)
+    return launch_scores_d<64>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
+                               bound_c, stats, stream);
+  return fail(KS_ERR_INVALID, "indexer scores: D=%lld, supported: 64, 128", (long long)D);
 }
 
 }  // namespace ks
@@ -511,7 +527,8 @@ namespace {
 int check_scores_args(const uint16_t *q, const uint16_t *k, const void *w, const float *qn, const int32_t *qsp,
                       const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S, int64_t H, int64_t D,
                       int64_t T, int64_t kbs, int32_t ratio, int64_t start_pos) {
-  KS_CHECK_ARG(D == 128, "ks_indexer_scores: D=%lld, the kernel is built for head_dim 128", (long long)D);
+  KS_CHECK_ARG(D == 128 || D == 64, "ks_indexer_scores: D=%lld, the kernel is built for head_dim 64 and 128",
+               (long long)D);
   KS_CHECK_ARG(H == 16 || H == 32 || H == 64, "ks_indexer_scores: H=%lld must be 16, 32 or 64", (long long)H);
   KS_CHECK_ARG(B >= 0 && S >= 0, "ks_indexer_scores: negative B or S");
   KS_CHECK_ARG(B < 65536 && S < (int64_t(1) << 24), "ks_indexer_scores: B or S too large");
@@ -535,8 +552,8 @@ extern "C" int ks_indexer_scores(const uint16_t *q, const uint16_t *k, const voi
                              start_pos);
   if (rc != KS_OK) return rc;
   if (B * S == 0) return KS_OK;
-  return ks::launch_indexer_scores(q, k, w, w_bf16 ? 1 : 0, q_norm, q_span, k_norm, k_span, scores, B, S, H, T,
-                                   k_batch_stride, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC, nullptr,
+  return ks::launch_indexer_scores(q, k, w, w_bf16 ? 1 : 0, q_norm, q_span, k_norm, k_span, scores, B, S, H, D,
+                                   T, k_batch_stride, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC, nullptr,
                                    static_cast<hipStream_t>(stream));
 }
 
@@ -552,7 +569,7 @@ extern "C" int ks_dbg_indexer_scores(const uint16_t *q, const uint16_t *k, const
                              start_pos);
   if (rc != KS_OK) return rc;
   if (B * S == 0) return KS_OK;
-  return ks::launch_indexer_scores(q, k, w, w_bf16 ? 1 : 0, q_norm, q_span, k_norm, k_span, scores, B, S, H, T,
-                                   k_batch_stride, causal ? 1 : 0, start_pos, ratio, bound_c, stats,
+  return ks::launch_indexer_scores(q, k, w, w_bf16 ? 1 : 0, q_norm, q_span, k_norm, k_span, scores, B, S, H, D,
+                                   T, k_batch_stride, causal ? 1 : 0, start_pos, ratio, bound_c, stats,
                                    static_cast<hipStream_t>(stream));
 }

@@ -81,13 +81,15 @@ def rope_inplace(x: torch.Tensor, freqs: torch.Tensor, rope_start: Optional[int]
 
 
 def indexer_row_stats(x: torch.Tensor):
-    """Row statistics (norm upper bound, span) of bf16 rows of length 128 for indexer_scores."""
-    _check(x.dtype == torch.bfloat16 and x.shape[-1] == 128, "x must be bfloat16 [..., 128]")
+    """Row statistics (norm upper bound, span) of bf16 rows of length 64 or 128 for indexer_scores."""
+    _check(x.dtype == torch.bfloat16 and x.shape[-1] in (64, 128), "x must be bfloat16 [..., 64 or 128]")
+    _check(x.is_contiguous(), "x must be contiguous")
     _on_gpu(x)
-    rows = x.numel() // 128
+    D = x.shape[-1]
+    rows = x.numel() // D
     norm = torch.empty(rows, dtype=torch.float32, device=x.device)
     span = torch.empty(rows, dtype=torch.int32, device=x.device)
-    _lib.check(_lib.load().ks_indexer_row_stats(_p(x), rows, 128, _p(norm), _p(span), _stream(x)), "indexer_row_stats")
+    _lib.check(_lib.load().ks_indexer_row_stats(_p(x), rows, D, _p(norm), _p(span), _stream(x)), "indexer_row_stats")
     return norm, span
 
 
@@ -95,7 +97,8 @@ def indexer_scores(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, caus
                    ratio: int = 1, T: Optional[int] = None, stats=None) -> torch.Tensor:
     """fused_qk_reduce(q, kvT, weights, causal, ratio) (indexer_torch.cpp:100), generalised.
 
-    q: bf16 [B, S, H, 128] (already rotated); k: bf16 [B, Tk, 128] (untransposed, first T rows used);
+    q: bf16 [B, S, H, D] (already rotated, D = 64 or 128); k: bf16 [B, Tk, D] contiguous (untransposed,
+    first T rows used);
     weights: float32 or bf16 [B, S, H].  Returns float32 scores [B, S, T] with -inf where masked.
     stats: optional ((q_norm, q_span), (k_norm, k_span)) from indexer_row_stats."""
     _check(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16, "q and k must be bfloat16")
@@ -105,6 +108,7 @@ def indexer_scores(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, caus
     B, S, H, D = q.shape
     _check(k.shape[0] == B and k.shape[2] == D, "k shape mismatch")
     _check(tuple(weights.shape) == (B, S, H), "weights shape mismatch")
+    _check(q.is_contiguous() and k.is_contiguous() and weights.is_contiguous(), "q, k, weights must be contiguous")
     Tk = k.shape[1]
     T = Tk if T is None else T
     if stats is None:
@@ -143,17 +147,26 @@ def indexer_workspace_size(B: int, S: int, H: int, D: int, T: int) -> int:
 def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Optional[torch.Tensor], k_top: int,
             causal: bool, start_pos: int, ratio: int = 1, offset: int = 0, rope_start: int = 0, rope_dim: int = 64,
             rope_k: bool = True, out_dtype: torch.dtype = torch.int32,
-            workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+            workspace: Optional[torch.Tensor] = None, T: Optional[int] = None) -> torch.Tensor:
     """Fused RoPE -> exact scores -> exact top-k (the reference wrapper's three-op sequence,
     optimized/indexer_project/indexer.py:197-222).  Inputs are not modified.
 
-    q: bf16 [B, S, H, 128]; k: bf16 [B, T, 128]; weights float32/bf16 [B, S, H];
-    freqs: float32 [rows, rope_dim/2, 2].  Returns [B, S, min(k_top, T)] int32 (default) or int64."""
+    q: bf16 [B, S, H, D] (D = 64 or 128); k: bf16 [B, Tk, D] whose rows are contiguous (a batch-strided view
+    such as kv_cache[:B] is accepted without a copy), the first T (default Tk) rows are the keys;
+    weights float32/bf16 [B, S, H]; freqs: float32 [rows, rope_dim/2, 2].
+    Returns [B, S, min(k_top, T)] int32 (default) or int64."""
     _check(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16, "q and k must be bfloat16")
     _check(weights.dtype in (torch.float32, torch.bfloat16), "weights must be float32 or bfloat16")
     _on_gpu(q, k, weights)
+    _check(q.dim() == 4 and k.dim() == 3 and weights.dim() == 3, "q [b,s,h,d], k [b,t,d], weights [b,s,h]")
     B, S, H, D = q.shape
-    T = k.shape[1]
+    _check(k.shape[0] >= B and k.shape[2] == D, "k shape mismatch")
+    _check(tuple(weights.shape) == (B, S, H), "weights shape mismatch")
+    _check(q.is_contiguous() and weights.is_contiguous(), "q and weights must be contiguous")
+    _check(k.stride(2) == 1 and k.stride(1) == D and k.stride(0) % D == 0, "k rows must be contiguous")
+    T = k.shape[1] if T is None else T
+    _check(1 <= T <= k.shape[1], "T out of range")
+    kbs = k.stride(0) // D if B > 1 else max(k.shape[1], T)
     if rope_dim > 0:
         _check(freqs is not None and freqs.dtype == torch.float32 and freqs.shape[1] * 2 == rope_dim,
                "freqs must be float32 [rows, rope_dim/2, 2]")
@@ -167,7 +180,7 @@ def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Opti
     _lib.check(_lib.load().ks_indexer(_p(q), _p(k), _p(weights), 1 if weights.dtype == torch.bfloat16 else 0,
                                       _p(freqs), fr, rope_start, rope_dim, 1 if rope_k else 0, k_top,
                                       1 if causal else 0, start_pos, ratio, offset, _p(out),
-                                      1 if out_dtype == torch.int64 else 0, B, S, H, D, T, T, _p(workspace),
+                                      1 if out_dtype == torch.int64 else 0, B, S, H, D, T, kbs, _p(workspace),
                                       workspace.numel(), _stream(q)), "indexer")
     return out
 

@@ -80,29 +80,31 @@ def _oracle_scores(q, k, w, causal, start_pos, ratio=1):
     return oracle.indexer_scores(_u16(q), _u16(k), wn, causal, start_pos, ratio)
 
 
+@pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("H", [16, 32, 64])
 @pytest.mark.parametrize("w_bf16", [False, True])
-def test_scores_small_bit_exact(device, H, w_bf16):
-    g = torch.Generator().manual_seed(H + w_bf16)
+def test_scores_small_bit_exact(device, H, w_bf16, D):
+    g = torch.Generator().manual_seed(H + w_bf16 + D)
     B, S, T = 2, 9, 300
-    q = torch.randn(B, S, H, 128, generator=g).bfloat16()
-    k = torch.randn(B, T, 128, generator=g).bfloat16()
+    q = torch.randn(B, S, H, D, generator=g).bfloat16()
+    k = torch.randn(B, T, D, generator=g).bfloat16()
     w = torch.randn(B, S, H, generator=g) / 8
     if w_bf16:
         w = w.bfloat16()
-    print(f"[case] scores small H={H} w_bf16={w_bf16}", flush=True)
+    print(f"[case] scores small H={H} D={D} w_bf16={w_bf16}", flush=True)
     got, st = _scores_gpu(q, k, w, True, T - S)
     want = _oracle_scores(q, k, w, True, T - S)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
     assert st[1] == 0
 
 
-def test_scores_midpoint_ties_exact_path(device):
+@pytest.mark.parametrize("D", [128, 64])
+def test_scores_midpoint_ties_exact_path(device, D):
     # small-integer inputs: every dot is an integer computed exactly by the MFMA; odd values above 256
     # sit exactly on bf16 midpoints, so ties-to-even must come from the exact recomputation
     g = torch.Generator().manual_seed(7)
-    q = torch.randint(-3, 4, (1, 8, 64, 128), generator=g).bfloat16()
-    k = torch.randint(-3, 4, (1, 512, 128), generator=g).bfloat16()
+    q = torch.randint(-3, 4, (1, 8, 64, D), generator=g).bfloat16()
+    k = torch.randint(-3, 4, (1, 512, D), generator=g).bfloat16()
     w = torch.randn(1, 8, 64, generator=g) / 8
     print("[case] scores integer midpoints", flush=True)
     got, st = _scores_gpu(q, k, w, False, 0)

@@ -4,187 +4,364 @@
 // dense-N megakernel (optimized/sparse_attention/op_kernel/fused_sparse_attn_basic_kernel.asc:535-648,
 // transpose_kv_kernel.asc:35-63), which only handled N = 32 keys, with a real gather.
 //
-// Decomposition: the K indices of query (b, m) are split into NS ranges; workgroup (range, m, b) has one
-// wave per 16 heads and walks its range in chunks of 32 keys:
-//   gather   the chunk's kv rows (16-byte loads, invalid indices -> zero rows) into LDS twice: row-major
-//            K (rows padded by 16 bytes so 16 lanes reading 16 keys hit distinct banks) and a key-interleaved
-//            V copy [key/8][d][key%8] whose 8-key runs are MFMA B-operand columns;
-//   QK^T     S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (M = 16 keys, N = 16 heads), the wave's q rows held
-//            as B-fragments in VGPRs; lane (head = l%16, g = l/16) receives keys 4g..4g+3 of each 16-key tile;
-//   softmax  online (running max / sum per head, base-2 exponentials), invalid keys -> 0;
-//   PV       O = P V with M = 16 heads, N = 16 dv columns, K = 32 keys: a lane's 8 probabilities
-//            {4g..4g+3, 16+4g..16+4g+3} are its A-fragment as-is, and V is read with the same key
-//            permutation (two 8-byte LDS reads), so P never goes through LDS.
-// NS == 1 finalises in place (sink added, bf16 store); otherwise partial (O, max, sum) go to the
-// workspace and a combine kernel merges ranges with the sink (log-sum-exp).
+// Work item = (query (b, m), key range).  A group of GW waves (16 heads each) owns one item; a workgroup
+// holds GROUPS groups (as many as 8 waves and the LDS budget allow).  The group walks its key range in
+// chunks of 32 keys.  Each chunk's kv rows are gathered straight into LDS with global_load_lds_dwordx4
+// (no VGPR round trip): a DMA instruction writes 64 consecutive 16-byte slots, one per lane, and the lane
+// chooses which (key, unit) it fetches, so the buffer holds the rows in a swizzled row-major layout
+// (unit u of key k in slot k*UPR + (u ^ swz(k))) that keeps both read patterns below free of bank
+// conflicts.  Two buffers: chunk c + 1 is in flight while chunk c is computed; the row indices are fetched
+// one chunk further ahead; one barrier per chunk.
+//   QK^T   S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (M = 16 keys, N = 16 heads), q rows as B-fragments
+//          in VGPRs; lane (head = l%16, g = l/16) receives keys 16t + 4g + r (t = 0, 1; r = 0..3).
+//   softmax online in base 2 with a lazily updated reference max (rescale only when a chunk's max exceeds
+//          it by more than 2^8), invalid keys -> 0.
+//   PV     O = P V (M = 16 heads, N = 16 dv columns, K = 32 keys).  A lane's 8 probabilities are its
+//          A-fragment as they are; the matching V fragment (keys 4g..4g+3 and 16+4g..16+4g+3 of one column)
+//          comes from the same buffer with two ds_read_b64_tr_b16 transpose reads, so V is neither copied
+//          nor transposed.
+// One range per query finalises in place (sink added, bf16 store); otherwise partial (O, max, sum) go to
+// the workspace and a combine kernel merges the ranges with the sink (one wave per output row).
 #include "common.h"
 
 namespace ks {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kKC = 32;  // keys per chunk
+constexpr int kKC = 32;               // keys per chunk
+constexpr int kLdsBudget = 160 * 1024 - 1024;
+constexpr int kTargetWaves = 2048;    // waves in flight the split heuristic aims for
+constexpr int kMinChunks = 4;         // at least this many chunks per work item
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleTau = 8.f;    // lazy rescale threshold (log2 units): probabilities stay <= 2^8
 
 __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                   0, 0, 0);
 }
 
+// Two fp32 -> packed bf16 (RNE), one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16_rne(lo)) | (static_cast<uint32_t>(f32_to_bf16_rne(hi)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
-// Split heuristic shared by the launcher and the workspace-size query: aim for ~2048 waves in flight.
-__host__ __device__ inline int choose_splits(int64_t B, int64_t M, int64_t H, int64_t K) {
-  const int64_t waves_per_query = (H + 15) / 16;
+// 2^x with the hardware transcendental (v_exp_f32); softmax weights need no denormal results.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ds_read_b64_tr_b16: within each 16-lane row, lane i receives element i%4 of the 8-byte rows addressed by
+// lanes 4e + i/4 (e = 0..3), i.e. a 4 x 4 block transpose of 16-bit elements across lane quads.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
+  typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t *)(const_cast<uint16_t *>(p)));
+  return __builtin_bit_cast(uint2, v);
+}
+
+// 16 bytes from global memory into LDS: lane i of the wave writes lds_base + 16 i (lds_base wave-uniform).
+// Issued as inline assembly so that the compiler does not order the LDS reads of the other buffer behind
+// it; completion is awaited explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes the chunk.
+// base: wave-uniform 64-bit global address (SGPR pair), voff: per-lane byte offset, lds: LDS byte address.
+__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+// A wave-uniform pointer moved to SGPRs (the compiler cannot prove uniformity of values derived from the
+// wave index).
+template <typename T>
+__device__ __forceinline__ T *uniform_ptr(T *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<T *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// LDS byte address of a __shared__ object (an address-space cast of a known LDS pointer, done once).
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T *p) {
+  typedef __attribute__((address_space(3))) T lds_t;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_t *)(p)));
+}
+
+// Reductions over the four 16-lane rows of the wave (lanes l, l^16, l^32, l^48), result in every lane:
+// v_permlane16_swap exchanges rows 1/3 of its first operand with rows 0/2 of its second, so with the value
+// in both operands each lane holds its row pair's two values; v_permlane32_swap does the same across the
+// wave halves.  Inline assembly (the builtin form was miscompiled into v op v when both operands carry the
+// same value); the NOPs cover the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void swap16(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float &a, float &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float rows_max(float v) {
+  float a = v, b = v;
+  swap16(a, b);
+  float c = fmaxf(a, b), d = c;
+  swap32(c, d);
+  return fmaxf(c, d);
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  float a = v, b = v;
+  swap16(a, b);
+  float c = a + b, d = c;
+  swap32(c, d);
+  return c + d;
+}
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int DQK, int DV, int GW>
+struct SaShape {
+  static constexpr int UPR = DQK / 8;  // 16-byte units per row
+  static constexpr int NTG = 64 * GW;  // threads per group
+  static constexpr int UNITS = kKC * UPR;
+  static constexpr int TI = UNITS / 64;          // DMA instructions per chunk (64 slots each)
+  static constexpr int NJ = (TI + GW - 1) / GW;  // ... per wave
+  static constexpr int BUF = UNITS * 8;          // bf16 elements per chunk buffer
+  // q fragments (one uint4 per lane and k-step): the first QREG k-steps stay in VGPRs, the rest in LDS
+  // (wide heads: 16 heads x 576 dims of q plus 16 x 512 fp32 accumulators would not fit 256 VGPRs)
+  static constexpr int QJ = DQK / 32;
+  static constexpr int QREG = DQK > 256 ? QJ / 2 : QJ;
+  static constexpr int QL = QJ - QREG;
+  static constexpr int GROUP_BYTES = 2 * BUF * 2 + GW * (QL > 0 ? QL : 0) * 64 * 16;
+  static constexpr int FIT = kLdsBudget / GROUP_BYTES;
+  static constexpr int GROUPS = (8 / GW) < FIT ? (8 / GW) : FIT;
+  static constexpr int THREADS = GROUPS * NTG;
+  static_assert(GROUPS >= 1, "one group must fit in LDS");
+  static_assert(UNITS % 64 == 0 && UPR % 8 == 0, "chunk must be whole DMA instructions");
+  // Slot of unit u of key k.  Rows of 16 units start on bank 0: XOR with 2(k & 7) spreads 8 keys over the
+  // 8 odd/even unit pairs; rows of 72 units alternate between bank halves: XOR with k & 7 suffices.
+  static constexpr int SW = UPR % 16 == 0 ? 16 : 8;  // the XOR touches unit bits below SW
+  __device__ static __forceinline__ int swz(int k) { return UPR % 16 == 0 ? (k & 7) << 1 : (k & 7); }
+  // slot of unit u = u_hi + u_lo with u_hi a compile-time multiple of SW and 0 <= u_lo < SW: written so
+  // that u_hi folds into the LDS instruction's immediate offset
+  __device__ static __forceinline__ int slot(int k, int u_hi, int u_lo) { return k * UPR + u_hi + (u_lo ^ swz(k)); }
+};
+
+inline int waves_per_group(int64_t H) {
+  const int64_t w = (H + 15) / 16;
+  return w <= 1 ? 1 : w <= 2 ? 2 : w <= 4 ? 4 : 8;
+}
+
+// Key ranges per query: enough work items for ~kTargetWaves waves, at least kMinChunks chunks each.
+inline int choose_splits(int64_t B, int64_t M, int64_t H, int64_t K) {
+  const int64_t waves_base = B * M * waves_per_group(H);
   const int64_t chunks = (K + kKC - 1) / kKC;
-  int64_t ns = 2048 / (B * M * waves_per_query > 0 ? B * M * waves_per_query : 1);
-  if (ns < 1) ns = 1;
-  if (ns > chunks) ns = chunks;
+  int64_t ns = (kTargetWaves + waves_base - 1) / (waves_base > 0 ? waves_base : 1);
+  const int64_t cap = chunks / kMinChunks > 1 ? chunks / kMinChunks : 1;
+  if (ns > cap) ns = cap;
   if (ns > 64) ns = 64;
+  if (ns < 1) ns = 1;
   return static_cast<int>(ns);
 }
 
-template <int DQK, int DV>
-struct SaLds {
-  static constexpr int kRowStride = DQK + 8;  // bf16 elements per padded K row (+16 bytes)
-  uint16_t krm[kKC * kRowStride];
-  uint16_t vil[kKC * DV];  // [key/8][d][key%8]
-  int32_t rows[kKC];       // gathered row index, -1 = invalid
+struct SaSplit {
+  int ns;   // ranges actually used
+  int kr;   // keys per range (multiple of kKC)
 };
 
-template <int DQK, int DV>
-__global__ __launch_bounds__(512) void sparse_attn_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ kv,
-                                                         const float *__restrict__ sink, const int32_t *__restrict__ idx,
-                                                         uint16_t *__restrict__ out, float *__restrict__ part_o,
-                                                         float *__restrict__ part_ml, int64_t M, int64_t H, int64_t N,
-                                                         int64_t K, int NS, int KR, float scale_log2) {
-  using L = SaLds<DQK, DV>;
-  constexpr int RS = L::kRowStride;
-  constexpr int QJ = DQK / 32;  // k-steps of the QK MFMA
+inline SaSplit split_plan(int64_t B, int64_t M, int64_t H, int64_t K) {
+  const int ns0 = choose_splits(B, M, H, K);
+  const int64_t chunks = (K + kKC - 1) / kKC;
+  const int64_t kr = ((chunks + ns0 - 1) / ns0) * kKC;
+  return SaSplit{static_cast<int>((K + kr - 1) / kr), static_cast<int>(kr)};
+}
+
+template <int DQK, int DV, int GW>
+__global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kv, const float *__restrict__ sink,
+    const int32_t *__restrict__ idx, uint16_t *__restrict__ out, float *__restrict__ part_o,
+    float *__restrict__ part_ml, int64_t n_items, int64_t M, int H, int64_t N, int64_t K, int NS, int KR,
+    float scale_log2) {
+  using Sh = SaShape<DQK, DV, GW>;
+  constexpr int QJ = Sh::QJ, QREG = Sh::QREG, QL = Sh::QL;  // k-steps of the QK MFMA
   constexpr int CT = DV / 16;   // dv column tiles
-  __shared__ L lds;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nthreads = blockDim.x;
-  const int split = blockIdx.x;
-  const int64_t m = blockIdx.y, b = blockIdx.z;
+  constexpr int UPR = Sh::UPR, NJ = Sh::NJ;
+  __shared__ __attribute__((aligned(16))) uint16_t kb[Sh::GROUPS][2][Sh::BUF];
+  __shared__ __attribute__((aligned(16))) uint4 qs[Sh::GROUPS][GW][QL > 0 ? QL : 1][64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps item / row math scalar
+  const int grp = wave / GW, gw = wave % GW;
   const int l16 = lane & 15, g = lane >> 4;
-  const int head = wave * 16 + l16;  // head of this lane in the S^T / softmax layout
-  const bool head_ok = head < H;
-  const int64_t qm = b * M + m;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * Sh::GROUPS + grp;
+  const bool item_ok = item < n_items;
+  const int64_t qm = item_ok ? item / NS : 0;
+  const int split = item_ok ? static_cast<int>(item % NS) : 0;
+  const int64_t b = qm / M;
+  const int head = gw * 16 + l16;
+  const bool head_ok = item_ok && head < H;
+  const int k_begin = split * KR;  // K < 2^31 (host-checked): key positions fit int32
+  const int k_end = item_ok ? (k_begin + KR < K ? k_begin + KR : static_cast<int>(K)) : k_begin;
+  const int32_t *irow = uniform_ptr(idx + qm * K);
+  const uint16_t *kvb = uniform_ptr(kv + b * N * DQK);
+  const int nch = (KR + kKC - 1) / kKC;  // the same for every group of the workgroup
+
+  // DMA slot 64 (gw + GW i) + lane of a chunk holds unit u_i of key key_i (fixed per lane).
+  int key_i[NJ], uoff_i[NJ];
+#pragma unroll
+  for (int i = 0; i < NJ; ++i) {
+    const int sl = 64 * (gw + GW * i) + lane;
+    key_i[i] = sl / UPR;
+    uoff_i[i] = ((sl % UPR) ^ Sh::swz(key_i[i])) * 16;  // the XOR is an involution
+  }
+  const uint32_t kb_lds = __builtin_amdgcn_readfirstlane(lds_addr(&kb[grp][0][0]));
+  const int n32 = static_cast<int>(N), k32 = static_cast<int>(K);
+  // Raw indices of chunk c: for each DMA slot i, and for key (lane & 31) (validity mask).  Loaded without
+  // a branch and validated only where they are used one chunk later, so no wait is placed behind the loads.
+  auto raw_idx = [&](int c, int key) -> int32_t {
+    const int t = k_begin + c * kKC + key;
+    return irow[t < k32 ? t : k32 - 1];
+  };
+  // bit k: key k of chunk c is valid (inside the range, index in [0, N)); wave-uniform
+  auto valid_mask = [&](int c, int32_t vraw) -> uint32_t {
+    const bool ok = k_begin + c * kKC + (lane & 31) < k_end && vraw >= 0 && vraw < n32;
+    return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(ok));
+  };
+  // gather chunk c's rows into buffer `buf` (invalid keys read row 0: finite data, masked by `vm`)
+  auto gather = [&](const int32_t(&raw)[NJ], uint32_t vm, int buf) {
+#pragma unroll
+    for (int i = 0; i < NJ; ++i) {
+      const int jj = gw + GW * i;
+      if (jj < Sh::TI) {
+        const bool ok = (vm >> key_i[i]) & 1u;
+        const uint32_t voff = static_cast<uint32_t>(ok ? raw[i] : 0) * (DQK * 2) + uoff_i[i];
+        dma16(kvb, voff, kb_lds + (buf * Sh::BUF + 64 * jj * 8) * 2);
+      }
+    }
+  };
 
   // q B-fragments: Q[head][32j + 8g .. +7]
-  uint4 qf[QJ];
+  uint4 qf[QREG];
 #pragma unroll
-  for (int j = 0; j < QJ; ++j)
-    qf[j] = head_ok ? *reinterpret_cast<const uint4 *>(q + (qm * H + head) * DQK + 32 * j + 8 * g)
-                    : make_uint4(0, 0, 0, 0);
+  for (int j = 0; j < QJ; ++j) {
+    const uint4 v = head_ok ? *reinterpret_cast<const uint4 *>(q + (qm * H + head) * DQK + 32 * j + 8 * g)
+                            : make_uint4(0, 0, 0, 0);
+    if (j < QREG) qf[j < QREG ? j : 0] = v;
+    else qs[grp][gw][j - QREG][lane] = v;
+  }
 
-  float run_max = -INFINITY, run_sum = 0.f;  // per head (lane l16), replicated over g
+  int32_t nraw[NJ];
+#pragma unroll
+  for (int i = 0; i < NJ; ++i) nraw[i] = raw_idx(0, key_i[i]);
+  int32_t nvraw = raw_idx(0, lane & 31);
+  uint32_t vm_cur = valid_mask(0, nvraw);
+  gather(nraw, vm_cur, 0);
+  const int c1 = nch > 1 ? 1 : 0;
+#pragma unroll
+  for (int i = 0; i < NJ; ++i) nraw[i] = raw_idx(c1, key_i[i]);
+  nvraw = raw_idx(c1, lane & 31);
+  wait_dma();
+  __syncthreads();
+
+  // Per-lane LDS element offsets of the swizzled reads, one per distinct low-unit pattern; the high unit
+  // bits add compile-time offsets.  QK: key 16t + l16, unit 4j + g.  PV (transpose reads): keys
+  // 4g + (l16 >> 2) (+16), unit 2cc + ((l16 & 3) >> 1), 8-byte half l16 & 1.
+  int qk_off[2][Sh::SW / 4], pv_off[2][Sh::SW / 2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int p = 0; p < Sh::SW / 4; ++p) qk_off[t][p] = Sh::slot(16 * t + l16, 0, 4 * p + g) * 8;
+    const int kv_key = 4 * g + (l16 >> 2) + 16 * t;
+#pragma unroll
+    for (int p = 0; p < Sh::SW / 2; ++p)
+      pv_off[t][p] = Sh::slot(kv_key, 0, 2 * p + ((l16 & 3) >> 1)) * 8 + 4 * (l16 & 1);
+  }
+
+  float m_ref = -INFINITY, l_run = 0.f;  // per head (lane l16), replicated over g
   f32x4_t o[CT];
 #pragma unroll
   for (int c = 0; c < CT; ++c) o[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t k_begin = static_cast<int64_t>(split) * KR;
-  const int64_t k_end = (k_begin + KR < K) ? k_begin + KR : K;
-  const int32_t *irow = idx + qm * K;
-  const uint16_t *kvb = kv + b * N * DQK;
-
-  for (int64_t c0 = k_begin; c0 < k_end; c0 += kKC) {
-    // ---- indices of this chunk
-    if (tid < kKC) {
-      const int64_t t = c0 + tid;
-      int32_t r = t < k_end ? irow[t] : -1;
-      if (r < 0 || r >= N) r = -1;
-      lds.rows[tid] = r;
-    }
-    __syncthreads();
-    // ---- gather: K row-major (padded) and V key-interleaved
-    constexpr int UPR = DQK / 8;  // 16-byte units per row
-    for (int u = tid; u < kKC * UPR; u += nthreads) {
-      const int key = u / UPR, ch = u % UPR;
-      const int32_t r = lds.rows[key];
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (r >= 0) v = *reinterpret_cast<const uint4 *>(kvb + static_cast<int64_t>(r) * DQK + ch * 8);
-      *reinterpret_cast<uint4 *>(&lds.krm[key * RS + ch * 8]) = v;
-      if (ch * 8 < DV) {
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-        uint16_t *dstv = &lds.vil[(key >> 3) * (DV * 8) + (ch * 8) * 8 + (key & 7)];
+  for (int c = 0; c < nch; ++c) {
+    const int buf = c & 1;
+    uint32_t vm_next = 0;
+    if (c + 1 < nch) {  // chunk c + 1 into the other buffer while this one is computed
+      vm_next = valid_mask(c + 1, nvraw);
+      gather(nraw, vm_next, buf ^ 1);
+      const int c2 = c + 2 < nch ? c + 2 : c + 1;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dstv[e * 8] = static_cast<uint16_t>(e & 1 ? (w4[e >> 1] >> 16) : (w4[e >> 1] & 0xFFFFu));
-      }
+      for (int i = 0; i < NJ; ++i) nraw[i] = raw_idx(c2, key_i[i]);
+      nvraw = raw_idx(c2, lane & 31);
     }
-    __syncthreads();
-
-    // ---- S^T = K Q^T for two 16-key tiles
+    const uint16_t *kbp = kb[grp][buf];
+    // ---- S^T = K Q^T for the chunk's two 16-key tiles
     f32x4_t st[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       st[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const int key = 16 * t + l16;
 #pragma unroll
       for (int j = 0; j < QJ; ++j) {
-        const uint4 a = *reinterpret_cast<const uint4 *>(&lds.krm[key * RS + 32 * j + 8 * g]);
-        st[t] = mfma16(a, qf[j], st[t]);
+        constexpr int kPat = Sh::SW / 4;  // distinct (4j mod SW) patterns
+        const uint16_t *a = kbp + qk_off[t][j % kPat] + ((4 * j) & ~(Sh::SW - 1)) * 8;
+        st[t] = mfma16(*reinterpret_cast<const uint4 *>(a),
+                       j < QREG ? qf[j < QREG ? j : 0] : qs[grp][gw][j < QREG ? 0 : j - QREG][lane], st[t]);
       }
     }
-    // lane holds keys 16t + 4g + r for head l16
-    float p[8];
+    // ---- online softmax (lane: head l16, keys 16t + 4g + r)
+    const uint32_t vbits = vm_cur >> (4 * g);  // bit 16t + r: key 16t + 4g + r
+    float sc[8];
     float cmax = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool ok = lds.rows[16 * t + 4 * g + r] >= 0;
+        const bool ok = (vbits >> (16 * t + r)) & 1u;
         const float sv = ok ? st[t][r] * scale_log2 : -INFINITY;
-        p[4 * t + r] = sv;
+        sc[4 * t + r] = sv;
         cmax = fmaxf(cmax, sv);
       }
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-    const float new_max = fmaxf(run_max, cmax);
-    const float alpha = (new_max == -INFINITY) ? 1.f : exp2f(run_max - new_max);
-    float csum = 0.f;
+    cmax = rows_max(cmax);
+    const bool need = cmax > m_ref + kRescaleTau;  // false for cmax = -inf; true for a first valid chunk
+    if (__builtin_amdgcn_ballot_w64(need) != 0ull) {
+      const float m_new = need ? cmax : m_ref;
+      const float alpha = need ? (m_ref == -INFINITY ? 0.f : fast_exp2(m_ref - m_new)) : 1.f;
+      l_run *= alpha;
+      m_ref = m_new;
+      // O rows are heads 4g + r; their alpha lives in lane 4g + r
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+        for (int cc = 0; cc < CT; ++cc) o[cc][r] *= ar;
+      }
+    }
+    float p[8], csum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      p[i] = (p[i] == -INFINITY) ? 0.f : exp2f(p[i] - new_max);
+      p[i] = sc[i] == -INFINITY ? 0.f : fast_exp2(sc[i] - m_ref);
       csum += p[i];
     }
-    csum += __shfl_xor(csum, 16, 64);
-    csum += __shfl_xor(csum, 32, 64);
-    run_sum = run_sum * alpha + csum;
-    run_max = new_max;
-    // rescale O rows (heads 4g + r of this wave): alpha lives in lane l16 = 4g + r
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(alpha, 4 * g + r, 64);
-#pragma unroll
-      for (int c = 0; c < CT; ++c) o[c][r] *= ar;
-    }
-    // ---- O += P V
+    l_run += rows_sum(csum);
+    // ---- O += P V: V fragment of keys 16h + 4g + (l16 >> 2), dv columns 16cc + 4(l16 & 3) .. +3
     const uint4 pa = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                                 pack_bf16x2(p[6], p[7]));
-    const int grp0 = g >> 1, off = 4 * (g & 1);
 #pragma unroll
-    for (int c = 0; c < CT; ++c) {
-      const int col = 16 * c + l16;
-      const uint2 v0 = *reinterpret_cast<const uint2 *>(&lds.vil[grp0 * (DV * 8) + col * 8 + off]);
-      const uint2 v1 = *reinterpret_cast<const uint2 *>(&lds.vil[(grp0 + 2) * (DV * 8) + col * 8 + off]);
-      o[c] = mfma16(pa, make_uint4(v0.x, v0.y, v1.x, v1.y), o[c]);
+    for (int cc = 0; cc < CT; ++cc) {
+      constexpr int kPat = Sh::SW / 2;  // distinct (2cc mod SW) patterns
+      const int hi = ((2 * cc) & ~(Sh::SW - 1)) * 8;
+      const uint2 b0 = lds_read_tr16(kbp + pv_off[0][cc % kPat] + hi);
+      const uint2 b1 = lds_read_tr16(kbp + pv_off[1][cc % kPat] + hi);
+      o[cc] = mfma16(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), o[cc]);
     }
-    __syncthreads();  // LDS is refilled by the next chunk
+    wait_dma();       // this wave's part of chunk c + 1 has landed
+    __syncthreads();  // ... everyone's; and buffer `buf` may be refilled
+    vm_cur = vm_next;
   }
 
+  if (!item_ok) return;
   // ---- finalise: O rows are heads 4g + r; their (max, sum) live in lanes 4g + r
   if (NS == 1) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int hr = wave * 16 + 4 * g + r;
-      const float mx = __shfl(run_max, 4 * g + r, 64);
-      const float sm = __shfl(run_sum, 4 * g + r, 64);
+      const int hr = gw * 16 + 4 * g + r;
+      const float mx = __shfl(m_ref, 4 * g + r, 64);
+      const float sm = __shfl(l_run, 4 * g + r, 64);
       if (hr < H) {
         const float sk = sink[hr] * kLog2e;
         const float zmax = fmaxf(mx, sk);
@@ -196,89 +373,120 @@ __global__ __launch_bounds__(512) void sparse_attn_kernel(const uint16_t *__rest
         }
         uint16_t *orow = out + (qm * H + hr) * DV;
 #pragma unroll
-        for (int c = 0; c < CT; ++c) orow[16 * c + l16] = f32_to_bf16_rne(o[c][r] * scale_o);
+        for (int cc = 0; cc < CT; ++cc) orow[16 * cc + l16] = f32_to_bf16_rne(o[cc][r] * scale_o);
       }
     }
   } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int hr = wave * 16 + 4 * g + r;
+      const int hr = gw * 16 + 4 * g + r;
       if (hr < H) {
-        float *po = part_o + ((qm * NS + split) * H + hr) * DV;
+        float *po = part_o + (item * H + hr) * DV;
 #pragma unroll
-        for (int c = 0; c < CT; ++c) po[16 * c + l16] = o[c][r];
+        for (int cc = 0; cc < CT; ++cc) po[16 * cc + l16] = o[cc][r];
       }
     }
     if (g == 0 && head_ok) {
-      float *pml = part_ml + ((qm * NS + split) * H + head) * 2;
-      pml[0] = run_max;
-      pml[1] = run_sum;
+      float *pml = part_ml + (item * H + head) * 2;
+      pml[0] = m_ref;
+      pml[1] = l_run;
     }
   }
 }
 
-// Merge NS partial ranges per (query, head) with the sink: one thread per output element.
+// Merge the NS partial ranges of one (query, head) row with the sink: one wave per row, lane s reads
+// range s's (max, sum); every lane then accumulates DV/64 columns over the ranges.
+template <int DV>
 __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const float *__restrict__ part_o,
                                                                  const float *__restrict__ part_ml,
                                                                  const float *__restrict__ sink,
-                                                                 uint16_t *__restrict__ out, int64_t QH, int64_t H,
-                                                                 int DV, int NS) {
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (e >= QH * DV) return;
-  const int64_t qh = e / DV;
-  const int col = static_cast<int>(e % DV);
-  const int64_t qi = qh / H, h = qh % H;
+                                                                 uint16_t *__restrict__ out, int64_t rows, int H,
+                                                                 int NS) {
+  constexpr int CPL = DV / 64;  // columns per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // uniform per wave
+  const int64_t qm = row / H;
+  const int h = static_cast<int>(row % H);
   const float sk = sink[h] * kLog2e;
-  float zmax = sk;
-  for (int s = 0; s < NS; ++s) zmax = fmaxf(zmax, part_ml[((qi * NS + s) * H + h) * 2]);
-  float den = 0.f, acc = 0.f;
-  if (zmax != -INFINITY) {
-    den = exp2f(sk - zmax);
-    for (int s = 0; s < NS; ++s) {
-      const int64_t base = (qi * NS + s) * H + h;
-      const float mx = part_ml[base * 2];
-      if (mx == -INFINITY) continue;
-      const float w = exp2f(mx - zmax);
-      den += part_ml[base * 2 + 1] * w;
-      acc += part_o[base * DV + col] * w;
+  float m = -INFINITY, l = 0.f;
+  if (lane < NS) {
+    const float *ml = part_ml + ((qm * NS + lane) * H + h) * 2;
+    m = ml[0];
+    l = ml[1];
+  }
+  float z = m;
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) z = fmaxf(z, __shfl_xor(z, d, 64));
+  z = fmaxf(z, sk);
+  const float w = (m == -INFINITY || z == -INFINITY) ? 0.f : exp2f(m - z);
+  float den = w * l;
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) den += __shfl_xor(den, d, 64);
+  if (z != -INFINITY) den += exp2f(sk - z);
+  float acc[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) acc[i] = 0.f;
+  const float *po = part_o + (qm * NS * H + h) * DV + lane * CPL;
+  // empty ranges have w = 0 and O = 0, so every range is accumulated without a branch
+#pragma unroll 8
+  for (int s = 0; s < NS; ++s) {
+    const float ws = __shfl(w, s, 64);
+    const float *src = po + static_cast<int64_t>(s) * H * DV;
+#pragma unroll
+    for (int i = 0; i < CPL; i += 2) {
+      const float2 v = *reinterpret_cast<const float2 *>(src + i);
+      acc[i] += ws * v.x;
+      acc[i + 1] += ws * v.y;
     }
   }
-  out[e] = f32_to_bf16_rne(den > 0.f ? acc / den : 0.f);
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  uint16_t *orow = out + row * DV + lane * CPL;
+#pragma unroll
+  for (int i = 0; i < CPL; i += 2)
+    *reinterpret_cast<uint32_t *>(orow + i) = pack_bf16x2(acc[i] * inv, acc[i + 1] * inv);
 }
 
-template <int DQK, int DV>
-int launch_sa(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
-              int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
-  const int NS = choose_splits(B, M, H, K);
-  const int64_t chunks = (K + kKC - 1) / kKC;
-  const int KR = static_cast<int>(((chunks + NS - 1) / NS) * kKC);
-  const int nsplit = static_cast<int>((K + KR - 1) / KR);  // ranges actually used
+template <int DQK, int DV, int GW>
+int launch_sa_gw(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
+                 int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
+  using Sh = SaShape<DQK, DV, GW>;
+  const SaSplit sp = split_plan(B, M, H, K);
+  const int64_t n_items = B * M * sp.ns;
   float *part_o = nullptr, *part_ml = nullptr;
-  if (nsplit > 1) {
+  if (sp.ns > 1) {
     part_o = static_cast<float *>(ws);
-    part_ml = part_o + B * M * nsplit * H * DV;
+    part_ml = part_o + n_items * H * DV;
   }
-  const int waves = static_cast<int>((H + 15) / 16);
-  dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(M), static_cast<unsigned>(B));
-  hipLaunchKernelGGL((sparse_attn_kernel<DQK, DV>), grid, dim3(64 * waves), 0, stream, q, kv, sink, idx, out, part_o,
-                     part_ml, M, H, N, K, nsplit, KR, scale * kLog2e);
+  const int64_t blocks = ceil_div(n_items, Sh::GROUPS);
+  hipLaunchKernelGGL((sparse_attn_kernel<DQK, DV, GW>), dim3(static_cast<unsigned>(blocks)), dim3(Sh::THREADS), 0,
+                     stream, q, kv, sink, idx, out, part_o, part_ml, n_items, M, static_cast<int>(H), N, K, sp.ns,
+                     sp.kr, scale * kLog2e);
   KS_CHECK_LAUNCH("sparse_attn_kernel");
-  if (nsplit > 1) {
-    const int64_t total = B * M * H * DV;
-    hipLaunchKernelGGL(sparse_attn_combine_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0,
-                       stream, part_o, part_ml, sink, out, B * M * H, H, DV, nsplit);
+  if (sp.ns > 1) {
+    const int64_t rows = B * M * H;
+    hipLaunchKernelGGL((sparse_attn_combine_kernel<DV>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
+                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), sp.ns);
     KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
   }
   return KS_OK;
 }
 
+template <int DQK, int DV>
+int launch_sa(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
+              int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
+  switch (waves_per_group(H)) {
+    case 1: return launch_sa_gw<DQK, DV, 1>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+    case 2: return launch_sa_gw<DQK, DV, 2>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+    case 4: return launch_sa_gw<DQK, DV, 4>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+    default: return launch_sa_gw<DQK, DV, 8>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+  }
+}
+
 size_t sa_workspace(int64_t B, int64_t M, int64_t H, int64_t K, int64_t DV) {
-  const int NS = choose_splits(B, M, H, K);
-  const int64_t chunks = (K + kKC - 1) / kKC;
-  const int64_t KR = ((chunks + NS - 1) / NS) * kKC;
-  const int64_t nsplit = (K + KR - 1) / KR;
-  if (nsplit <= 1) return 0;
-  return static_cast<size_t>(B * M * nsplit * H * (DV + 2)) * sizeof(float);
+  const SaSplit sp = split_plan(B, M, H, K);
+  if (sp.ns <= 1) return 0;
+  return static_cast<size_t>(B * M * sp.ns * H * (DV + 2)) * sizeof(float);
 }
 
 }  // namespace
@@ -302,6 +510,8 @@ extern "C" int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float
   KS_CHECK_ARG(d128 || d576, "ks_sparse_attn: (Dqk, Dv)=(%lld, %lld); supported: (128, 128), (576, 512)",
                (long long)Dqk, (long long)Dv);
   KS_CHECK_ARG(M < 65536 && B < 65536, "ks_sparse_attn: M and B must be < 65536");
+  KS_CHECK_ARG(K < (int64_t(1) << 31) && N * Dqk * 2 < (int64_t(1) << 32),
+               "ks_sparse_attn: K must be < 2^31 and one batch's kv (N*Dqk*2 bytes) < 4 GiB");
   if (B * M == 0) return KS_OK;
   KS_CHECK_ARG(q && kv && sink && idx && out, "ks_sparse_attn: null pointer");
   KS_CHECK_ARG(ks::aligned(q, 16) && ks::aligned(kv, 16), "ks_sparse_attn: q and kv must be 16-byte aligned");

@@ -189,7 +189,11 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps item / row math scalar
   const int grp = wave / GW, gw = wave % GW;
   const int l16 = lane & 15, g = lane >> 4;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * Sh::GROUPS + grp;
+  // Workgroups are dealt to the 8 XCDs round-robin (block id mod 8); consecutive logical workgroups (the
+  // ranges of one query, which share its q rows) are placed on one XCD so that they share its L2.
+  const int64_t nblk = gridDim.x;
+  const int64_t wg = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int64_t item = wg * Sh::GROUPS + grp;
   const bool item_ok = item < n_items;
   const int64_t qm = item_ok ? item / NS : 0;
   const int split = item_ok ? static_cast<int>(item % NS) : 0;
@@ -257,7 +261,7 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
   for (int i = 0; i < NJ; ++i) nraw[i] = raw_idx(c1, key_i[i]);
   nvraw = raw_idx(c1, lane & 31);
   wait_dma();
-  __syncthreads();
+  __syncthreads();  // also publishes the q fragments kept in LDS
 
   // Per-lane LDS element offsets of the swizzled reads, one per distinct low-unit pattern; the high unit
   // bits add compile-time offsets.  QK: key 16t + l16, unit 4j + g.  PV (transpose reads): keys
@@ -349,11 +353,78 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
       const uint2 b1 = lds_read_tr16(kbp + pv_off[1][cc % kPat] + hi);
       o[cc] = mfma16(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), o[cc]);
     }
-    wait_dma();       // this wave's part of chunk c + 1 has landed
-    __syncthreads();  // ... everyone's; and buffer `buf` may be refilled
+    // this wave's part of chunk c + 1 has landed (the DMA counts as a vector-memory load); with several
+    // waves per group, a barrier then publishes everyone's part and releases buffer `buf` for refilling.
+    // A one-wave group needs no barrier: its own reads of `buf` completed before the MFMAs that used them.
+    wait_dma();
+    if constexpr (GW > 1) __syncthreads();
     vm_cur = vm_next;
   }
 
+  // Merge of the GROUPS ranges of one query held by this workgroup (one-wave groups): each wave leaves its
+  // (max, sum) per head and its O in LDS (the chunk buffers are free now); the workgroup then combines
+  // them per (head, column) and writes one partial range (or the output, when it covers the query).
+  auto merge_groups = [&](const f32x4_t(&oo)[CT], float mr, float lr) {
+    static_assert(Sh::GROUPS * 16 * DV * 4 + Sh::GROUPS * 32 * 4 <= Sh::GROUPS * 2 * Sh::BUF * 2, "merge fits");
+    float *mo = reinterpret_cast<float *>(&kb[0][0][0]);  // [GROUPS][16 heads][DV]
+    float *mml = mo + Sh::GROUPS * 16 * DV;               // [GROUPS][16 heads][2]
+    __syncthreads();  // every wave is done reading its chunk buffers
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int cc = 0; cc < CT; ++cc) mo[(grp * 16 + 4 * g + r) * DV + 16 * cc + l16] = oo[cc][r];
+    if (g == 0) {
+      mml[(grp * 16 + l16) * 2] = item_ok ? mr : -INFINITY;
+      mml[(grp * 16 + l16) * 2 + 1] = item_ok ? lr : 0.f;
+    }
+    __syncthreads();
+    const int nsm = NS / Sh::GROUPS;  // merged ranges per query
+    const int64_t sitem = wg;         // merged range index: query qm = sitem / nsm
+    const int64_t sq = sitem / nsm;
+    if (sq >= n_items / NS) return;  // padding workgroup (uniform)
+    for (int e = tid; e < 16 * DV; e += Sh::THREADS) {
+      const int h = e / DV, d = e % DV;
+      float z = -INFINITY;
+#pragma unroll
+      for (int gi = 0; gi < Sh::GROUPS; ++gi) z = fmaxf(z, mml[(gi * 16 + h) * 2]);
+      float acc = 0.f, lsum = 0.f;
+      if (z != -INFINITY) {
+#pragma unroll
+        for (int gi = 0; gi < Sh::GROUPS; ++gi) {
+          const float mg = mml[(gi * 16 + h) * 2];
+          const float wgt = mg == -INFINITY ? 0.f : fast_exp2(mg - z);
+          lsum += wgt * mml[(gi * 16 + h) * 2 + 1];
+          acc += wgt * mo[(gi * 16 + h) * DV + d];
+        }
+      }
+      if (h >= H) continue;
+      if (nsm == 1) {
+        const float sk = sink[h] * kLog2e;
+        const float zz = fmaxf(z, sk);
+        float val = 0.f;
+        if (zz != -INFINITY) {
+          const float ez = z == -INFINITY ? 0.f : exp2f(z - zz);
+          const float den = lsum * ez + exp2f(sk - zz);
+          val = den > 0.f ? acc * ez / den : 0.f;
+        }
+        out[(sq * H + h) * DV + d] = f32_to_bf16_rne(val);
+      } else {
+        part_o[(sitem * H + h) * DV + d] = acc;
+        if (d == 0) {
+          part_ml[(sitem * H + h) * 2] = z;
+          part_ml[(sitem * H + h) * 2 + 1] = lsum;
+        }
+      }
+    }
+  };
+
+  // ---- one-wave groups whose workgroup holds consecutive ranges of one query merge in LDS first
+  if constexpr (GW == 1 && Sh::GROUPS > 1) {
+    if (NS % Sh::GROUPS == 0) {
+      merge_groups(o, m_ref, l_run);
+      return;
+    }
+  }
   if (!item_ok) return;
   // ---- finalise: O rows are heads 4g + r; their (max, sum) live in lanes 4g + r
   if (NS == 1) {
@@ -463,10 +534,13 @@ int launch_sa_gw(const uint16_t *q, const uint16_t *kv, const float *sink, const
                      stream, q, kv, sink, idx, out, part_o, part_ml, n_items, M, static_cast<int>(H), N, K, sp.ns,
                      sp.kr, scale * kLog2e);
   KS_CHECK_LAUNCH("sparse_attn_kernel");
-  if (sp.ns > 1) {
+  // one-wave groups merge the ranges of a workgroup in LDS when a workgroup holds whole ranges of a query
+  const bool merged = GW == 1 && Sh::GROUPS > 1 && sp.ns % Sh::GROUPS == 0;
+  const int ns_left = merged ? sp.ns / Sh::GROUPS : sp.ns;
+  if (ns_left > 1) {
     const int64_t rows = B * M * H;
     hipLaunchKernelGGL((sparse_attn_combine_kernel<DV>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
-                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), sp.ns);
+                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), ns_left);
     KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
   }
   return KS_OK;

@@ -60,4 +60,41 @@ __host__ __device__ inline uint16_t f32_to_bf16_rne(float f) {
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+
+// ---------------------------------------------------------------- cross-lane exchange
+// v_permlane16_swap / v_permlane32_swap (gfx950): the first operand's rows 1 and 3 (16-lane rows) trade
+// places with the second operand's rows 0 and 2 (16_swap), or its rows 2-3 with the second's rows 0-1
+// (32_swap).  Inline assembly: the builtin form was miscompiled when both operands carry the same value;
+// the NOPs cover the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void permlane16_swap(uint32_t &a, uint32_t &b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(uint32_t &a, uint32_t &b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// Value of lane (lane ^ S) for S in {1, 2, 4, 8, 16, 32}, without the LDS crossbar: DPP quad permutes,
+// half-row mirror, row rotate, or a permlane swap.
+template <int S>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
+  if constexpr (S == 1) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (S == 2) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (S == 4) {  // i ^ 4 = (i ^ 7) ^ 3: half-row mirror, then quad_perm [3,2,1,0]
+    const uint32_t m = __builtin_amdgcn_update_dpp(0u, x, 0x141, 0xF, 0xF, false);
+    return __builtin_amdgcn_update_dpp(0u, m, 0x1B, 0xF, 0xF, false);
+  } else if constexpr (S == 8) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (S == 16) {  // rows (0,1), (2,3) trade: even rows read the second result
+    uint32_t a = x, b = x;
+    permlane16_swap(a, b);
+    return ((__lane_id() >> 4) & 1) ? a : b;
+  } else {  // S == 32: rows (0,2), (1,3) trade
+    uint32_t a = x, b = x;
+    permlane32_swap(a, b);
+    return (__lane_id() >> 5) ? a : b;
+  }
+}
+
 }  // namespace ks

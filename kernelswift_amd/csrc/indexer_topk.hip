@@ -7,9 +7,11 @@
 //
 // One 1024-lane workgroup per row.  The row is read once into registers (column j*1024 + lane),
 // converted to order-preserving uint32 keys.  A 3-pass LDS radix select (11 + 11 + 10 bits) finds the
-// k-th largest key K*; keys > K* are collected unordered, keys == K* are collected in column order
-// (ordered block scan) only when more of them exist than are needed; the k winners are then bitonic
-// sorted in LDS on the 64-bit composite (key, ~column), which is exactly (score desc, column asc).
+// k-th largest key K*; keys > K* are collected unordered (slots from a block scan), keys == K* are collected
+// in column order (ordered block scan) only when more of them exist than are needed.  The k winners are
+// then bitonic-sorted (descending) on the 64-bit composite (key, ~column), which is exactly (score desc,
+// column asc); the elements stay in registers, and only exchange distances between 64 and the number of
+// active threads go through LDS, so the network costs one barrier per such stage instead of per stage.
 //
 // Causal rows: columns >= limit = (start_pos + s + 1) / ratio are -inf by definition of the masked
 // scores (baseline/indexer.py:185-193), so they are never read: the valid prefix is selected and, when
@@ -54,7 +56,6 @@ struct SelShared {
   uint32_t digit;
   uint32_t k_rem;
   uint32_t bucket_count;
-  uint32_t n_gt;
 };
 
 // One radix pass: histogram of digit (key >> shift) & (nbins-1) among keys whose bits above the
@@ -95,12 +96,112 @@ __device__ __forceinline__ void radix_pass(const uint32_t (&key)[KPT], uint32_t 
   __syncthreads();
 }
 
+// Post-processing of one selected column (baseline/indexer.py:198-206) and its store.
+__device__ __forceinline__ void store_index(void *out, int out_i64, int64_t at, int64_t col, int causal, int64_t limit,
+                                            int64_t offset) {
+  const int64_t v = (causal && col >= limit) ? int64_t(-1) : col + offset;
+  if (out_i64) {
+    static_cast<int64_t *>(out)[at] = v;
+  } else {
+    static_cast<int32_t *>(out)[at] = static_cast<int32_t>(v);
+  }
+}
+
+// One bitonic compare-exchange stage at distance S < 64 (partner in the same wave).
+template <int E, int S>
+__device__ __forceinline__ void wave_stage(uint64_t (&v)[E], int NT, int size) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int e = r * NT + tid;
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v[r]), S, 64);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v[r] >> 32), S, 64);
+    const uint64_t pv = (static_cast<uint64_t>(hi) << 32) | lo;
+    const bool keep_max = ((e & size) == 0) == ((e & S) == 0);
+    v[r] = keep_max ? (v[r] > pv ? v[r] : pv) : (v[r] > pv ? pv : v[r]);
+  }
+}
+
+// Bitonic sort (descending) of the P composites cand[0..k_sel) (absent = 0 sorts last) and store of the
+// first k_sel in order.  Element e = r*NT + tid lives in registers; compare-exchange partners at distance
+// >= NT are in the same thread, at distance < 64 in the same wave (shuffles); only distances in between go
+// through LDS (cand[0..2P) as two alternating exchange buffers: one barrier per such stage).
+template <int E>
+__device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, int k, void *out, int out_i64,
+                               int causal, int64_t limit, int64_t offset) {
+  const int tid = threadIdx.x;
+  const int NT = P / E < 64 ? 64 : P / E;  // active threads (at least one wave)
+  const bool act = tid < NT;
+  uint64_t v[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int e = r * NT + tid;
+    v[r] = (act && e < k_sel) ? cand[e] : 0ull;
+  }
+  __syncthreads();  // the candidates are in registers; LDS becomes the exchange area
+  int phase = 0;
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= NT) {  // partner in this thread
+        const int rs = stride / NT;
+#pragma unroll
+        for (int r = 0; r < E; ++r) {
+          if ((r & rs) == 0) {
+            const int e = r * NT + tid;
+            const uint64_t a = v[r], c = v[r | rs];
+            const uint64_t hi = a > c ? a : c, lo = a > c ? c : a;
+            const bool desc = (e & size) == 0;
+            v[r] = desc ? hi : lo;
+            v[r | rs] = desc ? lo : hi;
+          }
+        }
+      } else if (stride >= 64) {  // partner in another wave
+        uint64_t *xb = cand + (phase & 1) * P;
+        ++phase;
+        if (act) {
+#pragma unroll
+          for (int r = 0; r < E; ++r) xb[r * NT + tid] = v[r];
+        }
+        __syncthreads();
+        if (act) {
+#pragma unroll
+          for (int r = 0; r < E; ++r) {
+            const int e = r * NT + tid;
+            const uint64_t pv = xb[e ^ stride];
+            const bool keep_max = ((e & size) == 0) == ((e & stride) == 0);
+            v[r] = keep_max ? (v[r] > pv ? v[r] : pv) : (v[r] > pv ? pv : v[r]);
+          }
+        }
+      } else {  // partner in this wave
+        switch (stride) {
+          case 1: wave_stage<E, 1>(v, NT, size); break;
+          case 2: wave_stage<E, 2>(v, NT, size); break;
+          case 4: wave_stage<E, 4>(v, NT, size); break;
+          case 8: wave_stage<E, 8>(v, NT, size); break;
+          case 16: wave_stage<E, 16>(v, NT, size); break;
+          default: wave_stage<E, 32>(v, NT, size); break;
+        }
+      }
+    }
+  }
+  if (act) {
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const int e = r * NT + tid;
+      if (e < k_sel) {
+        const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[r] & 0xFFFFFFFFull));
+        store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+      }
+    }
+  }
+}
+
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__restrict__ scores, int64_t ld,
                                                                 int64_t S, int T, int k, int causal,
                                                                 int64_t start_pos, int ratio, int64_t offset,
-                                                                void *__restrict__ out, int out_i64, int P) {
-  extern __shared__ uint64_t cand[];  // P composites
+                                                                void *__restrict__ out, int out_i64) {
+  extern __shared__ uint64_t cand[];  // 2P composites: candidates, then the sort's exchange buffers
   __shared__ SelShared sh;
   const int64_t row = blockIdx.x;
   const int64_t s = row % S;
@@ -120,11 +221,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     const int col = j * kTopkThreads + tid;
     key[j] = col < n_valid ? score_key(src[col]) : 0u;
   }
-  for (int i = tid; i < P; i += kTopkThreads) cand[i] = 0ull;
-  if (tid == 0) {
-    sh.k_rem = static_cast<uint32_t>(k_sel);
-    sh.n_gt = 0;
-  }
+  if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
   __syncthreads();
 
   if (k_sel > 0) {
@@ -139,15 +236,17 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     const uint32_t eq_total = sh.bucket_count;  // how many keys == K* exist
     const uint32_t n_gt = static_cast<uint32_t>(k_sel) - take_eq;
 
-    // ---- collect keys > K* (unordered) and, if all of them are taken, keys == K*
+    // ---- collect keys > K* (unordered) and, if all of them are taken, keys == K*: slots from a block scan
+    uint32_t ntake = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) ntake += (key[j] > kstar || (key[j] == kstar && take_eq == eq_total)) ? 1u : 0u;
+    uint32_t pos = block_inclusive_scan(ntake, sh.wsum) - ntake;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       const uint32_t kk = key[j];
-      const bool take = kk > kstar || (kk == kstar && take_eq == eq_total);
-      if (take) {
-        const uint32_t pos = atomicAdd(&sh.n_gt, 1u);
+      if (kk > kstar || (kk == kstar && take_eq == eq_total)) {
         const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
-        cand[pos] = (static_cast<uint64_t>(kk) << 32) | static_cast<uint64_t>(~col);
+        cand[pos++] = (static_cast<uint64_t>(kk) << 32) | static_cast<uint64_t>(~col);
       }
     }
     // ---- ties at K*: the take_eq lowest columns, found with an ordered scan (column = j*1024 + lane)
@@ -171,50 +270,31 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     }
     __syncthreads();
 
-    // ---- bitonic sort of P composites, descending
-    for (int size = 2; size <= P; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int i = tid; i < (P >> 1); i += kTopkThreads) {
-          const int a = 2 * stride * (i / stride) + (i % stride);
-          const int b = a + stride;
-          const uint64_t va = cand[a], vb = cand[b];
-          const bool desc = (a & size) == 0;
-          if (desc ? (va < vb) : (va > vb)) {
-            cand[a] = vb;
-            cand[b] = va;
-          }
-        }
-        __syncthreads();
-      }
+    // ---- bitonic sort of the winners (descending composite), P = pow2 >= k_sel elements, E per thread
+    int P = 2;
+    while (P < k_sel) P <<= 1;
+    if (P <= kTopkThreads) {
+      sort_and_store<1>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+    } else if (P == 2 * kTopkThreads) {
+      sort_and_store<2>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+    } else {
+      sort_and_store<4>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
     }
   }
 
-  // ---- post-processing and store (baseline/indexer.py:198-206)
-  for (int j = tid; j < k; j += kTopkThreads) {
-    int64_t col;
-    if (j < k_sel) {
-      col = static_cast<int64_t>(~static_cast<uint32_t>(cand[j] & 0xFFFFFFFFull));
-    } else {
-      col = static_cast<int64_t>(n_valid) + (j - k_sel);  // masked columns, ascending (-inf ties)
-    }
-    const int64_t v = (causal && col >= limit) ? int64_t(-1) : col + offset;
-    if (out_i64) {
-      static_cast<int64_t *>(out)[row * k + j] = v;
-    } else {
-      static_cast<int32_t *>(out)[row * k + j] = static_cast<int32_t>(v);
-    }
-  }
+  // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order)
+  for (int j = k_sel + tid; j < k; j += kTopkThreads)
+    store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
 }
 
 template <int KPT>
 int launch_topk(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal, int64_t start_pos,
                 int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream) {
-  int P = 1;
+  int P = 2;
   while (P < k) P <<= 1;
-  if (P < 2) P = 2;
-  const size_t shmem = static_cast<size_t>(P) * sizeof(uint64_t);
+  const size_t shmem = static_cast<size_t>(2 * P) * sizeof(uint64_t);  // candidates, then the exchange buffers
   hipLaunchKernelGGL(topk_rows_kernel<KPT>, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, stream,
-                     scores, ld, S, T, k, causal, start_pos, ratio, offset, out, out_i64, P);
+                     scores, ld, S, T, k, causal, start_pos, ratio, offset, out, out_i64);
   KS_CHECK_LAUNCH("topk_rows_kernel");
   return KS_OK;
 }

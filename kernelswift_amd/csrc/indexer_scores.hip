@@ -57,6 +57,10 @@ struct ScoresLds {
   uint4 k[kKR * KD / 8];             // swizzled key block of this workgroup (KD / 8 16-byte chunks per key)
   KeyEntry ent[kQW][kEntCap];
   uint16_t dots[kQW][kDotCap];       // flattened near-tie dots: (pair << 4) | slot, pair = 4 entry + group
+  int32_t kspan[kKR];                // row statistics of the key block and of each wave's query rows, for
+  float knorm[kKR];                  // the exact recomputation (no global loads there)
+  int32_t qspan[kQW][64];
+  float qnorm[kQW][64];
   float red[kQW];
 };
 
@@ -216,24 +220,41 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int nd = min(kDotCap, ndots - base);
     const int dq = lane >> 2, sub = lane & 3;
+    // head of list entry i: slot s of pair (entry, group gg) is head 16 (s >> 2) + 4 gg + (s & 3)
+    auto dot_head = [&](int i) -> int {
+      const uint32_t de = D[i];
+      return 16 * ((de & 15) >> 2) + 4 * ((de >> 4) & 3) + (de & 3);
+    };
+    uint4 qcur[kLC];
+    {
+      const int h0 = dot_head(min(dq, nd - 1));
+      const uint4 *qp0 = reinterpret_cast<const uint4 *>(q + (qrow0 + h0) * KD + (KD / 4) * sub);
+#pragma unroll
+      for (int c = 0; c < kLC; ++c) qcur[c] = qp0[c];
+    }
     for (int b0 = 0; b0 < nd; b0 += 16) {
       const int di = min(b0 + dq, nd - 1);  // idle quads repeat the last dot (result identical)
       const uint32_t de = D[di];
       const int pr = static_cast<int>(de >> 4), slot = static_cast<int>(de & 15);
       const int e = pr >> 2, gg = pr & 3;
       const int h = 16 * (slot >> 2) + 4 * gg + (slot & 3);
-      const int64_t hrow = qrow0 + h;
       const int key = min(E[e].key, T - 1);  // entries only hold keys < T; clamp defensively
-      const int64_t krow = kbrow0 + key;
       const int kl = key - kb0;               // row of the key in the LDS block
-      const uint4 *qp = reinterpret_cast<const uint4 *>(q + hrow * KD + (KD / 4) * sub);
+      const uint4 *qp = reinterpret_cast<const uint4 *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
       uint4 qa[kLC], ka[kLC];
 #pragma unroll
       for (int c = 0; c < kLC; ++c) {
-        qa[c] = qp[c];
+        qa[c] = qcur[c];
         ka[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
       }
-      const int span_sum = qsp[hrow] + ksp[krow];
+      // the next pass's q rows are in flight while this pass computes
+      if (b0 + 16 < nd) {
+        const int hn = dot_head(min(b0 + 16 + dq, nd - 1));
+        const uint4 *qpn = reinterpret_cast<const uint4 *>(q + (qrow0 + hn) * KD + (KD / 4) * sub);
+#pragma unroll
+        for (int c = 0; c < kLC; ++c) qcur[c] = qpn[c];
+      }
+      const int span_sum = L.qspan[wave][h] + L.kspan[kl];
       uint16_t r;
       if (__builtin_amdgcn_ballot_w64(span_sum > 52) == 0ull) {
         // every partial sum is a multiple of the smallest product LSB and below 2^53 of it: exact doubles
@@ -252,7 +273,7 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
         r = round_dir_to_bf16(quad_sum_f64(a0 + a1), 0);
       } else {
         // wide dynamic range: products above / below 2^(top - 38) accumulate separately, each exactly
-        const int top_sum = frexp_exp(qn[hrow]) + frexp_exp(kn[krow]);
+        const int top_sum = frexp_exp(L.qnorm[wave][h]) + frexp_exp(L.knorm[kl]);
         const bool split = span_sum > 52;
         const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
         double hi = 0.0, lo = 0.0;
@@ -329,12 +350,21 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
 
   // max key norm over this workgroup's range (the error bound uses it for every key)
   float knm = 0.f;
-  for (int i = tid; i < nk; i += kThreads) knm = fmaxf(knm, kn[krow0 + i]);
+  for (int i = tid; i < kKR; i += kThreads) {
+    const float nv = i < nk ? kn[krow0 + i] : 0.f;
+    L.knorm[i] = nv;
+    L.kspan[i] = i < nk ? ksp[krow0 + i] : 0;
+    knm = fmaxf(knm, nv);
+  }
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
   if (lane == 0) L.red[wave] = knm;
   // query rows as MFMA A-fragments
   const int64_t qrow0 = (b * S + (s_ok ? s : 0)) * H;
+  if (lane < H) {
+    L.qspan[wave][lane] = qsp[qrow0 + lane];
+    L.qnorm[wave][lane] = qn[qrow0 + lane];
+  }
   uint4 qa[HT][KD / 32];
 #pragma unroll
   for (int m = 0; m < HT; ++m)

@@ -1,10 +1,12 @@
-// Fused indexer entry: RoPE (q at start_pos + s, k at t) -> row statistics -> exact scores -> exact top-k.
+// Fused indexer entry: RoPE + row statistics of q and k (one launch) -> exact scores -> exact top-k.
 //
 // Semantics of baseline/indexer.py:161-206 after the two projections (which stay in the caller):
 // RoPE on the configured segment of q (and k), score = sum_h w_h * relu(bf16(q_h . k)), causal mask,
 // sorted top-k with lowest-index ties, -1 / +offset post-processing.  Replaces the reference's three-op
 // sequence rope_inplace -> fused_qk_reduce -> topk_mask (optimized/indexer_project/indexer.py:197-222).
-// All intermediates live in the caller's workspace; inputs are never modified.
+// All intermediates live in the caller's workspace; inputs are never modified.  RoPE stays a pass of its
+// own: done inside the score kernel it would be repeated by every workgroup that reads a row (S/8 times
+// per key row), which measured twice as slow as the separate pass.
 #include "common.h"
 #include "indexer_common.h"
 
@@ -81,27 +83,12 @@ extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, i
                "ks_indexer: workspace of %zu bytes required, %zu given", ws.bytes, workspace_bytes);
   KS_CHECK_ARG(ks::aligned(workspace, 256), "ks_indexer: workspace must be 256-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int rs = static_cast<int>(rope_start), rd = static_cast<int>(rope_dim);
-
-  // q: rotate at positions start_pos + s into the workspace copy, with row statistics
-  int rc = ks::launch_rope_rows(q, ws.q_rot, freqs, B * S * H, static_cast<int>(D), static_cast<int>(H), S, start_pos, rs, rd,
-                                ws.q_norm, ws.q_span, st);
+  const int rd = static_cast<int>(rope_dim);
+  // q rows at positions start_pos + s; k rows of every batch (stride k_batch_stride) at positions t
+  const ks::RowJob qjob{q, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H, H, S, start_pos, rd};
+  const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
+  int rc = ks::launch_rope_rows(qjob, kjob, freqs, static_cast<int>(D), static_cast<int>(rope_start), st);
   if (rc != KS_OK) return rc;
-  // k: rotate at positions t (or copy) per batch, with row statistics
-  const int rdk = rope_k ? rd : 0;
-  for (int64_t b = 0; b < B; ++b) {
-    rc = ks::launch_rope_rows(k + b * k_batch_stride * D, ws.k_rot + b * T * D, freqs, T, static_cast<int>(D), 1, T, 0, rs, rdk,
-                              ws.k_norm + b * T, ws.k_span + b * T, st);
-    if (rc != KS_OK) return rc;
-    if (k_batch_stride == T) {  // contiguous batches: the first launch may cover all of them
-      if (b == 0 && B > 1) {
-        rc = ks::launch_rope_rows(k + T * D, ws.k_rot + T * D, freqs, (B - 1) * T, static_cast<int>(D), 1, T, 0, rs, rdk,
-                                  ws.k_norm + T, ws.k_span + T, st);
-        if (rc != KS_OK) return rc;
-      }
-      break;
-    }
-  }
   rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, w_bf16 ? 1 : 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span,
                                  ws.scores, B, S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC,
                                  nullptr, st);

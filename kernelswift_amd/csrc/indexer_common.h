@@ -16,8 +16,66 @@ __host__ __device__ inline int bf16_lsb_exponent(uint16_t b) {
 // 0.68 (N(0,1) data) and 1.52 (heavy-tailed x^3 data) in the same units; 3.0 leaves >= 2x margin.
 constexpr float kScoreBoundC = 3.0f;
 
-int launch_rope_rows(const uint16_t *src, uint16_t *dst, const float *freqs, int64_t rows, int D, int H, int64_t S,
-                     int64_t pos0, int rope_start, int rope_dim, float *norm, int32_t *span, hipStream_t stream);
+// Canonical RoPE of one 16-byte chunk (4 consecutive pairs (2j, 2j+1)) with (cos, sin) pairs cs[0..3]:
+// y0 = fl(x0*c) - fl(x1*s), y1 = fl(x0*s) + fl(x1*c), then RNE to bf16 (the library is built with
+// -ffp-contract=off, so the products round separately, exactly like the CPU oracle).
+__device__ __forceinline__ uint4 rope_chunk(uint4 v, const float2 *__restrict__ cs) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float x0 = bf16_to_f32(static_cast<uint16_t>(w[p] & 0xFFFFu));
+    const float x1 = bf16_to_f32(static_cast<uint16_t>(w[p] >> 16));
+    const float2 t = cs[p];
+    const float y0 = x0 * t.x - x1 * t.y;
+    const float y1 = x0 * t.y + x1 * t.x;
+    w[p] = static_cast<uint32_t>(f32_to_bf16_rne(y0)) | (static_cast<uint32_t>(f32_to_bf16_rne(y1)) << 16);
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Row-statistics contributions of one chunk: sum of squares (each square is exact: 8-bit significands)
+// and the smallest LSB exponent of its nonzero elements (1 << 20 when all are zero).
+__device__ __forceinline__ void chunk_stats(uint4 v, float &ss, int &lsb) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint16_t b = static_cast<uint16_t>(h ? (w[p] >> 16) : (w[p] & 0xFFFFu));
+      const float f = bf16_to_f32(b);
+      ss += f * f;
+      if ((b & 0x7FFFu) != 0) lsb = min(lsb, bf16_lsb_exponent(b));
+    }
+  }
+}
+
+// Norm upper bound and span from a row's sum of squares and smallest LSB exponent: an fp32 sum of at most
+// 128 exact squares has relative error < 2^-16 and sqrt adds < 1 ulp; the 2^-12 pad covers both.
+__device__ __forceinline__ void row_norm_span(float ss, int lsb, float &norm, int32_t &span) {
+  norm = ss > 0.f ? sqrtf(ss) * (1.0f + 0x1p-12f) : 0.f;
+  int top = 0;
+  if (norm > 0.f) frexpf(norm, &top);  // norm < 2^top
+  span = norm > 0.f ? top - lsb : 0;
+}
+
+// One set of bf16 rows for the RoPE / row-statistics launch.  Row r (0 <= r < rows) of the set is
+// source row (r / rows_per_batch) * src_batch_rows + r % rows_per_batch and destination row r; its
+// position is pos0 + ((r % rows_per_batch) / H) % S.  dst may equal src (in place) or be null (statistics
+// only); norm/span (both or neither) receive the row statistics at index r.
+struct RowJob {
+  const uint16_t *src;
+  uint16_t *dst;
+  float *norm;
+  int32_t *span;
+  int64_t rows, rows_per_batch, src_batch_rows;
+  int64_t H, S, pos0;
+  int rope_dim;  // 0: copy / statistics only
+};
+
+// Both jobs in one launch (job1.rows may be 0); rows of D in {64, 128} for statistics, any multiple of 8
+// otherwise.  Rotated dims [rope_start, rope_start + job.rope_dim), freqs = (cos, sin) per position.
+int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
+                     hipStream_t stream);
 
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,

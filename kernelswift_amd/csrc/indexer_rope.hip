@@ -18,83 +18,77 @@
 namespace ks {
 namespace {
 
-__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float &y0, float &y1) {
-  y0 = x0 * c - x1 * s;
-  y1 = x0 * s + x1 * c;
-}
-
+// One thread per 16-byte chunk; blocks [0, blocks0) take job 0 and the rest job 1 (a uniform choice, so
+// each field is selected separately from the kernel arguments, never through a pointer to them).
 template <bool STATS>
-__global__ __launch_bounds__(256) void rope_rows_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst,
-                                                       const float *__restrict__ freqs, int64_t rows, int D, int H,
-                                                       int64_t S, int64_t pos0, int rope_start, int rope_dim,
-                                                       float *__restrict__ norm, int32_t *__restrict__ span) {
-  const int chunks_per_row = D / 8;
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t row = c / chunks_per_row;
-  const int j = static_cast<int>(c % chunks_per_row);
+__global__ __launch_bounds__(256) void rope_rows_kernel(RowJob j0, RowJob j1, uint32_t blocks0,
+                                                       const float *__restrict__ freqs, int D, int rope_start) {
+  const bool second = blockIdx.x >= blocks0;
+#define KS_PICK(f) (second ? j1.f : j0.f)
+  const uint16_t *__restrict__ src = KS_PICK(src);
+  uint16_t *__restrict__ dst = KS_PICK(dst);
+  const uint32_t rows = static_cast<uint32_t>(KS_PICK(rows));
+  const uint32_t rpb = static_cast<uint32_t>(KS_PICK(rows_per_batch));
+  const int64_t sbr = KS_PICK(src_batch_rows);
+  const uint32_t H = static_cast<uint32_t>(KS_PICK(H)), S = static_cast<uint32_t>(KS_PICK(S));
+  const int64_t pos0 = KS_PICK(pos0);
+  const int rope_dim = KS_PICK(rope_dim);
+#undef KS_PICK
+  const uint32_t blk = second ? blockIdx.x - blocks0 : blockIdx.x;
+  const uint32_t cpr = static_cast<uint32_t>(D) / 8;  // chunks per row
+  const uint32_t c = blk * 256u + threadIdx.x;         // < 2^31 (checked on the host)
+  const uint32_t row = c / cpr, j = c % cpr;
   const bool live = row < rows;
+  const uint32_t rb = live ? row / rpb : 0, rr = live ? row % rpb : 0;
+  const int64_t srow = static_cast<int64_t>(rb) * sbr + rr;
   uint4 v = make_uint4(0, 0, 0, 0);
-  if (live) v = *reinterpret_cast<const uint4 *>(src + row * D + 8 * j);
-  const int e0 = 8 * j;
+  if (live) v = *reinterpret_cast<const uint4 *>(src + srow * D + 8 * j);
+  const int e0 = 8 * static_cast<int>(j);
   if (live && rope_dim > 0 && e0 >= rope_start && e0 < rope_start + rope_dim) {
-    const int64_t s = (row / H) % S;
-    const float2 *cs = reinterpret_cast<const float2 *>(freqs) + (pos0 + s) * (rope_dim / 2) + (e0 - rope_start) / 2;
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float x0 = bf16_to_f32(static_cast<uint16_t>(w[p] & 0xFFFFu));
-      const float x1 = bf16_to_f32(static_cast<uint16_t>(w[p] >> 16));
-      const float2 t = cs[p];
-      float y0, y1;
-      rope_pair(x0, x1, t.x, t.y, y0, y1);
-      w[p] = static_cast<uint32_t>(f32_to_bf16_rne(y0)) | (static_cast<uint32_t>(f32_to_bf16_rne(y1)) << 16);
-    }
-    v = make_uint4(w[0], w[1], w[2], w[3]);
+    const int64_t pos = pos0 + (rr / H) % S;
+    const float2 *cs = reinterpret_cast<const float2 *>(freqs) + pos * (rope_dim / 2) + (e0 - rope_start) / 2;
+    v = rope_chunk(v, cs);
   }
-  if (live && dst != nullptr) *reinterpret_cast<uint4 *>(dst + row * D + 8 * j) = v;
+  if (live && dst != nullptr) *reinterpret_cast<uint4 *>(dst + static_cast<int64_t>(row) * D + 8 * j) = v;
   if constexpr (STATS) {
     // D in {64, 128}: the D/8 lanes of a row are an aligned group of the wave.
     float ss = 0.f;
     int lsb = 1 << 20;
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint16_t b = static_cast<uint16_t>(h ? (w[p] >> 16) : (w[p] & 0xFFFFu));
-        const float f = bf16_to_f32(b);
-        ss += f * f;  // each square is exact (8-bit significand)
-        if ((b & 0x7FFFu) != 0) lsb = min(lsb, bf16_lsb_exponent(b));
-      }
-    }
-    for (int m = 1; m < chunks_per_row; m <<= 1) {
+    chunk_stats(v, ss, lsb);
+    for (uint32_t m = 1; m < cpr; m <<= 1) {
       ss += __shfl_xor(ss, m, 64);
       lsb = min(lsb, __shfl_xor(lsb, m, 64));
     }
     if (live && j == 0) {
-      // fp32 sum of <= 128 squares: relative error < 2^-16; sqrt adds < 1 ulp; pad by 2^-12.
-      const float nrm = ss > 0.f ? sqrtf(ss) * (1.0f + 0x1p-12f) : 0.f;
-      norm[row] = nrm;
-      int top = 0;
-      if (nrm > 0.f) frexpf(nrm, &top);  // nrm < 2^top
-      span[row] = nrm > 0.f ? top - lsb : 0;
+      float *norm = second ? j1.norm : j0.norm;
+      int32_t *span = second ? j1.span : j0.span;
+      row_norm_span(ss, lsb, norm[row], span[row]);
     }
   }
 }
 
 }  // namespace
 
-int launch_rope_rows(const uint16_t *src, uint16_t *dst, const float *freqs, int64_t rows, int D, int H, int64_t S,
-                     int64_t pos0, int rope_start, int rope_dim, float *norm, int32_t *span, hipStream_t stream) {
-  const int64_t chunks = rows * (D / 8);
-  if (chunks == 0) return KS_OK;
-  const int64_t blocks = ceil_div(chunks, 256);
-  if (norm != nullptr) {
-    hipLaunchKernelGGL(rope_rows_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, src, dst,
-                       freqs, rows, D, H, S, pos0, rope_start, rope_dim, norm, span);
+int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
+                     hipStream_t stream) {
+  const int64_t c0 = job0.rows * (D / 8), c1 = job1.rows * (D / 8);
+  KS_CHECK_ARG(c0 + c1 + 512 < (int64_t(1) << 31), "rope rows: %lld + %lld chunks exceed the 32-bit grid",
+               (long long)c0, (long long)c1);
+  KS_CHECK_ARG(job0.rows_per_batch >= 1 && job1.rows_per_batch >= 1 && job0.H >= 1 && job1.H >= 1 &&
+                   job0.S >= 1 && job1.S >= 1,
+               "rope rows: empty batch, head or position extent");
+  const int64_t b0 = ceil_div(c0, 256), b1 = ceil_div(c1, 256);
+  if (b0 + b1 == 0) return KS_OK;
+  const bool stats = job0.norm != nullptr;
+  KS_CHECK_ARG((job1.rows == 0 || (job1.norm != nullptr) == stats) && (!stats || D == 64 || D == 128),
+               "rope rows: statistics need D in {64, 128} and both jobs alike");
+  const dim3 grid(static_cast<unsigned>(b0 + b1));
+  if (stats) {
+    hipLaunchKernelGGL(rope_rows_kernel<true>, grid, dim3(256), 0, stream, job0, job1,
+                       static_cast<uint32_t>(b0), freqs, D, rope_start);
   } else {
-    hipLaunchKernelGGL(rope_rows_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, src, dst,
-                       freqs, rows, D, H, S, pos0, rope_start, rope_dim, norm, span);
+    hipLaunchKernelGGL(rope_rows_kernel<false>, grid, dim3(256), 0, stream, job0, job1,
+                       static_cast<uint32_t>(b0), freqs, D, rope_start);
   }
   KS_CHECK_LAUNCH("rope_rows_kernel");
   return KS_OK;
@@ -118,8 +112,9 @@ extern "C" int ks_rope_inplace(uint16_t *x, const float *freqs, int64_t B, int64
   if (rows == 0 || rope_dim == 0) return KS_OK;
   KS_CHECK_ARG(x != nullptr && freqs != nullptr, "ks_rope_inplace: null pointer");
   KS_CHECK_ARG(ks::aligned(x, 16) && ks::aligned(freqs, 8), "ks_rope_inplace: x must be 16-byte aligned");
-  return ks::launch_rope_rows(x, x, freqs, rows, static_cast<int>(D), static_cast<int>(H), S, pos0,
-                              static_cast<int>(rope_start), static_cast<int>(rope_dim), nullptr, nullptr,
+  const ks::RowJob job{x, x, nullptr, nullptr, rows, rows, rows, H, S, pos0, static_cast<int>(rope_dim)};
+  const ks::RowJob none{nullptr, nullptr, nullptr, nullptr, 0, 1, 0, 1, 1, 0, 0};
+  return ks::launch_rope_rows(job, none, freqs, static_cast<int>(D), static_cast<int>(rope_start),
                               static_cast<hipStream_t>(stream));
 }
 
@@ -131,6 +126,7 @@ extern "C" int ks_indexer_row_stats(const uint16_t *x, int64_t rows, int64_t D, 
   if (rows == 0) return KS_OK;
   KS_CHECK_ARG(x && norm && span, "ks_indexer_row_stats: null pointer");
   KS_CHECK_ARG(ks::aligned(x, 16), "ks_indexer_row_stats: x must be 16-byte aligned");
-  return ks::launch_rope_rows(x, nullptr, nullptr, rows, static_cast<int>(D), 1, 1, 0, 0, 0, norm, span,
-                              static_cast<hipStream_t>(stream));
+  const ks::RowJob job{x, nullptr, norm, span, rows, rows, rows, 1, 1, 0, 0};
+  const ks::RowJob none{nullptr, nullptr, nullptr, nullptr, 0, 1, 0, 1, 1, 0, 0};
+  return ks::launch_rope_rows(job, none, nullptr, static_cast<int>(D), 0, static_cast<hipStream_t>(stream));
 }

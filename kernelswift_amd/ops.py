@@ -27,10 +27,10 @@ def _check(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
-def _on_gpu(*ts: torch.Tensor) -> None:
+def _on_gpu(*ts: torch.Tensor, contiguous: bool = True) -> None:
     for t in ts:
         _check(t.is_cuda, "tensors must be on the GPU (there is no CPU path)")
-        _check(t.is_contiguous(), "tensors must be contiguous")
+        _check(not contiguous or t.is_contiguous(), "tensors must be contiguous")
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -157,7 +157,8 @@ def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Opti
     Returns [B, S, min(k_top, T)] int32 (default) or int64."""
     _check(q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16, "q and k must be bfloat16")
     _check(weights.dtype in (torch.float32, torch.bfloat16), "weights must be float32 or bfloat16")
-    _on_gpu(q, k, weights)
+    _on_gpu(q, weights)
+    _on_gpu(k, contiguous=False)  # batch-strided rows allowed, checked below
     _check(q.dim() == 4 and k.dim() == 3 and weights.dim() == 3, "q [b,s,h,d], k [b,t,d], weights [b,s,h]")
     B, S, H, D = q.shape
     _check(k.shape[0] >= B and k.shape[2] == D, "k shape mismatch")

@@ -44,7 +44,7 @@ def test_host_validation_without_gpu():
 
 def test_workspace_queries():
     lib = _lib.load()
-    assert lib.ks_indexer_workspace_size(1, 128, 64, 128, 4096) >= 128 * 64 * 128 * 2 + 128 * 4096 * 4
+    assert lib.ks_indexer_workspace_size(1, 128, 64, 128, 4096) >= 128 * 4096 * 4  # the fp32 score matrix
     # many queries -> one range per query -> no workspace
     assert lib.ks_sparse_attn_workspace_size(8, 2600, 64, 128, 128, 16) == 0
     assert lib.ks_sparse_attn_workspace_size(32, 1, 128, 576, 512, 2048) > 0

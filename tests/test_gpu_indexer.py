@@ -199,3 +199,58 @@ def test_indexer_baseline_semantics_ratio4_bf16_weights(device):
     torch.cuda.synchronize()
     want = oracle.indexer(_u16(q), _u16(k), _u16(w), tab.numpy(), 128, True, 0, 4, 9, 96, 32, False)
     np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def _indexer_vs_oracle(q, k, w, tab, k_top, causal, start_pos, ratio, offset, rs, rd, rope_k, T, cache_rows=None):
+    """ks_indexer (one RoPE/statistics launch over q and every batch's k, scores, top-k) vs the oracle.
+    cache_rows > T gives k as a batch-strided view of a larger cache (batch stride cache_rows rows)."""
+    B, S, H, D = q.shape
+    kd = k.to("cuda")
+    if cache_rows is not None:
+        cache = torch.zeros(B, cache_rows, D, dtype=torch.bfloat16, device="cuda")
+        cache[:, :T] = kd
+        kd = cache[:, :T]
+    got = ops.indexer(q.to("cuda"), kd, w.to("cuda"), tab.to("cuda"), k_top, causal, start_pos, ratio, offset, rs,
+                      rd, rope_k)
+    torch.cuda.synchronize()
+    wn = _u16(w) if w.dtype == torch.bfloat16 else w.numpy()
+    want = oracle.indexer(_u16(q), _u16(k), wn, tab.numpy(), k_top, causal, start_pos, ratio, offset, rs, rd, rope_k)
+    np.testing.assert_array_equal(got.cpu().numpy().astype(np.int64), want)
+
+
+@pytest.mark.parametrize("D,rs,rd,rope_k,w_bf16,cache_rows", [(128, 0, 64, True, False, 700),
+                                                              (64, 32, 32, False, True, None),
+                                                              (128, 64, 64, True, True, 301),
+                                                              (128, 0, 0, False, False, 512)])
+def test_indexer_prep_layouts(device, D, rs, rd, rope_k, w_bf16, cache_rows):
+    g = torch.Generator().manual_seed(D + rs + rd)
+    B, S, H, T = 2, 9, 64, 300
+    q = torch.randn(B, S, H, D, generator=g).bfloat16()
+    k = torch.randn(B, T, D, generator=g).bfloat16()
+    w = torch.randn(B, S, H, generator=g) / 8
+    if w_bf16:
+        w = w.bfloat16()
+    tab = workloads.freqs_table(max(rd, 2), 512)
+    print(f"[case] indexer D={D} rope=[{rs},{rs + rd}) rope_k={rope_k} w_bf16={w_bf16} cache_rows={cache_rows}",
+          flush=True)
+    _indexer_vs_oracle(q, k, w, tab, 64, True, T - S, 1, 0, rs, rd, rope_k, T, cache_rows)
+
+
+@pytest.mark.parametrize("dist", ["scaled", "tiny", "midpoints"])
+def test_indexer_adversarial(device, dist):
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(1, 16, 64, 128, generator=g)
+    k = torch.randn(1, 1024, 128, generator=g)
+    if dist == "scaled":
+        q = q * torch.exp2(torch.randint(-8, 9, (1, 16, 64, 1), generator=g).float())
+        k = k * torch.exp2(torch.randint(-8, 9, (1, 1024, 1), generator=g).float())
+    elif dist == "tiny":
+        q = q * torch.exp2(torch.randint(-30, 1, q.shape, generator=g).float())
+    else:  # integer inputs: many dots on exact bf16 midpoints before RoPE, many tied scores
+        q = torch.randint(-3, 4, q.shape, generator=g).float()
+        k = torch.randint(-3, 4, k.shape, generator=g).float()
+    q, k = q.bfloat16(), k.bfloat16()
+    w = torch.randn(1, 16, 64, generator=g) / 8
+    tab = workloads.freqs_table(64, 2048)
+    print(f"[case] indexer adversarial {dist}", flush=True)
+    _indexer_vs_oracle(q, k, w, tab, 256, True, 1024 - 16, 1, 0, 0, 64, True, 1024)

@@ -34,24 +34,36 @@ __device__ __forceinline__ uint32_t score_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP: row shifts by 1, 2, 4, 8 within each 16-lane
+// row, then the last lane of row 0 / row 2 broadcast into rows 1 / 3 and lane 31 into rows 2-3.  Lanes
+// whose DPP source is outside the row (or whose row is masked off) add 0.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 // Inclusive prefix sum over the 1024 lanes of the block (lane order).  `wsum` is kTopkWaves ints of LDS.
+// TRAIL: end with a barrier so that wsum may be rewritten at once; without it the caller must pass a
+// barrier before the next scan on the same wsum.
+template <bool TRAIL = true>
 __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t *wsum) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    uint32_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
+  v = wave_incl_scan(v);
   if (lane == 63) wsum[wave] = v;
   __syncthreads();
   uint32_t base = 0;
   for (int w = 0; w < wave; ++w) base += wsum[w];
-  __syncthreads();
+  if constexpr (TRAIL) __syncthreads();
   return v + base;
 }
 
 struct SelShared {
-  uint32_t hist[2048];
+  uint32_t hist[2][2048];  // pass p counts into hist[p & 1] while hist[(p + 1) & 1] is cleared
   uint32_t wsum[kTopkWaves];
   uint32_t digit;
   uint32_t k_rem;
@@ -59,28 +71,30 @@ struct SelShared {
 };
 
 // One radix pass: histogram of digit (key >> shift) & (nbins-1) among keys whose bits above the
-// digit equal `prefix` under `mask`; then locate the bucket holding the k_rem-th largest.
+// digit equal `prefix` under `mask`; then locate the bucket holding the k_rem-th largest.  hist[buf] is
+// zero on entry (cleared before the barrier that precedes the pass); hist[buf ^ 1] is cleared here for the
+// next pass (its last readers finished before that same barrier).
 template <int KPT>
 __device__ __forceinline__ void radix_pass(const uint32_t (&key)[KPT], uint32_t prefix, uint32_t mask, int shift,
-                                           int nbins, SelShared &sh) {
+                                           int nbins, SelShared &sh, int buf) {
   // k_rem must be read before the barrier that precedes this pass's single update of it
   const uint32_t k_rem = sh.k_rem;
-  for (int i = threadIdx.x; i < 2048; i += kTopkThreads) sh.hist[i] = 0;
-  __syncthreads();
+  uint32_t *hist = sh.hist[buf];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const uint32_t kk = key[j];
-    if (kk != 0 && (kk & mask) == prefix) atomicAdd(&sh.hist[(kk >> shift) & (nbins - 1)], 1u);
+    if (kk != 0 && (kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & (nbins - 1)], 1u);
   }
+  for (int i = threadIdx.x; i < 2048; i += kTopkThreads) sh.hist[buf ^ 1][i] = 0;
   __syncthreads();
   // Lane t owns bins hi = nbins-1-2t and lo = hi-1 (two bins per lane for 2048, one for 1024):
   // an inclusive lane-order scan is then a suffix sum over bins from the top.
   const int per = nbins / kTopkThreads;  // 2 or 1
   const int hi = nbins - 1 - per * static_cast<int>(threadIdx.x);
-  const uint32_t c_hi = sh.hist[hi];
-  const uint32_t c_lo = per == 2 ? sh.hist[hi - 1] : 0u;
+  const uint32_t c_hi = hist[hi];
+  const uint32_t c_lo = per == 2 ? hist[hi - 1] : 0u;
   const uint32_t mine = c_hi + c_lo;
-  const uint32_t incl = block_inclusive_scan(mine, sh.wsum);
+  const uint32_t incl = block_inclusive_scan<false>(mine, sh.wsum);  // the barrier below ends the pass
   const uint32_t excl = incl - mine;
   if (excl < k_rem && incl >= k_rem) {
     if (excl + c_hi >= k_rem) {
@@ -107,31 +121,36 @@ __device__ __forceinline__ void store_index(void *out, int out_i64, int64_t at, 
   }
 }
 
-// One bitonic compare-exchange stage at distance S < 64 (partner in the same wave).
+// One bitonic compare-exchange stage at distance S < 64: the partner (lane ^ S) is in the same wave and
+// its value arrives through DPP / permlane (no LDS).  A lane keeps the larger composite when it holds the
+// lower position of a descending pair or the upper position of an ascending one, so it takes the partner's
+// value exactly when (partner > own) == keep_max (on equality either value is the same).
 template <int E, int S>
 __device__ __forceinline__ void wave_stage(uint64_t (&v)[E], int NT, int size) {
   const int tid = threadIdx.x;
 #pragma unroll
   for (int r = 0; r < E; ++r) {
     const int e = r * NT + tid;
-    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v[r]), S, 64);
-    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v[r] >> 32), S, 64);
+    const uint32_t lo = lane_xor<S>(static_cast<uint32_t>(v[r]));
+    const uint32_t hi = lane_xor<S>(static_cast<uint32_t>(v[r] >> 32));
     const uint64_t pv = (static_cast<uint64_t>(hi) << 32) | lo;
     const bool keep_max = ((e & size) == 0) == ((e & S) == 0);
-    v[r] = keep_max ? (v[r] > pv ? v[r] : pv) : (v[r] > pv ? pv : v[r]);
+    v[r] = ((pv > v[r]) == keep_max) ? pv : v[r];
   }
 }
 
 // Bitonic sort (descending) of the P composites cand[0..k_sel) (absent = 0 sorts last) and store of the
 // first k_sel in order.  Element e = r*NT + tid lives in registers; compare-exchange partners at distance
-// >= NT are in the same thread, at distance < 64 in the same wave (shuffles); only distances in between go
-// through LDS (cand[0..2P) as two alternating exchange buffers: one barrier per such stage).
+// >= NT are in the same thread, at distance < 64 in the same wave (DPP / permlane, the six stages of a
+// merge step unrolled at compile time); only distances in between go through LDS (cand[0..2P) as two
+// alternating exchange buffers: one barrier per such stage).  Waves holding no elements only join the
+// barriers.
 template <int E>
 __device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, int k, void *out, int out_i64,
                                int causal, int64_t limit, int64_t offset) {
   const int tid = threadIdx.x;
   const int NT = P / E < 64 ? 64 : P / E;  // active threads (at least one wave)
-  const bool act = tid < NT;
+  const bool act = tid < NT;               // uniform per wave (NT is a multiple of 64)
   uint64_t v[E];
 #pragma unroll
   for (int r = 0; r < E; ++r) {
@@ -141,8 +160,9 @@ __device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, in
   __syncthreads();  // the candidates are in registers; LDS becomes the exchange area
   int phase = 0;
   for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= NT) {  // partner in this thread
+    int stride = size >> 1;
+    for (; stride >= NT; stride >>= 1) {  // partner in this thread (E > 1)
+      if (act) {
         const int rs = stride / NT;
 #pragma unroll
         for (int r = 0; r < E; ++r) {
@@ -155,33 +175,33 @@ __device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, in
             v[r | rs] = desc ? lo : hi;
           }
         }
-      } else if (stride >= 64) {  // partner in another wave
-        uint64_t *xb = cand + (phase & 1) * P;
-        ++phase;
-        if (act) {
+      }
+    }
+    for (; stride >= 64; stride >>= 1) {  // partner in another wave
+      uint64_t *xb = cand + (phase & 1) * P;
+      ++phase;
+      if (act) {
 #pragma unroll
-          for (int r = 0; r < E; ++r) xb[r * NT + tid] = v[r];
-        }
-        __syncthreads();
-        if (act) {
+        for (int r = 0; r < E; ++r) xb[r * NT + tid] = v[r];
+      }
+      __syncthreads();
+      if (act) {
 #pragma unroll
-          for (int r = 0; r < E; ++r) {
-            const int e = r * NT + tid;
-            const uint64_t pv = xb[e ^ stride];
-            const bool keep_max = ((e & size) == 0) == ((e & stride) == 0);
-            v[r] = keep_max ? (v[r] > pv ? v[r] : pv) : (v[r] > pv ? pv : v[r]);
-          }
-        }
-      } else {  // partner in this wave
-        switch (stride) {
-          case 1: wave_stage<E, 1>(v, NT, size); break;
-          case 2: wave_stage<E, 2>(v, NT, size); break;
-          case 4: wave_stage<E, 4>(v, NT, size); break;
-          case 8: wave_stage<E, 8>(v, NT, size); break;
-          case 16: wave_stage<E, 16>(v, NT, size); break;
-          default: wave_stage<E, 32>(v, NT, size); break;
+        for (int r = 0; r < E; ++r) {
+          const int e = r * NT + tid;
+          const uint64_t pv = xb[e ^ stride];
+          const bool keep_max = ((e & size) == 0) == ((e & stride) == 0);
+          v[r] = ((pv > v[r]) == keep_max) ? pv : v[r];
         }
       }
+    }
+    if (act) {  // partner in this wave: strides min(size / 2, 32) .. 1
+      if (size >= 64) wave_stage<E, 32>(v, NT, size);
+      if (size >= 32) wave_stage<E, 16>(v, NT, size);
+      if (size >= 16) wave_stage<E, 8>(v, NT, size);
+      if (size >= 8) wave_stage<E, 4>(v, NT, size);
+      if (size >= 4) wave_stage<E, 2>(v, NT, size);
+      wave_stage<E, 1>(v, NT, size);
     }
   }
   if (act) {
@@ -222,15 +242,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     key[j] = col < n_valid ? score_key(src[col]) : 0u;
   }
   if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
+  for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;
   __syncthreads();
 
   if (k_sel > 0) {
     // ---- radix select of the k_sel-th largest key
-    radix_pass<KPT>(key, 0u, 0u, 21, 2048, sh);
+    radix_pass<KPT>(key, 0u, 0u, 21, 2048, sh, 0);
     const uint32_t d1 = sh.digit;
-    radix_pass<KPT>(key, d1 << 21, 0xFFE00000u, 10, 2048, sh);
+    radix_pass<KPT>(key, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
     const uint32_t d2 = sh.digit;
-    radix_pass<KPT>(key, (d1 << 21) | (d2 << 10), 0xFFFFFC00u, 0, 1024, sh);
+    radix_pass<KPT>(key, (d1 << 21) | (d2 << 10), 0xFFFFFC00u, 0, 1024, sh, 0);
     const uint32_t kstar = (d1 << 21) | (d2 << 10) | sh.digit;
     const uint32_t take_eq = sh.k_rem;          // how many keys == K* are selected (>= 1)
     const uint32_t eq_total = sh.bucket_count;  // how many keys == K* exist

@@ -41,7 +41,7 @@ constexpr int kQW = 8;        // queries (= waves) per workgroup
 constexpr int kThreads = kQW * 64;
 constexpr int kKR = 256;      // keys per workgroup
 constexpr int kEntCap = 36;   // deferred key entries per wave (flushed above kEntCap - 16)
-constexpr int kDotCap = 512;  // near-tie dots listed at a time per wave
+constexpr int kDotCap = 256;  // near-tie dots listed at a time per wave
 
 // Context of one key whose score depends on a near-tie dot: for the four head groups, the relu'd bf16
 // values of the two interval ends (packed pairs; they differ exactly at the near-tie slots).
@@ -56,7 +56,8 @@ template <int KD>
 struct ScoresLds {
   uint4 k[kKR * KD / 8];             // swizzled key block of this workgroup (KD / 8 16-byte chunks per key)
   KeyEntry ent[kQW][kEntCap];
-  uint16_t dots[kQW][kDotCap];       // flattened near-tie dots: (pair << 4) | slot, pair = 4 entry + group
+  uint32_t dots[kQW][kDotCap];       // near-tie dots: head << 24 | key row << 16 | pair << 4 | slot,
+                                     // pair = 4 entry + group
   int32_t kspan[kKR];                // row statistics of the key block and of each wave's query rows, for
   float knorm[kKR];                  // the exact recomputation (no global loads there)
   int32_t qspan[kQW][64];
@@ -136,6 +137,18 @@ __device__ uint16_t round2_to_bf16(double a, double b) {
   return round_dir_to_bf16(s, (t == 0.0) ? 0 : (((t > 0.0) == (s > 0.0)) ? 1 : -1));
 }
 
+// RNE to bf16 of a double s with |s| in [2^-126, 2^127) (or s == 0): round to fp32 with round-to-odd (the
+// RNE conversion, stepped one unit toward zero when it went away from zero, with the last bit set when it
+// was inexact), then RNE to bf16.  Rounding to odd at 24 bits and then to nearest at 8 bits equals direct
+// rounding to nearest at 8 bits (the intermediate keeps more than two extra bits).
+__device__ __forceinline__ uint16_t round_to_bf16_fast(double s) {
+  const float f = static_cast<float>(s);
+  const double back = static_cast<double>(f);
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if (back != s) u = (u - (fabs(back) > fabs(s) ? 1u : 0u)) | 1u;
+  return f32_to_bf16_rne(__builtin_bit_cast(float, u));
+}
+
 // ((G0 + G1) + (G2 + G3)) over the four 16-lane rows of the wave (row g holds head group g), returned in
 // every lane.  v_permlane16_swap exchanges row 1 of its first operand with row 0 of its second (and rows
 // 3 / 2), so with G in both operands every lane ends up holding its row pair's two values; the sum of the
@@ -182,12 +195,17 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
                               int64_t kbrow0, float *orow, int64_t limit, int T, int kb0, const float (&wv)[HT][4],
                               uint32_t &n_exact, uint32_t &n_unres) {
   KeyEntry *E = L.ent[wave];
-  uint16_t *D = L.dots[wave];
+  uint32_t *D = L.dots[wave];
   const int g = lane >> 4, l16 = lane & 15;
   // 1. near-tie masks of the (entry, group) pairs, pair = 4 * entry + group; taken before any patching
   const int npairs = 4 * nent;
+  auto key_row = [&](int pair) {  // row of the entry's key in the LDS block (entries hold keys of the block)
+    return static_cast<uint32_t>(min(max(E[pair >> 2].key - kb0, 0), kKR - 1));
+  };
   const uint32_t m0 = lane < npairs ? entry_mask<HT>(E[lane >> 2], lane & 3) : 0u;
   const uint32_t m1 = lane + 64 < npairs ? entry_mask<HT>(E[(lane + 64) >> 2], lane & 3) : 0u;
+  const uint32_t r0 = lane < npairs ? key_row(lane) : 0u;
+  const uint32_t r1 = lane + 64 < npairs ? key_row(lane + 64) : 0u;
   const uint32_t c0 = __builtin_popcount(m0), c1 = __builtin_popcount(m1);
   const uint32_t i0 = wave_incl_scan(c0);
   const uint32_t t0 = __shfl(i0, 63, 64);
@@ -195,8 +213,14 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
   const int ndots = static_cast<int>(t0 + __shfl(i1, 63, 64));
   n_exact += static_cast<uint32_t>(ndots);
   // 2. the dot list, kDotCap at a time: exact dots, 16 per pass, 4 lanes per dot (lane quarter `sub` owns
-  //    elements KD/4 sub .. KD/4 (sub + 1) - 1); the exact relu'd value replaces the pl value of its slot
+  //    elements KD/4 sub .. KD/4 (sub + 1) - 1); the exact relu'd value replaces the pl value of its slot.
+  //    List entry: head (slot s of pair (entry, group gg) is head 16 (s >> 2) + 4 gg + (s & 3)), key row,
+  //    pair and slot, so that one LDS read locates both operands.
   constexpr int kC = KD / 8, kLC = KD / 32;  // 16-byte chunks per key row; chunks per lane
+  auto pack = [](uint32_t pair, uint32_t row, int bit) {
+    const uint32_t h = 16u * (bit >> 2) + 4u * (pair & 3u) + (bit & 3);
+    return (h << 24) | (row << 16) | (pair << 4) | static_cast<uint32_t>(bit);
+  };
   for (int base = 0; base < ndots; base += kDotCap) {
     {
       uint32_t mm = m0;
@@ -204,7 +228,7 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
       while (mm) {
         const int bit = __builtin_ctz(mm);
         mm &= mm - 1;
-        if (pos >= 0 && pos < kDotCap) D[pos] = static_cast<uint16_t>((lane << 4) | bit);
+        if (pos >= 0 && pos < kDotCap) D[pos] = pack(static_cast<uint32_t>(lane), r0, bit);
         ++pos;
       }
       mm = m1;
@@ -212,7 +236,7 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
       while (mm) {
         const int bit = __builtin_ctz(mm);
         mm &= mm - 1;
-        if (pos >= 0 && pos < kDotCap) D[pos] = static_cast<uint16_t>(((lane + 64) << 4) | bit);
+        if (pos >= 0 && pos < kDotCap) D[pos] = pack(static_cast<uint32_t>(lane + 64), r1, bit);
         ++pos;
       }
     }
@@ -220,65 +244,62 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int nd = min(kDotCap, ndots - base);
     const int dq = lane >> 2, sub = lane & 3;
-    // head of list entry i: slot s of pair (entry, group gg) is head 16 (s >> 2) + 4 gg + (s & 3)
-    auto dot_head = [&](int i) -> int {
-      const uint32_t de = D[i];
-      return 16 * ((de & 15) >> 2) + 4 * ((de >> 4) & 3) + (de & 3);
-    };
-    uint4 qcur[kLC];
-    {
-      const int h0 = dot_head(min(dq, nd - 1));
-      const uint4 *qp0 = reinterpret_cast<const uint4 *>(q + (qrow0 + h0) * KD + (KD / 4) * sub);
-#pragma unroll
-      for (int c = 0; c < kLC; ++c) qcur[c] = qp0[c];
-    }
-    for (int b0 = 0; b0 < nd; b0 += 16) {
-      const int di = min(b0 + dq, nd - 1);  // idle quads repeat the last dot (result identical)
-      const uint32_t de = D[di];
-      const int pr = static_cast<int>(de >> 4), slot = static_cast<int>(de & 15);
-      const int e = pr >> 2, gg = pr & 3;
-      const int h = 16 * (slot >> 2) + 4 * gg + (slot & 3);
-      const int key = min(E[e].key, T - 1);  // entries only hold keys < T; clamp defensively
-      const int kl = key - kb0;               // row of the key in the LDS block
+    // list entry i (idle quads repeat the last one; the result is identical), its q row quarter (global,
+    // L2-resident), its key row quarter (LDS) and the span sum that decides the exact path
+    auto fetch = [&](int i, uint32_t &de, uint4 (&qv)[kLC], uint4 (&kv)[kLC], int &spn) {
+      de = D[min(i, nd - 1)];
+      const int h = static_cast<int>(de >> 24), kl = static_cast<int>((de >> 16) & 255u);
       const uint4 *qp = reinterpret_cast<const uint4 *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
-      uint4 qa[kLC], ka[kLC];
 #pragma unroll
-      for (int c = 0; c < kLC; ++c) {
-        qa[c] = qcur[c];
-        ka[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
-      }
-      // the next pass's q rows are in flight while this pass computes
-      if (b0 + 16 < nd) {
-        const int hn = dot_head(min(b0 + 16 + dq, nd - 1));
-        const uint4 *qpn = reinterpret_cast<const uint4 *>(q + (qrow0 + hn) * KD + (KD / 4) * sub);
+      for (int c = 0; c < kLC; ++c) qv[c] = qp[c];
 #pragma unroll
-        for (int c = 0; c < kLC; ++c) qcur[c] = qpn[c];
-      }
-      const int span_sum = L.qspan[wave][h] + L.kspan[kl];
+      for (int c = 0; c < kLC; ++c) kv[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
+      spn = L.qspan[wave][h] + L.kspan[kl];
+    };
+    uint32_t dcur;
+    uint4 qcur[kLC], kcur[kLC];
+    int scur;
+    fetch(dq, dcur, qcur, kcur, scur);
+    for (int b0 = 0; b0 < nd; b0 += 16) {
+      // the next pass's operands are in flight while this pass computes
+      const bool more = b0 + 16 < nd;
+      uint32_t dnx = 0;
+      uint4 qnx[kLC], knx[kLC];
+      int snx = 0;
+      if (more) fetch(b0 + 16 + dq, dnx, qnx, knx, snx);
+      const int h = static_cast<int>(dcur >> 24), kl = static_cast<int>((dcur >> 16) & 255u);
+      const int pr = static_cast<int>((dcur >> 4) & 255u), slot = static_cast<int>(dcur & 15u);
       uint16_t r;
-      if (__builtin_amdgcn_ballot_w64(span_sum > 52) == 0ull) {
+      if (__builtin_amdgcn_ballot_w64(scur > 52) == 0ull) {
         // every partial sum is a multiple of the smallest product LSB and below 2^53 of it: exact doubles
         // in any order
         double a0 = 0.0, a1 = 0.0;
 #pragma unroll
         for (int c = 0; c < kLC; ++c) {
-          const uint32_t qw[4] = {qa[c].x, qa[c].y, qa[c].z, qa[c].w};
-          const uint32_t kw[4] = {ka[c].x, ka[c].y, ka[c].z, ka[c].w};
+          const uint32_t qw[4] = {qcur[c].x, qcur[c].y, qcur[c].z, qcur[c].w};
+          const uint32_t kw[4] = {kcur[c].x, kcur[c].y, kcur[c].z, kcur[c].w};
 #pragma unroll
           for (int p = 0; p < 4; ++p) {
             a0 = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), a0);
             a1 = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), a1);
           }
         }
-        r = round_dir_to_bf16(quad_sum_f64(a0 + a1), 0);
+        const double sum = quad_sum_f64(a0 + a1);
+        const bool outside = sum != 0.0 && !(fabs(sum) >= 0x1p-126 && fabs(sum) < 0x1p127);
+        if (__builtin_amdgcn_ballot_w64(outside) == 0ull) {
+          r = round_to_bf16_fast(sum);
+        } else {
+          r = round_dir_to_bf16(sum, 0);
+        }
       } else {
         // wide dynamic range: products above / below 2^(top - 38) accumulate separately, each exactly
+        const int span_sum = scur;
         const int top_sum = frexp_exp(L.qnorm[wave][h]) + frexp_exp(L.knorm[kl]);
         const bool split = span_sum > 52;
         const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
         double hi = 0.0, lo = 0.0;
         // rare path, kept register-light: one dword of q and k per step, re-read from memory
-        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qp);
+        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
 #pragma unroll 1
         for (int j = 0; j < 4 * kLC; ++j) {
           const uint32_t qw = q32[j];
@@ -293,11 +314,20 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
       }
       const uint32_t rv = (r & 0x8000) ? 0u : r;  // ReLU (also maps -0 to +0)
       if (sub == 0 && b0 + dq < nd) {
-        if (span_sum <= 84) {
-          uint16_t *half = reinterpret_cast<uint16_t *>(&E[e].pl[gg][slot >> 1]) + (slot & 1);
+        if (scur <= 84) {
+          uint16_t *half = reinterpret_cast<uint16_t *>(&E[pr >> 2].pl[pr & 3][slot >> 1]) + (slot & 1);
           *half = static_cast<uint16_t>(rv);
         } else {
           ++n_unres;
+        }
+      }
+      if (more) {
+        dcur = dnx;
+        scur = snx;
+#pragma unroll
+        for (int c = 0; c < kLC; ++c) {
+          qcur[c] = qnx[c];
+          kcur[c] = knx[c];
         }
       }
     }
@@ -338,7 +368,9 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
   __shared__ ScoresLds<KD> L;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is uniform per wave; readfirstlane lets the compiler keep the query row, the causal limit
+  // and the tile loop in scalar registers
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
   const int64_t b = blockIdx.z;
   const int kb0 = blockIdx.x * kKR;

@@ -5,9 +5,13 @@
 // The reference kernel (optimized/sinkhorn_project/op_kernel/sinkhorn_kernel.asc:168-189) keeps all
 // iterations on chip; here every matrix lives in registers for the whole call.
 //
-// Layout: matrix m is 16 contiguous floats (row-major); lane g owns row (g % 4) of matrix (g / 4) as one
-// float4, so a wave moves 1 KiB of contiguous memory per load/store (fully coalesced 16-byte accesses).
-// Row sums are in-lane; column sums are quad reductions with DPP quad permutes (no LDS, no barrier).
+// Two kernels, chosen by batch size (both read and write every byte exactly once):
+// - fewer than 65536 matrices (latency-bound launches): lane g owns row (g % 4) of matrix (g / 4) as one
+//   float4; row sums are in-lane, column sums are quad reductions with DPP quad permutes.  Four lanes per
+//   matrix give four times the waves, which is what a short launch needs.
+// - larger batches (VALU-bound at this arithmetic intensity): one matrix per lane; global accesses stay
+//   fully coalesced through a per-wave LDS tile, and the matrix is carried as x_ij = a_i y_ij b_j so a
+//   normalisation step updates four scales instead of rescaling sixteen elements.
 // Reciprocals use v_rcp_f32 (<= 1 ulp) followed by a multiply; the result stays within a few fp32 ulps of
 // true division after 20 normalisations (the reference needed a Newton step for its 10-bit reciprocal,
 // optimized/sinkhorn_project/design.md:51-52).
@@ -73,6 +77,101 @@ __global__ __launch_bounds__(256) void sinkhorn4x4_kernel(const float4 *__restri
   if (live) out[g] = v;
 }
 
+// Matrix-per-lane form (large batches): lane t owns matrix t in 16 registers, so row and column sums
+// are both in-lane and nothing is computed redundantly (the row-per-lane form recomputes every column sum
+// and reciprocal in all four lanes of a quad).  Softmax uses v_exp_f32 and a reciprocal multiply.
+// Global traffic stays fully coalesced: each wave loads its 64 matrices (4 KiB) as four 1 KiB wave-wide
+// rows of 16-byte chunks and passes them through a per-wave LDS tile to the matrix-per-lane layout (and
+// back before the store).  In the tile, row r of matrix m sits at 16-byte unit 4m + (r ^ ((m >> 2) & 3)),
+// which keeps both the coalesced-side and the matrix-side accesses of every 16 lanes on distinct banks.
+constexpr int kSkWaves = 4;  // waves per block
+
+__device__ __forceinline__ int sk_unit(int m, int r) { return 4 * m + (r ^ ((m >> 2) & 3)); }
+
+__global__ __launch_bounds__(64 * kSkWaves) void sinkhorn4x4_mat_kernel(const float4 *__restrict__ x,
+                                                                       float4 *__restrict__ out, int64_t n_mats,
+                                                                       int repeat, float eps) {
+  __shared__ float4 tile[kSkWaves][256];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kSkWaves + wave) * 64;  // first matrix of the wave
+  if (m0 >= n_mats) return;  // whole wave idle (no block-wide synchronisation below)
+  const int64_t chunks = 4 * (n_mats - m0);  // 16-byte chunks left from the wave's start
+  float4 *T = tile[wave];
+  const float4 *src = x + 4 * m0;
+  // load: chunk c = 64 j + lane is row c % 4 of matrix c / 4
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = 64 * j + lane;
+    T[sk_unit(c >> 2, c & 3)] = c < chunks ? src[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float v[16];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float4 a = T[sk_unit(lane, r)];
+    v[4 * r] = a.x;
+    v[4 * r + 1] = a.y;
+    v[4 * r + 2] = a.z;
+    v[4 * r + 3] = a.w;
+  }
+  // softmax over each row, then + eps (baseline/sinkhorn.py:14; no eps inside the softmax)
+  constexpr float kLog2e = 1.44269504088896341f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float *w = v + 4 * r;
+    const float ml = fmaxf(fmaxf(w[0], w[1]), fmaxf(w[2], w[3])) * kLog2e;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = __builtin_amdgcn_exp2f(__builtin_fmaf(w[c], kLog2e, -ml));
+    const float q = rcp((w[0] + w[1]) + (w[2] + w[3]));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w[c] = __builtin_fmaf(w[c], q, eps);
+  }
+  // The matrix is kept as x_ij = a_i y_ij b_j with y the softmax output above: a row normalisation
+  // divides a_i by (a_i sum_j y_ij b_j + eps) = (row sum + eps), a column normalisation b_j by
+  // (b_j sum_i a_i y_ij + eps), so each step costs one 4-term dot and one reciprocal per row or column
+  // instead of rescaling all 16 elements.
+  float a[4] = {1.f, 1.f, 1.f, 1.f}, b[4] = {1.f, 1.f, 1.f, 1.f};
+  auto col_step = [&]() {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float t = a[0] * v[c];
+#pragma unroll
+      for (int r = 1; r < 4; ++r) t = __builtin_fmaf(a[r], v[4 * r + c], t);
+      b[c] *= rcp(__builtin_fmaf(b[c], t, eps));
+    }
+  };
+  auto row_step = [&]() {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float t = v[4 * r] * b[0];
+#pragma unroll
+      for (int c = 1; c < 4; ++c) t = __builtin_fmaf(v[4 * r + c], b[c], t);
+      a[r] *= rcp(__builtin_fmaf(a[r], t, eps));
+    }
+  };
+  col_step();  // :15
+  for (int it = 1; it < repeat; ++it) {  // :16-18
+    row_step();
+    col_step();
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[4 * r + c] = (a[r] * v[4 * r + c]) * b[c];
+  // store through the tile (each lane rewrites only the units it read)
+#pragma unroll
+  for (int r = 0; r < 4; ++r) T[sk_unit(lane, r)] = make_float4(v[4 * r], v[4 * r + 1], v[4 * r + 2], v[4 * r + 3]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float4 *dst = out + 4 * m0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = 64 * j + lane;
+    if (c < chunks) dst[c] = T[sk_unit(c >> 2, c & 3)];
+  }
+}
+
 }  // namespace
 }  // namespace ks
 
@@ -83,11 +182,19 @@ extern "C" int ks_sinkhorn(const float *x, float *out, int64_t n_mats, int32_t r
   if (n_mats == 0) return KS_OK;
   KS_CHECK_ARG(x != nullptr && out != nullptr, "ks_sinkhorn: null pointer");
   KS_CHECK_ARG(ks::aligned(x, 16) && ks::aligned(out, 16), "ks_sinkhorn: x and out must be 16-byte aligned");
-  const int64_t n_rows = n_mats * 4;
-  const int64_t blocks = ks::ceil_div(n_rows, 256);
-  hipLaunchKernelGGL(ks::sinkhorn4x4_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+  if (n_mats < (int64_t(1) << 16)) {
+    // small batches: one row per lane gives four times the waves, which is what a latency-bound launch needs
+    const int64_t n_rows = n_mats * 4;
+    hipLaunchKernelGGL(ks::sinkhorn4x4_kernel, dim3(static_cast<unsigned>(ks::ceil_div(n_rows, 256))), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), reinterpret_cast<const float4 *>(x),
+                       reinterpret_cast<float4 *>(out), n_rows, static_cast<int>(repeat), eps);
+    KS_CHECK_LAUNCH("sinkhorn4x4_kernel");
+    return KS_OK;
+  }
+  const int64_t blocks = ks::ceil_div(n_mats, 64 * ks::kSkWaves);
+  hipLaunchKernelGGL(ks::sinkhorn4x4_mat_kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * ks::kSkWaves), 0,
                      static_cast<hipStream_t>(stream), reinterpret_cast<const float4 *>(x),
-                     reinterpret_cast<float4 *>(out), n_rows, static_cast<int>(repeat), eps);
-  KS_CHECK_LAUNCH("sinkhorn4x4_kernel");
+                     reinterpret_cast<float4 *>(out), n_mats, static_cast<int>(repeat), eps);
+  KS_CHECK_LAUNCH("sinkhorn4x4_mat_kernel");
   return KS_OK;
 }

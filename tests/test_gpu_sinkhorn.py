@@ -60,3 +60,15 @@ def test_sinkhorn_large_doubly_stochastic(device):
     want = oracle.sinkhorn(x.cpu().numpy(), 10, 1e-6)
     np.testing.assert_allclose(y.cpu().numpy(), want, atol=1e-2, rtol=1e-2)
     assert np.max(np.abs(y.cpu().numpy() - want)) < 1e-4
+
+
+@pytest.mark.parametrize("shape,repeat", [((65536, 4, 4), 10), ((65536 + 77, 4, 4), 10), ((3, 25001, 4, 4), 5)])
+def test_sinkhorn_matrix_per_lane_ragged(device, shape, repeat):
+    # batches from 65536 matrices on take the matrix-per-lane kernel; ragged tails leave part of the last
+    # wave idle
+    g = torch.Generator().manual_seed(sum(shape) + repeat)
+    x = (torch.randn(shape, generator=g) * 3).to(device)
+    got = _run(x, repeat)
+    want = oracle.sinkhorn(x.cpu().numpy(), repeat, 1e-6)
+    np.testing.assert_allclose(got, want, atol=1e-2, rtol=1e-2)
+    assert np.max(np.abs(got - want)) < 1e-5

@@ -58,6 +58,22 @@ __device__ __forceinline__ void row_norm_span(float ss, int lsb, float &norm, in
   span = norm > 0.f ? top - lsb : 0;
 }
 
+// Division by a runtime divisor 1 <= d < 2^32 with a multiply-high, an add and a shift (the round-up
+// reciprocal of Granlund and Montgomery, "Division by invariant integers using multiplication", 1994):
+// with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(m, n) + n) >> l for every
+// 32-bit n when the sum is formed in 64 bits.
+struct FastDiv {
+  uint32_t d, m, l;
+  FastDiv() = default;
+  explicit FastDiv(uint32_t dv) : d(dv), m(0), l(0) {
+    while ((uint64_t(1) << l) < dv) ++l;
+    m = static_cast<uint32_t>(((uint64_t(1) << 32) * ((uint64_t(1) << l) - dv)) / dv + 1);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return static_cast<uint32_t>((static_cast<uint64_t>(__umulhi(n, m)) + n) >> l);
+  }
+};
+
 // One set of bf16 rows for the RoPE / row-statistics launch.  Row r (0 <= r < rows) of the set is
 // source row (r / rows_per_batch) * src_batch_rows + r % rows_per_batch and destination row r; its
 // position is pos0 + ((r % rows_per_batch) / H) % S.  dst may equal src (in place) or be null (statistics

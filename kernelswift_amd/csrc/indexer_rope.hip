@@ -18,47 +18,95 @@
 namespace ks {
 namespace {
 
+// Kernel-side form of a RowJob: 32-bit row arithmetic with precomputed divisors.
+struct RowJobK {
+  const uint16_t *src;
+  uint16_t *dst;
+  float *norm;
+  int32_t *span;
+  int64_t src_batch_rows, pos0;
+  uint32_t rows;
+  int rope_dim;
+  FastDiv rpb, H, S;
+};
+
+RowJobK kernel_job(const RowJob &j) {
+  RowJobK k{};
+  k.src = j.src;
+  k.dst = j.dst;
+  k.norm = j.norm;
+  k.span = j.span;
+  k.src_batch_rows = j.src_batch_rows;
+  k.pos0 = j.pos0;
+  k.rows = static_cast<uint32_t>(j.rows);
+  k.rope_dim = j.rope_dim;
+  k.rpb = FastDiv(static_cast<uint32_t>(j.rows_per_batch));
+  k.H = FastDiv(static_cast<uint32_t>(j.H));
+  k.S = FastDiv(static_cast<uint32_t>(j.S));
+  return k;
+}
+
+// Sum and minimum over the CPR lanes of a row (CPR in {8, 16}: an aligned lane group) with DPP exchanges.
+template <int CPR>
+__device__ __forceinline__ void row_reduce(float &ss, int &lsb) {
+#define KS_STEP(S)                                                                 \
+  ss += __builtin_bit_cast(float, lane_xor<S>(__builtin_bit_cast(uint32_t, ss)));  \
+  lsb = min(lsb, static_cast<int>(lane_xor<S>(static_cast<uint32_t>(lsb))));
+  KS_STEP(1)
+  KS_STEP(2)
+  KS_STEP(4)
+  if constexpr (CPR == 16) {
+    KS_STEP(8)
+  }
+#undef KS_STEP
+}
+
 // One thread per 16-byte chunk; blocks [0, blocks0) take job 0 and the rest job 1 (a uniform choice, so
 // each field is selected separately from the kernel arguments, never through a pointer to them).
-template <bool STATS>
-__global__ __launch_bounds__(256) void rope_rows_kernel(RowJob j0, RowJob j1, uint32_t blocks0,
-                                                       const float *__restrict__ freqs, int D, int rope_start) {
+// CPR: chunks per row, 8 or 16 with statistics (0: any D, no statistics).
+template <int CPR>
+__global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, uint32_t blocks0,
+                                                       const float *__restrict__ freqs, int D, FastDiv cpr,
+                                                       int rope_start) {
   const bool second = blockIdx.x >= blocks0;
 #define KS_PICK(f) (second ? j1.f : j0.f)
   const uint16_t *__restrict__ src = KS_PICK(src);
   uint16_t *__restrict__ dst = KS_PICK(dst);
-  const uint32_t rows = static_cast<uint32_t>(KS_PICK(rows));
-  const uint32_t rpb = static_cast<uint32_t>(KS_PICK(rows_per_batch));
+  const uint32_t rows = KS_PICK(rows);
   const int64_t sbr = KS_PICK(src_batch_rows);
-  const uint32_t H = static_cast<uint32_t>(KS_PICK(H)), S = static_cast<uint32_t>(KS_PICK(S));
   const int64_t pos0 = KS_PICK(pos0);
   const int rope_dim = KS_PICK(rope_dim);
+  const FastDiv rpb = KS_PICK(rpb), Hd = KS_PICK(H), Sd = KS_PICK(S);
 #undef KS_PICK
   const uint32_t blk = second ? blockIdx.x - blocks0 : blockIdx.x;
-  const uint32_t cpr = static_cast<uint32_t>(D) / 8;  // chunks per row
-  const uint32_t c = blk * 256u + threadIdx.x;         // < 2^31 (checked on the host)
-  const uint32_t row = c / cpr, j = c % cpr;
+  const uint32_t c = blk * 256u + threadIdx.x;  // < 2^31 (checked on the host)
+  uint32_t row, j;
+  if constexpr (CPR == 0) {
+    row = cpr.div(c);
+    j = c - row * cpr.d;
+  } else {
+    row = c / CPR;  // power of two: a shift
+    j = c % CPR;
+  }
   const bool live = row < rows;
-  const uint32_t rb = live ? row / rpb : 0, rr = live ? row % rpb : 0;
+  const uint32_t rb = live ? rpb.div(row) : 0, rr = live ? row - rb * rpb.d : 0;
   const int64_t srow = static_cast<int64_t>(rb) * sbr + rr;
   uint4 v = make_uint4(0, 0, 0, 0);
   if (live) v = *reinterpret_cast<const uint4 *>(src + srow * D + 8 * j);
   const int e0 = 8 * static_cast<int>(j);
   if (live && rope_dim > 0 && e0 >= rope_start && e0 < rope_start + rope_dim) {
-    const int64_t pos = pos0 + (rr / H) % S;
+    const uint32_t t = Hd.div(rr);
+    const int64_t pos = pos0 + (t - Sd.div(t) * Sd.d);
     const float2 *cs = reinterpret_cast<const float2 *>(freqs) + pos * (rope_dim / 2) + (e0 - rope_start) / 2;
     v = rope_chunk(v, cs);
   }
   if (live && dst != nullptr) *reinterpret_cast<uint4 *>(dst + static_cast<int64_t>(row) * D + 8 * j) = v;
-  if constexpr (STATS) {
-    // D in {64, 128}: the D/8 lanes of a row are an aligned group of the wave.
+  if constexpr (CPR != 0) {
+    // the CPR lanes of a row are an aligned group of the wave
     float ss = 0.f;
     int lsb = 1 << 20;
     chunk_stats(v, ss, lsb);
-    for (uint32_t m = 1; m < cpr; m <<= 1) {
-      ss += __shfl_xor(ss, m, 64);
-      lsb = min(lsb, __shfl_xor(lsb, m, 64));
-    }
+    row_reduce<CPR>(ss, lsb);
     if (live && j == 0) {
       float *norm = second ? j1.norm : j0.norm;
       int32_t *span = second ? j1.span : j0.span;
@@ -75,20 +123,25 @@ int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs,
   KS_CHECK_ARG(c0 + c1 + 512 < (int64_t(1) << 31), "rope rows: %lld + %lld chunks exceed the 32-bit grid",
                (long long)c0, (long long)c1);
   KS_CHECK_ARG(job0.rows_per_batch >= 1 && job1.rows_per_batch >= 1 && job0.H >= 1 && job1.H >= 1 &&
-                   job0.S >= 1 && job1.S >= 1,
-               "rope rows: empty batch, head or position extent");
+                   job0.S >= 1 && job1.S >= 1 && job0.rows_per_batch < (int64_t(1) << 31) &&
+                   job1.rows_per_batch < (int64_t(1) << 31) && job0.H < (int64_t(1) << 31) &&
+                   job1.H < (int64_t(1) << 31) && job0.S < (int64_t(1) << 31) && job1.S < (int64_t(1) << 31),
+               "rope rows: batch, head or position extent out of range");
   const int64_t b0 = ceil_div(c0, 256), b1 = ceil_div(c1, 256);
   if (b0 + b1 == 0) return KS_OK;
   const bool stats = job0.norm != nullptr;
   KS_CHECK_ARG((job1.rows == 0 || (job1.norm != nullptr) == stats) && (!stats || D == 64 || D == 128),
                "rope rows: statistics need D in {64, 128} and both jobs alike");
   const dim3 grid(static_cast<unsigned>(b0 + b1));
-  if (stats) {
-    hipLaunchKernelGGL(rope_rows_kernel<true>, grid, dim3(256), 0, stream, job0, job1,
-                       static_cast<uint32_t>(b0), freqs, D, rope_start);
+  const RowJobK k0 = kernel_job(job0), k1 = kernel_job(job1);
+  const FastDiv cpr(static_cast<uint32_t>(D / 8));
+  const uint32_t n0 = static_cast<uint32_t>(b0);
+  if (stats && D == 128) {
+    hipLaunchKernelGGL(rope_rows_kernel<16>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start);
+  } else if (stats) {
+    hipLaunchKernelGGL(rope_rows_kernel<8>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start);
   } else {
-    hipLaunchKernelGGL(rope_rows_kernel<false>, grid, dim3(256), 0, stream, job0, job1,
-                       static_cast<uint32_t>(b0), freqs, D, rope_start);
+    hipLaunchKernelGGL(rope_rows_kernel<0>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start);
   }
   KS_CHECK_LAUNCH("rope_rows_kernel");
   return KS_OK;

@@ -40,7 +40,9 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kQW = 8;        // queries (= waves) per workgroup
 constexpr int kThreads = kQW * 64;
 constexpr int kKR = 256;      // keys per workgroup
-constexpr int kEntCap = 36;   // deferred key entries per wave (flushed above kEntCap - 16)
+constexpr int kEntCap = 36;   // deferred key entries per wave (flushed before a tile would overflow them)
+static_assert(kEntCap >= 16, "one tile can defer 16 keys");
+static_assert(4 * kEntCap <= 255, "list entries hold the (entry, group) pair in 8 bits");
 constexpr int kDotCap = 256;  // near-tie dots listed at a time per wave
 
 // Context of one key whose score depends on a near-tie dot: for the four head groups, the relu'd bf16
@@ -190,9 +192,7 @@ __device__ __forceinline__ uint32_t entry_mask(const KeyEntry &en, int gg) {
 // Exact recomputation of the deferred near-tie dots of one wave, then of the affected scores.
 template <int HT, int KD, bool WBF>
 __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
-                              const float *__restrict__ qn, const int32_t *__restrict__ qsp,
-                              const float *__restrict__ kn, const int32_t *__restrict__ ksp, int64_t qrow0,
-                              int64_t kbrow0, float *orow, int64_t limit, int T, int kb0, const float (&wv)[HT][4],
+                              int64_t qrow0, float *orow, int64_t limit, int T, int kb0, const float (&wv)[HT][4],
                               uint32_t &n_exact, uint32_t &n_unres) {
   KeyEntry *E = L.ent[wave];
   uint32_t *D = L.dots[wave];
@@ -202,16 +202,22 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
   auto key_row = [&](int pair) {  // row of the entry's key in the LDS block (entries hold keys of the block)
     return static_cast<uint32_t>(min(max(E[pair >> 2].key - kb0, 0), kKR - 1));
   };
-  const uint32_t m0 = lane < npairs ? entry_mask<HT>(E[lane >> 2], lane & 3) : 0u;
-  const uint32_t m1 = lane + 64 < npairs ? entry_mask<HT>(E[(lane + 64) >> 2], lane & 3) : 0u;
-  const uint32_t r0 = lane < npairs ? key_row(lane) : 0u;
-  const uint32_t r1 = lane + 64 < npairs ? key_row(lane + 64) : 0u;
-  const uint32_t c0 = __builtin_popcount(m0), c1 = __builtin_popcount(m1);
-  const uint32_t i0 = wave_incl_scan(c0);
-  const uint32_t t0 = __shfl(i0, 63, 64);
-  const uint32_t i1 = wave_incl_scan(c1);
-  const int ndots = static_cast<int>(t0 + __shfl(i1, 63, 64));
-  n_exact += static_cast<uint32_t>(ndots);
+  // pairs are taken 64 at a time: pair 64 i + lane in set i
+  constexpr int kSets = (4 * kEntCap + 63) / 64;
+  uint32_t mset[kSets], rset[kSets], cset[kSets], first[kSets];
+  uint32_t ndots_u = 0;
+#pragma unroll
+  for (int i = 0; i < kSets; ++i) {
+    const int pair = 64 * i + lane;
+    mset[i] = pair < npairs ? entry_mask<HT>(E[pair >> 2], pair & 3) : 0u;
+    rset[i] = pair < npairs ? key_row(pair) : 0u;
+    cset[i] = __builtin_popcount(mset[i]);
+    const uint32_t incl = wave_incl_scan(cset[i]);
+    first[i] = ndots_u + incl - cset[i];  // list position of this pair's first dot
+    ndots_u += __shfl(incl, 63, 64);
+  }
+  const int ndots = static_cast<int>(ndots_u);
+  n_exact += ndots_u;
   // 2. the dot list, kDotCap at a time: exact dots, 16 per pass, 4 lanes per dot (lane quarter `sub` owns
   //    elements KD/4 sub .. KD/4 (sub + 1) - 1); the exact relu'd value replaces the pl value of its slot.
   //    List entry: head (slot s of pair (entry, group gg) is head 16 (s >> 2) + 4 gg + (s & 3)), key row,
@@ -222,21 +228,14 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
     return (h << 24) | (row << 16) | (pair << 4) | static_cast<uint32_t>(bit);
   };
   for (int base = 0; base < ndots; base += kDotCap) {
-    {
-      uint32_t mm = m0;
-      int pos = static_cast<int>(i0 - c0) - base;
+#pragma unroll
+    for (int i = 0; i < kSets; ++i) {
+      uint32_t mm = mset[i];
+      int pos = static_cast<int>(first[i]) - base;
       while (mm) {
         const int bit = __builtin_ctz(mm);
         mm &= mm - 1;
-        if (pos >= 0 && pos < kDotCap) D[pos] = pack(static_cast<uint32_t>(lane), r0, bit);
-        ++pos;
-      }
-      mm = m1;
-      pos = static_cast<int>(t0 + i1 - c1) - base;
-      while (mm) {
-        const int bit = __builtin_ctz(mm);
-        mm &= mm - 1;
-        if (pos >= 0 && pos < kDotCap) D[pos] = pack(static_cast<uint32_t>(lane + 64), r1, bit);
+        if (pos >= 0 && pos < kDotCap) D[pos] = pack(static_cast<uint32_t>(64 * i + lane), rset[i], bit);
         ++pos;
       }
     }
@@ -244,30 +243,18 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int nd = min(kDotCap, ndots - base);
     const int dq = lane >> 2, sub = lane & 3;
-    // list entry i (idle quads repeat the last one; the result is identical), its q row quarter (global,
-    // L2-resident), its key row quarter (LDS) and the span sum that decides the exact path
-    auto fetch = [&](int i, uint32_t &de, uint4 (&qv)[kLC], uint4 (&kv)[kLC], int &spn) {
-      de = D[min(i, nd - 1)];
-      const int h = static_cast<int>(de >> 24), kl = static_cast<int>((de >> 16) & 255u);
+    for (int b0 = 0; b0 < nd; b0 += 16) {
+      // list entry of this quad (idle quads repeat the last one; the result is identical), its q row
+      // quarter (global, L2-resident), its key row quarter (LDS) and the span sum that decides the path
+      const uint32_t dcur = D[min(b0 + dq, nd - 1)];
+      const int h = static_cast<int>(dcur >> 24), kl = static_cast<int>((dcur >> 16) & 255u);
+      uint4 qcur[kLC], kcur[kLC];
       const uint4 *qp = reinterpret_cast<const uint4 *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
 #pragma unroll
-      for (int c = 0; c < kLC; ++c) qv[c] = qp[c];
+      for (int c = 0; c < kLC; ++c) qcur[c] = qp[c];
 #pragma unroll
-      for (int c = 0; c < kLC; ++c) kv[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
-      spn = L.qspan[wave][h] + L.kspan[kl];
-    };
-    uint32_t dcur;
-    uint4 qcur[kLC], kcur[kLC];
-    int scur;
-    fetch(dq, dcur, qcur, kcur, scur);
-    for (int b0 = 0; b0 < nd; b0 += 16) {
-      // the next pass's operands are in flight while this pass computes
-      const bool more = b0 + 16 < nd;
-      uint32_t dnx = 0;
-      uint4 qnx[kLC], knx[kLC];
-      int snx = 0;
-      if (more) fetch(b0 + 16 + dq, dnx, qnx, knx, snx);
-      const int h = static_cast<int>(dcur >> 24), kl = static_cast<int>((dcur >> 16) & 255u);
+      for (int c = 0; c < kLC; ++c) kcur[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
+      const int scur = L.qspan[wave][h] + L.kspan[kl];
       const int pr = static_cast<int>((dcur >> 4) & 255u), slot = static_cast<int>(dcur & 15u);
       uint16_t r;
       if (__builtin_amdgcn_ballot_w64(scur > 52) == 0ull) {
@@ -319,15 +306,6 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
           *half = static_cast<uint16_t>(rv);
         } else {
           ++n_unres;
-        }
-      }
-      if (more) {
-        dcur = dnx;
-        scur = snx;
-#pragma unroll
-        for (int c = 0; c < kLC; ++c) {
-          qcur[c] = qnx[c];
-          kcur[c] = knx[c];
         }
       }
     }
@@ -449,13 +427,14 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     }
   };
 
-  auto tile_epilogue = [&](int t, const f32x4_t(&acc)[HT]) {
+  // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot; pl / ph keep the
+  // interval ends for them
+  auto tile_epilogue = [&](int t, const f32x4_t(&acc)[HT], uint32_t(&pl)[2 * HT], uint32_t(&ph)[2 * HT]) {
     const int key_l = 16 * t + l16;
     const int key = kb0 + key_l;
     const bool kvalid = key_l < nk;
     // interval test: RNE(A - delta) == RNE(A + delta) (after ReLU) <=> the exact dot rounds to the same
     // relu'd bf16 value; pl holds that value for the head sum
-    uint32_t pl[2 * HT], ph[2 * HT];
     uint64_t anyr = 0;
 #pragma unroll
     for (int m = 0; m < HT; ++m)
@@ -485,9 +464,31 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const float outv = WBF ? round_bf16_f(tot) : tot;
     if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
     anyr &= __builtin_amdgcn_ballot_w64(kvalid);  // keys past T are zero rows, never deferred
-    if (anyr != 0ull) {
+    return static_cast<uint32_t>((anyr | (anyr >> 16) | (anyr >> 32) | (anyr >> 48)) & 0xFFFFull);
+  };
+
+  // software pipeline: the MFMAs of the next tile are in flight during the current tile's epilogue.  The
+  // deferred keys are flushed at one place: before a tile's deferred keys would overflow the list, and in
+  // one extra round after the last tile.
+  f32x4_t acc[HT], nxt[HT];
+  if (nlive > 0) tile_mfma(0, acc);
+  for (int t = 0; t <= nlive; ++t) {
+    const bool live_t = t < nlive;
+    uint32_t pl[2 * HT], ph[2 * HT];
+    uint32_t km = 0;
+    if (live_t) {
+      if (t + 1 < nlive) tile_mfma(t + 1, nxt);
+      km = tile_epilogue(t, acc, pl, ph);
+    }
+    const int cnt = __builtin_popcount(km);
+    if (live_t ? (nent + cnt > kEntCap) : (nent > 0)) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
+      nent = 0;
+    }
+    if (km != 0u) {
       // defer the keys holding a near-tie dot: save all four groups' interval ends
-      const uint32_t km = static_cast<uint32_t>((anyr | (anyr >> 16) | (anyr >> 32) | (anyr >> 48)) & 0xFFFFull);
       if ((km >> l16) & 1u) {
         const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
         KeyEntry &en = L.ent[wave][e];
@@ -496,28 +497,14 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
           en.pl[g][p] = pl[p];
           en.ph[g][p] = ph[p];
         }
-        if (g == 0) en.key = key;
+        if (g == 0) en.key = kb0 + 16 * t + l16;
       }
-      nent += __builtin_popcount(km);
+      nent += cnt;
     }
-  };
-
-  // software pipeline: the MFMAs of the next tile are in flight during the current tile's epilogue; the
-  // deferred entries are flushed at one place (when a further tile could overflow them, and at the end)
-  f32x4_t acc[HT], nxt[HT];
-  if (nlive > 0) tile_mfma(0, acc);
-  for (int t = 0; t < nlive; ++t) {
-    if (t + 1 < nlive) tile_mfma(t + 1, nxt);
-    tile_epilogue(t, acc);
-    if (nent > kEntCap - 16 || (t == nlive - 1 && nent > 0)) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qn, qsp, kn, ksp, qrow0, kbrow0, orow, limit, T, kb0, wv,
-                             n_exact, n_unres);
-      nent = 0;
-    }
+    if (live_t) {
 #pragma unroll
-    for (int m = 0; m < HT; ++m) acc[m] = nxt[m];
+      for (int m = 0; m < HT; ++m) acc[m] = nxt[m];
+    }
   }
   // masked tiles (at or past the causal limit)
   for (int t = nlive; t < ntiles; ++t) {

@@ -99,6 +99,26 @@ def test_scores_small_bit_exact(device, H, w_bf16, D):
 
 
 @pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("H", [16, 64])
+@pytest.mark.parametrize("w_bf16", [False, True])
+def test_scores_every_dot_deferred(device, H, w_bf16, D):
+    # a huge error-bound constant makes every positive dot a near-tie: every key of every tile is deferred,
+    # the per-wave entry list fills to capacity and each flush runs the exact path on all of its dots
+    g = torch.Generator().manual_seed(7 * H + w_bf16 + D)
+    B, S, T = 1, 11, 530
+    q = torch.randn(B, S, H, D, generator=g).bfloat16()
+    k = torch.randn(B, T, D, generator=g).bfloat16()
+    w = torch.randn(B, S, H, generator=g) / 8
+    if w_bf16:
+        w = w.bfloat16()
+    print(f"[case] scores all deferred H={H} D={D} w_bf16={w_bf16}", flush=True)
+    got, st = _scores_gpu(q, k, w, True, T - S, bound_c=1e6)
+    want = _oracle_scores(q, k, w, True, T - S)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert st[0] > S * H * T // 4 and st[1] == 0
+
+
+@pytest.mark.parametrize("D", [128, 64])
 def test_scores_midpoint_ties_exact_path(device, D):
     # small-integer inputs: every dot is an integer computed exactly by the MFMA; odd values above 256
     # sit exactly on bf16 midpoints, so ties-to-even must come from the exact recomputation

@@ -228,10 +228,10 @@ def run_sinkhorn(steps, warmup, do_cpu, cpu_budget):
         sweep[str(n)] = {"us": round(us, 2), "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
         del xx, oo
     res = {"us_per_call": round(dev_med, 3), "wall_us_per_call_sync": round(wall_med, 3), "ms_per_step": ms_step,
-           "kernels_us": {"sinkhorn4x4_mat_kernel": round(kus, 3)},
-           "roofline": {"bound": "hbm", "kernel": "sinkhorn4x4_mat_kernel", "achieved": round(achieved, 1),
+           "kernels_us": {"sinkhorn4x4_kernel": round(kus, 3)},
+           "roofline": {"bound": "hbm", "kernel": "sinkhorn4x4_kernel", "achieved": round(achieved, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                        "traffic": _traffic("sinkhorn4x4_mat_kernel@cfg1"), "cache": "warm (2 MiB fits in L2)"},
+                        "traffic": _traffic("sinkhorn4x4_kernel@cfg1"), "cache": "warm (2 MiB fits in L2)"},
            "size_sweep_matrices": sweep}
     if do_cpu:
         from oracle import torch_ref

@@ -342,7 +342,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
     const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
-    int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats) {
+    int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats, int xcd_pk) {
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
   __shared__ ScoresLds<KD> L;
@@ -350,10 +350,21 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   // and the tile loop in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
+  // XCD-aware placement: workgroup i of a batch slice runs on XCD i % 8 (the slice holds a multiple of 8
+  // workgroups when xcd_pk > 0).  XCD j takes a (gridDim.y / Pq) x (gridDim.x / Pk) tile of (query
+  // group, key block) pairs with Pk = xcd_pk, Pq = 8 / Pk, so its L2 holds Pk-th of the queries' rows and
+  // Pq-th of the keys instead of every query group.
+  int kblk = blockIdx.x, qgrp = blockIdx.y;
+  if (xcd_pk > 0) {
+    const int wg = blockIdx.y * gridDim.x + blockIdx.x, xcd = wg & 7, l = wg >> 3;
+    const int gxk = gridDim.x / xcd_pk, gyq = gridDim.y / (8 / xcd_pk);
+    qgrp = (xcd / xcd_pk) * gyq + l / gxk;
+    kblk = (xcd % xcd_pk) * gxk + l % gxk;
+  }
   const int64_t b = blockIdx.z;
-  const int kb0 = blockIdx.x * kKR;
+  const int kb0 = kblk * kKR;
   const int nk = min(kKR, T - kb0);
-  const int64_t s = static_cast<int64_t>(blockIdx.y) * kQW + wave;
+  const int64_t s = static_cast<int64_t>(qgrp) * kQW + wave;
   const bool s_ok = s < S;
   const int64_t kbrow0 = b * kbs;        // first key row of batch b
   const int64_t krow0 = kbrow0 + kb0;    // first key row of this workgroup
@@ -524,12 +535,28 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
                      hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
+  // XCD tiling (Pq x Pk = 8) that minimises the L2 fills: each query group's rows are read by Pk XCDs,
+  // each key block by Pq; 0 keeps the launch order (slice not a multiple of 8 or no tiling divides it)
+  int xcd_pk = 0;
+  if ((static_cast<int64_t>(grid.x) * grid.y) % 8 == 0) {
+    const double qbytes = static_cast<double>(S) * 16 * HT * KD, kbytes = static_cast<double>(T) * KD;
+    double best = 0.0;
+    for (int pk = 1; pk <= 8; pk *= 2) {
+      const int pq = 8 / pk;
+      if (grid.x % pk != 0 || grid.y % pq != 0) continue;
+      const double cost = qbytes * pk + kbytes * pq;
+      if (xcd_pk == 0 || cost < best) {
+        best = cost;
+        xcd_pk = pk;
+      }
+    }
+  }
   if (w_bf16) {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn, ksp,
-                       scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats);
+                       scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk);
   } else {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn,
-                       ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats);
+                       ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;

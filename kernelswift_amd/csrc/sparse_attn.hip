@@ -175,7 +175,7 @@ inline SaSplit split_plan(int64_t B, int64_t M, int64_t H, int64_t K) {
 template <int DQK, int DV, int GW>
 __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ kv, const float *__restrict__ sink,
-    const int32_t *__restrict__ idx, uint16_t *__restrict__ out, float *__restrict__ part_o,
+    const int32_t *__restrict__ idx, uint16_t *__restrict__ out, uint16_t *__restrict__ part_o,
     float *__restrict__ part_ml, int64_t n_items, int64_t M, int H, int64_t N, int64_t K, int NS, int KR,
     float scale_log2) {
   using Sh = SaShape<DQK, DV, GW>;
@@ -409,7 +409,7 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
         }
         out[(sq * H + h) * DV + d] = f32_to_bf16_rne(val);
       } else {
-        part_o[(sitem * H + h) * DV + d] = acc;
+        part_o[(sitem * H + h) * DV + d] = f32_to_bf16_rne(acc);
         if (d == 0) {
           part_ml[(sitem * H + h) * 2] = z;
           part_ml[(sitem * H + h) * 2 + 1] = lsum;
@@ -452,9 +452,13 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
     for (int r = 0; r < 4; ++r) {
       const int hr = gw * 16 + 4 * g + r;
       if (hr < H) {
-        float *po = part_o + (item * H + hr) * DV;
+        uint16_t *po = part_o + (item * H + hr) * DV;
 #pragma unroll
-        for (int cc = 0; cc < CT; ++cc) po[16 * cc + l16] = o[cc][r];
+        for (int cc = 0; cc < CT; cc += 2) {  // one packed convert per two column tiles
+          const uint32_t pk = pack_bf16x2(o[cc][r], o[cc + 1][r]);
+          po[16 * cc + l16] = static_cast<uint16_t>(pk & 0xFFFFu);
+          po[16 * (cc + 1) + l16] = static_cast<uint16_t>(pk >> 16);
+        }
       }
     }
     if (g == 0 && head_ok) {
@@ -468,7 +472,7 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
 // Merge the NS partial ranges of one (query, head) row with the sink: one wave per row, lane s reads
 // range s's (max, sum); every lane then accumulates DV/64 columns over the ranges.
 template <int DV>
-__global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const float *__restrict__ part_o,
+__global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const uint16_t *__restrict__ part_o,
                                                                  const float *__restrict__ part_ml,
                                                                  const float *__restrict__ sink,
                                                                  uint16_t *__restrict__ out, int64_t rows, int H,
@@ -498,17 +502,17 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const float *_
   float acc[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) acc[i] = 0.f;
-  const float *po = part_o + (qm * NS * H + h) * DV + lane * CPL;
+  const uint16_t *po = part_o + (qm * NS * H + h) * DV + lane * CPL;
   // empty ranges have w = 0 and O = 0, so every range is accumulated without a branch
 #pragma unroll 8
   for (int s = 0; s < NS; ++s) {
     const float ws = __shfl(w, s, 64);
-    const float *src = po + static_cast<int64_t>(s) * H * DV;
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(po + static_cast<int64_t>(s) * H * DV);
 #pragma unroll
     for (int i = 0; i < CPL; i += 2) {
-      const float2 v = *reinterpret_cast<const float2 *>(src + i);
-      acc[i] += ws * v.x;
-      acc[i + 1] += ws * v.y;
+      const uint32_t v = src[i / 2];
+      acc[i] += ws * __builtin_bit_cast(float, v << 16);
+      acc[i + 1] += ws * __builtin_bit_cast(float, v & 0xFFFF0000u);
     }
   }
   const float inv = den > 0.f ? 1.f / den : 0.f;
@@ -524,10 +528,13 @@ int launch_sa_gw(const uint16_t *q, const uint16_t *kv, const float *sink, const
   using Sh = SaShape<DQK, DV, GW>;
   const SaSplit sp = split_plan(B, M, H, K);
   const int64_t n_items = B * M * sp.ns;
-  float *part_o = nullptr, *part_ml = nullptr;
+  // split partials: (max, sum) pairs in fp32, then the unnormalised O rows in bf16 (16-byte aligned: H is a
+  // multiple of 16)
+  uint16_t *part_o = nullptr;
+  float *part_ml = nullptr;
   if (sp.ns > 1) {
-    part_o = static_cast<float *>(ws);
-    part_ml = part_o + n_items * H * DV;
+    part_ml = static_cast<float *>(ws);
+    part_o = reinterpret_cast<uint16_t *>(part_ml + n_items * H * 2);
   }
   const int64_t blocks = ceil_div(n_items, Sh::GROUPS);
   hipLaunchKernelGGL((sparse_attn_kernel<DQK, DV, GW>), dim3(static_cast<unsigned>(blocks)), dim3(Sh::THREADS), 0,
@@ -560,7 +567,7 @@ int launch_sa(const uint16_t *q, const uint16_t *kv, const float *sink, const in
 size_t sa_workspace(int64_t B, int64_t M, int64_t H, int64_t K, int64_t DV) {
   const SaSplit sp = split_plan(B, M, H, K);
   if (sp.ns <= 1) return 0;
-  return static_cast<size_t>(B * M * sp.ns * H * (DV + 2)) * sizeof(float);
+  return static_cast<size_t>(B * M * sp.ns * H) * (2 * sizeof(float) + DV * sizeof(uint16_t));
 }
 
 }  // namespace

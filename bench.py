@@ -126,6 +126,29 @@ def _traffic(name):
         return None
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def _gpu_clocks():
+    """Shader-clock levels as rocm-smi reports them (best effort; None when the tool is unavailable)."""
+    import subprocess
+    try:
+        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True, text=True, timeout=30)
+        d = json.loads(r.stdout)
+        card = next(iter(d.values()))
+        return {k: v for k, v in card.items() if "sclk" in k.lower() or "fclk" in k.lower() or "mclk" in k.lower()}
+    except Exception:
+        return None
+
+
 def _cpu_threads():
     try:
         return len(os.sched_getaffinity(0))
@@ -215,6 +238,9 @@ def run_sinkhorn(steps, warmup, do_cpu, cpu_budget):
     dev_med, dev_mean = _events_median(lambda: ops.sinkhorn(x, 10, 1e-6), steps, warmup)
     wall_med, ms_step = _wall(lambda: ops.sinkhorn(x, 10, 1e-6), steps, warmup)
     kus = _events_avg(k, steps, warmup)
+    # the reference's other configured iteration count (hc_sinkhorn_iters = 20)
+    kus20 = _events_avg(lambda: _lib.check(lib.ks_sinkhorn(x.data_ptr(), out.data_ptr(), x.shape[0], 20, 1e-6, stream),
+                                           "sinkhorn"), steps, warmup)
     nbytes = 2 * x.numel() * 4
     achieved = nbytes / (kus * 1e-6) / 1e9
     # size sweep (asymptotic bandwidth; the 2 MiB config is launch/latency bound)
@@ -232,7 +258,7 @@ def run_sinkhorn(steps, warmup, do_cpu, cpu_budget):
            "roofline": {"bound": "hbm", "kernel": "sinkhorn4x4_kernel", "achieved": round(achieved, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                         "traffic": _traffic("sinkhorn4x4_kernel@cfg1"), "cache": "warm (2 MiB fits in L2)"},
-           "size_sweep_matrices": sweep}
+           "size_sweep_matrices": sweep, "repeat20_kernel_us": round(kus20, 3)}
     if do_cpu:
         from oracle import torch_ref
         xc = x.cpu()
@@ -267,7 +293,9 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
            "kernels_us": {"sparse_attn_kernel+combine": round(op_us, 3)},
            "roofline": {"bound": "mfma", "kernel": "sparse_attn_kernel (+ combine)", "achieved": round(achieved, 2),
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                        "traffic": _traffic(f"sparse_attn_kernel@cfg{cfg}")},
+                        "traffic": _traffic(f"sparse_attn_kernel@cfg{cfg}"),
+                        "cache": ("warm (the 2 MiB kv fits in L2)" if cfg == 3
+                                  else "kv 2.25 GiB: gathered rows come from HBM")},
            "gathered_GBps": round(gathered / (op_us * 1e-6) / 1e9, 1)}
     if do_cpu:
         from oracle import torch_ref
@@ -341,6 +369,8 @@ def main():
         "wall_us_per_call_sync": head["wall_us_per_call_sync"],
         "per_config": {str(k): v for k, v in per.items()},
         "device": torch.cuda.get_device_name(0),
+        "gpu_clocks": _gpu_clocks(),
+        "host": {"cpu_model": _cpu_model(), "threads": _cpu_threads()},
     }
     print(json.dumps(line), flush=True)
 

@@ -1,4 +1,4 @@
-// Fused indexer entry: RoPE + row statistics of q and k (one launch) -> exact scores -> exact top-k.
+// Fused indexer entry: RoPE + row statistics of q and k (one launch) -> scores -> exact top-k.
 //
 // Semantics of baseline/indexer.py:161-206 after the two projections (which stay in the caller):
 // RoPE on the configured segment of q (and k), score = sum_h w_h * relu(bf16(q_h . k)), causal mask,
@@ -7,6 +7,12 @@
 // All intermediates live in the caller's workspace; inputs are never modified.  RoPE stays a pass of its
 // own: done inside the score kernel it would be repeated by every workgroup that reads a row (S/8 times
 // per key row), which measured twice as slow as the separate pass.
+//
+// With 64 heads, D = 128 and fp32 weights the scores are computed with bounds instead of exactly: the
+// score kernel keeps the canonical score of the lower interval ends plus a per-score bound, and the top-k
+// kernel recomputes exactly only the scores whose interval reaches its selection threshold.  The selected
+// indices are identical to those of the exact path (same intervals, same exact recomputation, same
+// canonical sums wherever a score can matter); the exact path runs every other shape.
 #include "common.h"
 #include "indexer_common.h"
 
@@ -20,6 +26,8 @@ struct IndexerWs {
   float *k_norm;
   int32_t *k_span;
   float *scores;
+  float *bounds;  // per-score bounds of the bounded path
+  float *kmax;    // per key block norm maxima of the bounded path
   size_t bytes;
 };
 
@@ -40,6 +48,8 @@ IndexerWs carve(void *base, int64_t B, int64_t S, int64_t H, int64_t D, int64_t 
   w.k_norm = reinterpret_cast<float *>(take(size_t(B * T) * 4));
   w.k_span = reinterpret_cast<int32_t *>(take(size_t(B * T) * 4));
   w.scores = reinterpret_cast<float *>(take(size_t(B * S * T) * 4));
+  w.bounds = reinterpret_cast<float *>(take(size_t(B * S * T) * 4));
+  w.kmax = reinterpret_cast<float *>(take(size_t(B * ((T + ks::kScoreKeyBlock - 1) / ks::kScoreKeyBlock)) * 4));
   w.bytes = off;
   return w;
 }
@@ -51,12 +61,15 @@ extern "C" size_t ks_indexer_workspace_size(int64_t B, int64_t S, int64_t H, int
   return carve(nullptr, B, S, H, D, T).bytes;
 }
 
-extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,
-                          int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
-                          int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out,
-                          int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D, int64_t T,
-                          int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream) {
+namespace {
+// path: 0 = bounded when the shape allows it, 1 = exact, 2 = bounded (error when the shape does not allow it)
+int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,
+                 int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
+                 int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64,
+                 int64_t B, int64_t S, int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
+                 size_t workspace_bytes, void *stream, float bound_c, uint32_t *stats, int path) {
   ks::last_error().clear();
+  KS_CHECK_ARG(path >= 0 && path <= 3, "ks_indexer: path %d", path);
   KS_CHECK_ARG(D == 128 || D == 64, "ks_indexer: D=%lld, the kernels are built for head_dim 64 and 128",
                (long long)D);
   KS_CHECK_ARG(H == 16 || H == 32 || H == 64, "ks_indexer: H=%lld must be 16, 32 or 64", (long long)H);
@@ -89,9 +102,46 @@ extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, i
   const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
   int rc = ks::launch_rope_rows(qjob, kjob, freqs, static_cast<int>(D), static_cast<int>(rope_start), st);
   if (rc != KS_OK) return rc;
+  const bool can_bound = H == 64 && D == 128 && !w_bf16 && T <= 32768 && kk <= 2048;
+  KS_CHECK_ARG(path < 2 || can_bound,
+               "ks_indexer: the bounded path needs H = 64, D = 128, fp32 weights, T <= 32768 and k <= 2048");
+  if (can_bound && path != 1) {
+    rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span, ws.scores, B,
+                                   S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, bound_c, nullptr, st, ws.bounds,
+                                   ws.kmax);
+    if (rc != KS_OK) return rc;
+    const ks::TopkRecompute trc{ws.bounds, ws.kmax, ws.q_rot, ws.k_rot, static_cast<const float *>(w), ws.q_norm,
+                                ws.q_span, ws.k_norm, ws.k_span, T, bound_c, stats, path == 3 ? 1 : 0};
+    return ks::launch_indexer_topk_bounded(ws.scores, T, B, S, T, kk, causal ? 1 : 0, start_pos, ratio, offset, out,
+                                           out_i64 ? 1 : 0, trc, st);
+  }
   rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, w_bf16 ? 1 : 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span,
-                                 ws.scores, B, S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC,
-                                 nullptr, st);
+                                 ws.scores, B, S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, bound_c, stats, st);
   if (rc != KS_OK) return rc;
   return ks_indexer_topk(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, stream);
+}
+}  // namespace
+
+extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,
+                          int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
+                          int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out,
+                          int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D, int64_t T,
+                          int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream) {
+  return indexer_impl(q, k, w, w_bf16, freqs, freq_rows, rope_start, rope_dim, rope_k, k_top, causal, start_pos, ratio,
+                      offset, out, out_i64, B, S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream,
+                      ks::kScoreBoundC, nullptr, 0);
+}
+
+// Diagnostic variant (not part of the public header): explicit error-bound constant, path choice (0 auto,
+// 1 exact, 2 bounded, 3 bounded with a third counter) and device counters stats[0] += exact dot
+// recomputations, stats[1] += dots outside the provably exact range (path 3: stats[2] += recomputed scores).
+extern "C" int ks_dbg_indexer(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,
+                              int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
+                              int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out,
+                              int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D, int64_t T,
+                              int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream,
+                              float bound_c, uint32_t *stats, int32_t path) {
+  return indexer_impl(q, k, w, w_bf16, freqs, freq_rows, rope_start, rope_dim, rope_k, k_top, causal, start_pos, ratio,
+                      offset, out, out_i64, B, S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, bound_c,
+                      stats, path);
 }

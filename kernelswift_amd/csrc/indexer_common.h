@@ -93,9 +93,39 @@ struct RowJob {
 int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
                      hipStream_t stream);
 
+// Exact scores (bounds == nullptr), or, with bounds (H = 64, D = 128, fp32 weights), the canonical score from
+// the lower interval end of every dot plus a per-score bound U: the exact score lies in [score - U,
+// score + U], both ends also after rounding to nearest, and U = 0 exactly when the score is exact.  kmax
+// [B][ceil(T / kScoreKeyBlock)] then receives each key block's key-norm maximum (the interval half-width
+// of a dot is bound_c 2^-23 ||q_h|| kmax), for an exact recomputation with the same intervals.
+constexpr int kScoreKeyBlock = 256;
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
-                          int ratio, float bound_c, uint32_t *stats, hipStream_t stream);
+                          int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds = nullptr,
+                          float *kmax = nullptr);
+
+// Sorted exact top-k of rows of bounded scores (the bound-emitting score kernel's output): selects with the
+// lower ends, recomputes exactly the scores that may reach the top k (interval test with the score
+// kernel's half-widths, exact double-precision dots for the near ties, canonical head sum), then runs the
+// exact selection.  q / k: the rotated rows and their statistics (64 heads, D = 128), w fp32 [B, S, 64].
+struct TopkRecompute {
+  const float *bounds;
+  const float *kmax;
+  const uint16_t *q;
+  const uint16_t *k;
+  const float *w;
+  const float *qn;
+  const int32_t *qsp;
+  const float *kn;
+  const int32_t *ksp;
+  int64_t kbs;  // key rows per batch in k, kn, ksp
+  float bound_c;
+  uint32_t *stats;  // optional: [0] += exact dot recomputations, [1] += dots outside the exact range
+  int stats_ext;    // with stats: [2] += recomputed scores
+};
+int launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
+                                int causal, int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
+                                const TopkRecompute &rc, hipStream_t stream);
 
 }  // namespace ks

@@ -27,19 +27,17 @@
 // exact; beyond that the dot keeps the lower interval end and is counted as unresolved.
 #include "common.h"
 #include "indexer_common.h"
+#include "indexer_exact.h"
+
+#include <type_traits>
 
 namespace ks {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef short short2_t __attribute__((ext_vector_type(2)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kQW = 8;        // queries (= waves) per workgroup
 constexpr int kThreads = kQW * 64;
-constexpr int kKR = 256;      // keys per workgroup
+constexpr int kKR = kScoreKeyBlock;  // keys per workgroup
 constexpr int kEntCap = 36;   // deferred key entries per wave (flushed before a tile would overflow them)
 static_assert(kEntCap >= 16, "one tile can defer 16 keys");
 static_assert(4 * kEntCap <= 255, "list entries hold the (entry, group) pair in 8 bits");
@@ -66,104 +64,6 @@ struct ScoresLds {
   float qnorm[kQW][64];
   float red[kQW];
 };
-
-__device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
-                                                  0, 0, 0);
-}
-
-__device__ __forceinline__ float round_bf16_f(float a) { return bf16_to_f32(f32_to_bf16_rne(a)); }
-
-// Packed RNE conversion of two fp32 values and ReLU on the bf16 bit patterns (negative bf16 values are
-// negative int16, so a signed max with 0 clears them to +0).
-__device__ __forceinline__ uint32_t cvt_relu_pk(float lo, float hi) {
-  const bf16x2_t v = __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t);  // one v_cvt_pk_bf16_f32
-  const short2_t s = __builtin_elementwise_max(__builtin_bit_cast(short2_t, v), short2_t{0, 0});
-  return __builtin_bit_cast(uint32_t, s);
-}
-
-__device__ __forceinline__ float unpack_hi(uint32_t p) { return __builtin_bit_cast(float, p & 0xFFFF0000u); }
-__device__ __forceinline__ float unpack_lo(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
-
-__device__ __forceinline__ int frexp_exp(float x) {
-  int e = 0;
-  frexpf(x, &e);
-  return e;
-}
-
-template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double v) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u), CTRL, 0xF, 0xF, false);
-  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u >> 32), CTRL, 0xF, 0xF, false);
-  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// Sum over the 4 lanes of a quad (quad_perm xor 1, xor 2); exact whenever every partial sum is.
-__device__ __forceinline__ double quad_sum_f64(double v) {
-  v += dpp_f64<0xB1>(v);
-  return v + dpp_f64<0x4E>(v);
-}
-
-// RNE to bf16 of a double value s, with the sign of a residual t (s + t is the exact value, |t| below the
-// double spacing at s) deciding exact bf16 midpoints; t == 0 ties to even.
-__device__ uint16_t round_dir_to_bf16(double s, int tdir) {
-  if (s == 0.0) return 0;
-  const uint64_t bits = __builtin_bit_cast(uint64_t, s);
-  const uint16_t sign = (bits >> 63) ? 0x8000 : 0;
-  const uint64_t mag = bits & 0x7FFFFFFFFFFFFFFFull;
-  const int e = static_cast<int>(mag >> 52) - 1023;
-  if (e >= -126) {
-    uint64_t kept = mag >> 45;
-    const uint64_t rem = mag & ((1ull << 45) - 1);
-    const uint64_t half = 1ull << 44;
-    const bool up = rem > half || (rem == half && (tdir > 0 || (tdir == 0 && (kept & 1))));
-    if (up) ++kept;
-    const int ebf = static_cast<int>(kept >> 7) - 1023 + 127;
-    if (ebf >= 255) return sign | 0x7F80;
-    return sign | static_cast<uint16_t>(ebf << 7) | static_cast<uint16_t>(kept & 0x7F);
-  }
-  const double x = ldexp(fabs(s), 133);  // exact; x < 2^7
-  const double n = floor(x);
-  const double rem = x - n;
-  const uint32_t ni = static_cast<uint32_t>(n);
-  const bool up = rem > 0.5 || (rem == 0.5 && (tdir > 0 || (tdir == 0 && (ni & 1))));
-  return sign | static_cast<uint16_t>(ni + (up ? 1u : 0u));  // 128 -> smallest normal, bits 0x0080
-}
-
-// RNE to bf16 of the exact value a + b (two doubles): TwoSum gives s + t == a + b exactly.
-__device__ uint16_t round2_to_bf16(double a, double b) {
-  const double s = a + b;
-  const double bb = s - a;
-  const double t = (a - (s - bb)) + (b - bb);
-  return round_dir_to_bf16(s, (t == 0.0) ? 0 : (((t > 0.0) == (s > 0.0)) ? 1 : -1));
-}
-
-// RNE to bf16 of a double s with |s| in [2^-126, 2^127) (or s == 0): round to fp32 with round-to-odd (the
-// RNE conversion, stepped one unit toward zero when it went away from zero, with the last bit set when it
-// was inexact), then RNE to bf16.  Rounding to odd at 24 bits and then to nearest at 8 bits equals direct
-// rounding to nearest at 8 bits (the intermediate keeps more than two extra bits).
-__device__ __forceinline__ uint16_t round_to_bf16_fast(double s) {
-  const float f = static_cast<float>(s);
-  const double back = static_cast<double>(f);
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if (back != s) u = (u - (fabs(back) > fabs(s) ? 1u : 0u)) | 1u;
-  return f32_to_bf16_rne(__builtin_bit_cast(float, u));
-}
-
-// ((G0 + G1) + (G2 + G3)) over the four 16-lane rows of the wave (row g holds head group g), returned in
-// every lane.  v_permlane16_swap exchanges row 1 of its first operand with row 0 of its second (and rows
-// 3 / 2), so with G in both operands every lane ends up holding its row pair's two values; the sum of the
-// two registers is G0 + G1 in rows 0-1 and G2 + G3 in rows 2-3.  v_permlane32_swap does the same across
-// the wave halves.  Written as inline assembly (the builtin form was miscompiled into v + v when both
-// operands carry the same value); the NOPs cover the VALU-write -> permlane-read hazard.
-__device__ __forceinline__ float combine_groups(float G) {
-  float a = G, b = G;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-  float c = a + b, d = c;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
-  return c + d;
-}
 
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
@@ -337,15 +237,29 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int HT, int KD, bool WBF>
+// Shared memory of the bound-emitting variant: the key block and the per-wave norm maxima only (no
+// deferred-key entries, no dot lists, no row statistics).
+template <int KD>
+struct ScoresLdsBound {
+  uint4 k[kKR * KD / 8];
+  float knorm[kKR];
+  int32_t kspan[kKR];
+  int32_t qspan[kQW][64];
+  float qnorm[kQW][64];
+  float red[kQW];
+};
+
+template <int HT, int KD, bool WBF, bool BOUND>
 __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
     const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
-    int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats, int xcd_pk) {
+    int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats, int xcd_pk,
+    float *__restrict__ bounds, float *__restrict__ kmax) {
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
-  __shared__ ScoresLds<KD> L;
+  static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
+  __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD>, ScoresLds<KD>> L;
   // the wave index is uniform per wave; readfirstlane lets the compiler keep the query row, the causal limit
   // and the tile loop in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -406,6 +320,11 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   knm = L.red[0];
 #pragma unroll
   for (int i = 1; i < kQW; ++i) knm = fmaxf(knm, L.red[i]);
+  // BOUND: the block's key-norm maximum for the exact recomputation of candidate scores, which must use
+  // the same interval width (every query group writes the same value)
+  if constexpr (BOUND) {
+    if (tid == 0) kmax[b * gridDim.x + kblk] = knm;
+  }
   if (!s_ok) return;
   float wv[HT][4], dl[HT][4];
 #pragma unroll
@@ -417,8 +336,25 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
       dl[m][r] = bound_c * 0x1p-23f * qn[hr] * knm;
     }
 
+  // BOUND: A-fragments holding bf16 upper bounds of |w| for the two 32-head halves.  With the relu'd
+  // interval ends of a tile as B-fragments (lane (l16, g) holds heads 4g + 0..3 and 16 + 4g + 0..3 of
+  // each half, exactly the k-slots 8g .. 8g + 7 of a 16x16x32 B operand), one MFMA per half sums
+  // w_up * r over the 32 heads for every key, in every output row.
+  uint4 wa[2] = {};
+  if constexpr (BOUND) {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const float *wr = wv[2 * hh];
+      const float *wr1 = wv[2 * hh + 1];
+      auto pk = [](float a, float c) {
+        return static_cast<uint32_t>(bf16_abs_round_up(a)) | (static_cast<uint32_t>(bf16_abs_round_up(c)) << 16);
+      };
+      wa[hh] = make_uint4(pk(wr[0], wr[1]), pk(wr[2], wr[3]), pk(wr1[0], wr1[1]), pk(wr1[2], wr1[3]));
+    }
+  }
   const int64_t limit = causal ? (start_pos + s + 1) / ratio : INT64_MAX;
   float *orow = scores + (b * S + s) * T;
+  float *urow = BOUND ? bounds + (b * S + s) * T : nullptr;
   uint32_t n_exact = 0, n_unres = 0;
   int nent = 0;
   // tiles of 16 keys; tiles at or past the causal limit are masked without MFMA work
@@ -475,7 +411,23 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const float outv = WBF ? round_bf16_f(tot) : tot;
     if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
     anyr &= __builtin_amdgcn_ballot_w64(kvalid);  // keys past T are zero rows, never deferred
-    return static_cast<uint32_t>((anyr | (anyr >> 16) | (anyr >> 32) | (anyr >> 48)) & 0xFFFFull);
+    const uint32_t km = static_cast<uint32_t>((anyr | (anyr >> 16) | (anyr >> 32) | (anyr >> 48)) & 0xFFFFull);
+    if constexpr (BOUND) {
+      // |exact score - tot| <= sum_h |w_h| (ph_h - pl_h) + (rounding of the canonical sum: 38 roundings of
+      // at most 2^-24 of sum_h |w_h| ph_h, < 2^-18 of it) <= dph - dpl + 2^-16 (dph + dpl), dph / dpl the
+      // MFMA sums of w_up * ph / pl (64 nonnegative exact products: relative error < 63 * 2^-23 < 2^-17
+      // even with truncating additions).  The 2^-21 |tot| term lets tot -/+ bound be rounded to nearest and
+      // stay a bound.  Keys without a near-tie dot have bound 0 (tot is exact).
+      f32x4_t dph = f32x4_t{0.f, 0.f, 0.f, 0.f}, dpl = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        dph = mfma16(wa[hh], make_uint4(ph[4 * hh], ph[4 * hh + 1], ph[4 * hh + 2], ph[4 * hh + 3]), dph);
+        dpl = mfma16(wa[hh], make_uint4(pl[4 * hh], pl[4 * hh + 1], pl[4 * hh + 2], pl[4 * hh + 3]), dpl);
+      }
+      const float u = (dph[0] - dpl[0]) + 0x1p-16f * (dph[0] + dpl[0]) + 0x1p-21f * fabsf(tot) + 0x1p-100f;
+      if (g == 0 && kvalid) urow[key] = (key < limit && ((km >> l16) & 1u)) ? u : 0.f;
+    }
+    return km;
   };
 
   // software pipeline: the MFMAs of the next tile are in flight during the current tile's epilogue.  The
@@ -491,26 +443,30 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
       if (t + 1 < nlive) tile_mfma(t + 1, nxt);
       km = tile_epilogue(t, acc, pl, ph);
     }
+    if constexpr (BOUND) km = 0u;  // the bound replaces the exact recomputation
     const int cnt = __builtin_popcount(km);
-    if (live_t ? (nent + cnt > kEntCap) : (nent > 0)) {
+    if (!BOUND && (live_t ? (nent + cnt > kEntCap) : (nent > 0))) {  // never taken with BOUND
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
+      if constexpr (!BOUND)
+        flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
       nent = 0;
     }
-    if (km != 0u) {
-      // defer the keys holding a near-tie dot: save all four groups' interval ends
-      if ((km >> l16) & 1u) {
-        const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
-        KeyEntry &en = L.ent[wave][e];
+    if constexpr (!BOUND) {
+      if (km != 0u) {
+        // defer the keys holding a near-tie dot: save all four groups' interval ends
+        if ((km >> l16) & 1u) {
+          const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
+          KeyEntry &en = L.ent[wave][e];
 #pragma unroll
-        for (int p = 0; p < 2 * HT; ++p) {
-          en.pl[g][p] = pl[p];
-          en.ph[g][p] = ph[p];
+          for (int p = 0; p < 2 * HT; ++p) {
+            en.pl[g][p] = pl[p];
+            en.ph[g][p] = ph[p];
+          }
+          if (g == 0) en.key = kb0 + 16 * t + l16;
         }
-        if (g == 0) en.key = kb0 + 16 * t + l16;
+        nent += cnt;
       }
-      nent += cnt;
     }
     if (live_t) {
 #pragma unroll
@@ -532,7 +488,7 @@ template <int HT, int KD>
 int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                      const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                      int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c, uint32_t *stats,
-                     hipStream_t stream) {
+                     float *bounds, float *kmax, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
   // XCD tiling (Pq x Pk = 8) that minimises the L2 fills: each query group's rows are read by Pk XCDs,
@@ -551,12 +507,23 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
       }
     }
   }
-  if (w_bf16) {
-    hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn, ksp,
-                       scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk);
+  if (bounds != nullptr) {
+    if constexpr (HT == 4) {
+      if (w_bf16) return fail(KS_ERR_INVALID, "indexer scores: score bounds need fp32 weights");
+      hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true>), grid, dim3(kThreads), 0, stream, q, k, w, qn,
+                         qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats,
+                         xcd_pk, bounds, kmax);
+    } else {
+      return fail(KS_ERR_INVALID, "indexer scores: score bounds need H = 64");
+    }
+  } else if (w_bf16) {
+    hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp,
+                       kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk,
+                       nullptr, nullptr);
   } else {
-    hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp, kn,
-                       ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk);
+    hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn,
+                       qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats,
+                       xcd_pk, nullptr, nullptr);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;
@@ -566,17 +533,17 @@ template <int KD>
 int launch_scores_d(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                     const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                     int64_t H, int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c,
-                    uint32_t *stats, hipStream_t stream) {
+                    uint32_t *stats, float *bounds, float *kmax, hipStream_t stream) {
   switch (H) {
     case 16:
       return launch_scores_ht<1, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, stream);
+                                     ratio, bound_c, stats, bounds, kmax, stream);
     case 32:
       return launch_scores_ht<2, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, stream);
+                                     ratio, bound_c, stats, bounds, kmax, stream);
     case 64:
       return launch_scores_ht<4, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, stream);
+                                     ratio, bound_c, stats, bounds, kmax, stream);
     default:
       return fail(KS_ERR_INVALID, "indexer scores: H=%lld, supported: 16, 32, 64", (long long)H);
   }
@@ -587,13 +554,14 @@ int launch_scores_d(const uint16_t *q, const uint16_t *k, const void *w, int w_b
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
-                          int ratio, float bound_c, uint32_t *stats, hipStream_t stream) {
+                          int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds,
+                          float *kmax) {
   if (D == 128)
     return launch_scores_d<128>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                                bound_c, stats, stream);
+                                bound_c, stats, bounds, kmax, stream);
   if (D == 64)
     return launch_scores_d<64>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                               bound_c, stats, stream);
+                               bound_c, stats, bounds, kmax, stream);
   return fail(KS_ERR_INVALID, "indexer scores: D=%lld, supported: 64, 128", (long long)D);
 }
 

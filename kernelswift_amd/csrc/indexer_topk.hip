@@ -18,6 +18,8 @@
 // it holds fewer than k columns, the remaining slots are the masked columns in ascending order, which
 // post-processing turns into -1 (the reference's prefix pruning, indexer_topk.asc:96-152).
 #include "common.h"
+#include "indexer_common.h"
+#include "indexer_exact.h"
 
 namespace ks {
 namespace {
@@ -216,6 +218,69 @@ __device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, in
   }
 }
 
+// Exact selection of the k_sel largest keys of a row held in registers (column j*1024 + lane), then the
+// sorted store.  sh.k_rem == k_sel and sh.hist[0] == 0 on entry, behind a barrier.
+template <int KPT>
+__device__ __forceinline__ void select_sort_store(const uint32_t (&key)[KPT], int k_sel, int64_t row, int k, void *out, int out_i64,
+                                  int causal, int64_t limit, int64_t offset, uint64_t *cand, SelShared &sh) {
+  const int tid = threadIdx.x;
+  // ---- radix select of the k_sel-th largest key
+  radix_pass<KPT>(key, 0u, 0u, 21, 2048, sh, 0);
+  const uint32_t d1 = sh.digit;
+  radix_pass<KPT>(key, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
+  const uint32_t d2 = sh.digit;
+  radix_pass<KPT>(key, (d1 << 21) | (d2 << 10), 0xFFFFFC00u, 0, 1024, sh, 0);
+  const uint32_t kstar = (d1 << 21) | (d2 << 10) | sh.digit;
+  const uint32_t take_eq = sh.k_rem;          // how many keys == K* are selected (>= 1)
+  const uint32_t eq_total = sh.bucket_count;  // how many keys == K* exist
+  const uint32_t n_gt = static_cast<uint32_t>(k_sel) - take_eq;
+
+  // ---- collect keys > K* (unordered) and, if all of them are taken, keys == K*: slots from a block scan
+  uint32_t ntake = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) ntake += (key[j] > kstar || (key[j] == kstar && take_eq == eq_total)) ? 1u : 0u;
+  uint32_t pos = block_inclusive_scan(ntake, sh.wsum) - ntake;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const uint32_t kk = key[j];
+    if (kk > kstar || (kk == kstar && take_eq == eq_total)) {
+      const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
+      cand[pos++] = (static_cast<uint64_t>(kk) << 32) | static_cast<uint64_t>(~col);
+    }
+  }
+  // ---- ties at K*: the take_eq lowest columns, found with an ordered scan (column = j*1024 + lane)
+  if (take_eq != eq_total) {
+    uint32_t base = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const uint32_t f = key[j] == kstar ? 1u : 0u;
+      const uint32_t incl = block_inclusive_scan(f, sh.wsum);
+      const uint32_t rank = base + incl - f;
+      if (f && rank < take_eq) {
+        const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
+        cand[n_gt + rank] = (static_cast<uint64_t>(kstar) << 32) | static_cast<uint64_t>(~col);
+      }
+      // block total of this slice = sum of the per-wave totals left in wsum by the scan
+      uint32_t tot = 0;
+      for (int w = 0; w < kTopkWaves; ++w) tot += sh.wsum[w];
+      base += tot;
+      __syncthreads();  // wsum is rewritten by the next slice's scan
+    }
+  }
+  __syncthreads();
+
+  // ---- bitonic sort of the winners (descending composite), P = pow2 >= k_sel elements, E per thread
+  int P = 2;
+  while (P < k_sel) P <<= 1;
+  if (P <= kTopkThreads) {
+    sort_and_store<1>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+  } else if (P == 2 * kTopkThreads) {
+    sort_and_store<2>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+  } else {
+    sort_and_store<4>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+  }
+}
+
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__restrict__ scores, int64_t ld,
                                                                 int64_t S, int T, int k, int causal,
@@ -245,63 +310,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
   for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;
   __syncthreads();
 
-  if (k_sel > 0) {
-    // ---- radix select of the k_sel-th largest key
-    radix_pass<KPT>(key, 0u, 0u, 21, 2048, sh, 0);
-    const uint32_t d1 = sh.digit;
-    radix_pass<KPT>(key, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
-    const uint32_t d2 = sh.digit;
-    radix_pass<KPT>(key, (d1 << 21) | (d2 << 10), 0xFFFFFC00u, 0, 1024, sh, 0);
-    const uint32_t kstar = (d1 << 21) | (d2 << 10) | sh.digit;
-    const uint32_t take_eq = sh.k_rem;          // how many keys == K* are selected (>= 1)
-    const uint32_t eq_total = sh.bucket_count;  // how many keys == K* exist
-    const uint32_t n_gt = static_cast<uint32_t>(k_sel) - take_eq;
-
-    // ---- collect keys > K* (unordered) and, if all of them are taken, keys == K*: slots from a block scan
-    uint32_t ntake = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) ntake += (key[j] > kstar || (key[j] == kstar && take_eq == eq_total)) ? 1u : 0u;
-    uint32_t pos = block_inclusive_scan(ntake, sh.wsum) - ntake;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const uint32_t kk = key[j];
-      if (kk > kstar || (kk == kstar && take_eq == eq_total)) {
-        const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
-        cand[pos++] = (static_cast<uint64_t>(kk) << 32) | static_cast<uint64_t>(~col);
-      }
-    }
-    // ---- ties at K*: the take_eq lowest columns, found with an ordered scan (column = j*1024 + lane)
-    if (take_eq != eq_total) {
-      uint32_t base = 0;
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        const uint32_t f = key[j] == kstar ? 1u : 0u;
-        const uint32_t incl = block_inclusive_scan(f, sh.wsum);
-        const uint32_t rank = base + incl - f;
-        if (f && rank < take_eq) {
-          const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
-          cand[n_gt + rank] = (static_cast<uint64_t>(kstar) << 32) | static_cast<uint64_t>(~col);
-        }
-        // block total of this slice = sum of the per-wave totals left in wsum by the scan
-        uint32_t tot = 0;
-        for (int w = 0; w < kTopkWaves; ++w) tot += sh.wsum[w];
-        base += tot;
-        __syncthreads();  // wsum is rewritten by the next slice's scan
-      }
-    }
-    __syncthreads();
-
-    // ---- bitonic sort of the winners (descending composite), P = pow2 >= k_sel elements, E per thread
-    int P = 2;
-    while (P < k_sel) P <<= 1;
-    if (P <= kTopkThreads) {
-      sort_and_store<1>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
-    } else if (P == 2 * kTopkThreads) {
-      sort_and_store<2>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
-    } else {
-      sort_and_store<4>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
-    }
-  }
+  if (k_sel > 0) select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh);
 
   // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order)
   for (int j = k_sel + tid; j < k; j += kTopkThreads)
@@ -320,6 +329,316 @@ int launch_topk(const float *scores, int64_t ld, int64_t rows, int64_t S, int T,
   return KS_OK;
 }
 
+
+// ---------------------------------------------------------------- rows of bounded scores
+// Inverse of score_key for keys of finite scores.
+__device__ __forceinline__ float key_score(uint32_t key) {
+  return __builtin_bit_cast(float, (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+}
+
+constexpr int kRecD = 128;        // head dim of the recomputation
+constexpr int kRecH = 64;         // heads
+constexpr int kRecC = kRecD / 8;  // 16-byte chunks per row
+
+// The row's query (64 heads) staged once per workgroup: rows in LDS with a 16-byte XOR swizzle (chunk c of
+// head h at c ^ (h & 15): the 16 lanes reading one chunk of 16 heads hit distinct banks), and the head
+// weights and statistics.
+struct RecShared {
+  uint4 q[kRecH * kRecC];
+  float w[kRecH];
+  float qn[kRecH];
+  int32_t qsp[kRecH];
+};
+
+__device__ __forceinline__ uint4 rec_q(const RecShared &rs, int h, int c) { return rs.q[h * kRecC + (c ^ (h & 15))]; }
+
+// Per-wave scratch of the recomputation: the tile's 16 key rows (row-major, 16-byte XOR swizzle) and the
+// tile's near-tie dot list with the exact values.
+constexpr int kNearCap = 256;  // near-tie dots listed at a time (a tile has at most 64 x 16)
+struct RecWave {
+  uint4 k[16 * kRecC];
+  uint16_t ent[kNearCap];  // lane << 4 | head bit (4 m + r); overwritten by the dot's exact value
+};
+
+// Exact scores of the keys list[0 .. n) of one row, by the canonical contract, written over the row's
+// scores (srow, the workspace copy the selection reads next).  Each wave takes tiles of 16 keys: four
+// 16-head MFMA rounds (heads 16m + 4g + r, m = 0..3) with the score kernel's interval test (same
+// half-widths: bound_c 2^-23 ||q_h|| times the key block's norm maximum) keep the relu'd lower ends of all
+// 64 heads; the tile's near-tie dots are then recomputed exactly, 16 at a time with a quad of lanes per dot
+// (q_h and the key row from LDS: exact_dot_bf16's arithmetic), and the fp32 fma head sum runs in the
+// canonical order over the corrected values.
+__device__ void recompute_scores(const int32_t *list, int n, float *srow, const TopkRecompute &rc,
+                                 const RecShared &rs, RecWave &rw, int64_t kbrow0, int64_t kmax_row0,
+                                 uint32_t &n_exact, uint32_t &n_unres) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int ntile = (n + 15) / 16;
+  for (int t = wave; t < ntile; t += kTopkWaves) {
+    const int li = 16 * t + l16;
+    const bool kv = li < n;
+    const int col = list[kv ? li : n - 1];
+    const int64_t krow = kbrow0 + col;
+    uint4 kb[kRecD / 32];
+#pragma unroll
+    for (int kk = 0; kk < kRecD / 32; ++kk) {
+      kb[kk] = *reinterpret_cast<const uint4 *>(rc.k + krow * kRecD + 32 * kk + 8 * g);
+      rw.k[l16 * kRecC + ((4 * kk + g) ^ l16)] = kb[kk];
+    }
+    const float knm = rc.kmax[kmax_row0 + col / kScoreKeyBlock];
+    uint32_t pl[8];     // relu'd lower ends, heads 16m + 4g + (0, 1) | (2, 3): pl[2m], pl[2m + 1]
+    uint32_t ntm = 0;   // bit 4m + r: head 16m + 4g + r is a near tie
+#pragma unroll
+    for (int m = 0; m < kRecH / 16; ++m) {
+      f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < kRecD / 32; ++kk) acc = mfma16(rec_q(rs, 16 * m + l16, 4 * kk + g), kb[kk], acc);
+#pragma unroll
+      for (int rp = 0; rp < 2; ++rp) {
+        const int h0 = 16 * m + 4 * g + 2 * rp;
+        const float d0 = rc.bound_c * 0x1p-23f * rs.qn[h0] * knm, d1 = rc.bound_c * 0x1p-23f * rs.qn[h0 + 1] * knm;
+        const uint32_t lo = cvt_relu_pk(acc[2 * rp] - d0, acc[2 * rp + 1] - d1);
+        const uint32_t hi = cvt_relu_pk(acc[2 * rp] + d0, acc[2 * rp + 1] + d1);
+        pl[2 * m + rp] = lo;
+        const uint32_t x = lo ^ hi;
+        ntm |= ((x & 0xFFFFu) != 0u && kv ? 1u : 0u) << (4 * m + 2 * rp);
+        ntm |= ((x >> 16) != 0u && kv ? 1u : 0u) << (4 * m + 2 * rp + 1);
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(ntm != 0u) != 0ull) {
+      const uint32_t cnt = __builtin_popcount(ntm);
+      const uint32_t incl = wave_incl_scan(cnt);
+      const int nd = static_cast<int>(__builtin_amdgcn_readlane(incl, 63));
+      const int pos0 = static_cast<int>(incl - cnt);
+      const int dq = lane >> 2, sub = lane & 3;
+      for (int s0 = 0; s0 < nd; s0 += kNearCap) {  // list segments of kNearCap dots
+        const int ns = nd - s0 < kNearCap ? nd - s0 : kNearCap;
+        {
+          uint32_t mm = ntm;
+          int p = pos0;
+          while (mm) {
+            const int bit = __builtin_ctz(mm);
+            mm &= mm - 1;
+            if (p >= s0 && p < s0 + ns) rw.ent[p - s0] = static_cast<uint16_t>((lane << 4) | bit);
+            ++p;
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int b0 = 0; b0 < ns; b0 += 16) {
+          const int e = rw.ent[min(b0 + dq, ns - 1)];
+          const int sl = e >> 4, bit = e & 15;
+          const int h = 16 * (bit >> 2) + 4 * (sl >> 4) + (bit & 3), kl = sl & 15;
+          const int li2 = 16 * t + kl;
+          const int64_t kr2 = kbrow0 + list[li2 < n ? li2 : n - 1];
+          const int span = rs.qsp[h] + rc.ksp[kr2];
+          const bool split = span > 52;
+          double hi = 0.0, lo = 0.0;
+          if (__builtin_amdgcn_ballot_w64(split) == 0ull) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const uint4 qv = rec_q(rs, h, 4 * sub + c);
+              const uint4 kv4 = rw.k[kl * kRecC + ((4 * sub + c) ^ kl)];
+              const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+              const uint32_t kw[4] = {kv4.x, kv4.y, kv4.z, kv4.w};
+#pragma unroll
+              for (int p = 0; p < 4; ++p) {
+                hi = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), hi);
+                hi = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), hi);
+              }
+            }
+          } else {
+            // wide dynamic range (rare): products above / below 2^(top - 38) accumulate separately
+            const double thr = split ? ldexp(1.0, frexp_exp(rs.qn[h]) + frexp_exp(rc.kn[kr2]) - 38) : 0.0;
+#pragma unroll 1
+            for (int c = 0; c < 4; ++c) {
+              const uint4 qv = rec_q(rs, h, 4 * sub + c);
+              const uint4 kv4 = rw.k[kl * kRecC + ((4 * sub + c) ^ kl)];
+              const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+              const uint32_t kw[4] = {kv4.x, kv4.y, kv4.z, kv4.w};
+#pragma unroll
+              for (int p = 0; p < 4; ++p) {
+                const double p0 = static_cast<double>(unpack_lo(qw[p])) * static_cast<double>(unpack_lo(kw[p]));
+                const double p1 = static_cast<double>(unpack_hi(qw[p])) * static_cast<double>(unpack_hi(kw[p]));
+                if (!split || fabs(p0) >= thr) hi += p0; else lo += p0;
+                if (!split || fabs(p1) >= thr) hi += p1; else lo += p1;
+              }
+            }
+          }
+          hi = quad_sum_f64(hi);
+          lo = quad_sum_f64(lo);
+          uint16_t v;
+          if (!split && (hi == 0.0 || (fabs(hi) >= 0x1p-126 && fabs(hi) < 0x1p127))) v = round_to_bf16_fast(hi);
+          else v = round2_to_bf16(hi, lo);
+          const uint16_t rv = (v & 0x8000u) ? 0 : v;  // ReLU (also maps -0 to +0)
+          // each quad reads only its own entry before this write (the value replaces the entry)
+          if (sub == 0 && b0 + dq < ns) rw.ent[b0 + dq] = span <= 84 ? rv : 0xFFFFu;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        uint32_t mm = ntm;
+        int p = pos0;
+        while (mm) {
+          const int bit = __builtin_ctz(mm);
+          mm &= mm - 1;
+          if (p >= s0 && p < s0 + ns) {
+            const uint16_t v = rw.ent[p - s0];
+            if (v != 0xFFFFu) {
+              const int m = bit >> 2, r = bit & 3;
+              const uint32_t sh = (r & 1) ? 16u : 0u;
+              uint32_t &word = pl[2 * m + (r >> 1)];
+              word = (word & ~(0xFFFFu << sh)) | (static_cast<uint32_t>(v) << sh);
+              ++n_exact;
+            } else {
+              ++n_unres;
+            }
+          }
+          ++p;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    }
+    float G = 0.f;
+#pragma unroll
+    for (int m = 0; m < kRecH / 16; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t p2 = pl[2 * m + (r >> 1)];
+        G = __builtin_fmaf((r & 1) ? unpack_hi(p2) : unpack_lo(p2), rs.w[16 * m + 4 * g + r], G);
+      }
+    const float tot = combine_groups(G);
+    if (g == 0 && kv) srow[col] = tot;
+  }
+}
+
+// One 1024-lane workgroup per row of bounded scores: lower ends lo = score - U select a threshold tau (the
+// bucket edge, two radix passes deep, of the k-th largest lo: no exact score of the k largest lies below
+// it); every score with U > 0 whose upper end reaches tau is recomputed exactly (in batches of the list
+// capacity); the row's keys then hold exact scores wherever they can matter, and the exact selection runs
+// on them.  A score with U > 0 below tau keeps its stale value, which lies below tau as well.
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float *scores, int64_t ld,
+                                                                   int64_t S, int T, int k, int causal,
+                                                                   int64_t start_pos, int ratio, int64_t offset,
+                                                                   void *__restrict__ out, int out_i64,
+                                                                   TopkRecompute rc, int lcap) {
+  extern __shared__ uint64_t cand[];  // the recomputation list first, then the selection's candidates
+  __shared__ SelShared sh;
+  __shared__ RecShared rs;
+  __shared__ RecWave rw[kTopkWaves];
+  const int64_t row = blockIdx.x;
+  const int64_t s = row % S, b = row / S;
+  const int tid = threadIdx.x;
+  int64_t limit = INT64_MAX;
+  int n_valid = T;
+  if (causal) {
+    limit = (start_pos + s + 1) / ratio;
+    n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
+  }
+  const int k_sel = k < n_valid ? k : n_valid;
+  const float *src = scores + row * ld;
+  const float *ub = rc.bounds + row * ld;
+
+  uint32_t key[KPT], lok[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int col = j * kTopkThreads + tid;
+    const bool v = col < n_valid;
+    const float sv = v ? src[col] : 0.f;
+    const float uv = v ? ub[col] : 0.f;
+    key[j] = v ? score_key(sv) : 0u;
+    lok[j] = v ? score_key(uv > 0.f ? sv - uv : sv) : 0u;
+  }
+  if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
+  for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;
+  __syncthreads();
+
+  if (k_sel > 0) {
+    // ---- tau: lower edge of the 22-bit bucket holding the k_sel-th largest lower end
+    radix_pass<KPT>(lok, 0u, 0u, 21, 2048, sh, 0);
+    const uint32_t d1 = sh.digit;
+    radix_pass<KPT>(lok, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
+    const uint32_t tau = (d1 << 21) | (sh.digit << 10);
+    // ---- scores to recompute: U > 0 and score + U >= tau; list ranks from a block scan
+    uint32_t cmask = 0;  // (the bounds are read again: keeping them would double the row's registers)
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int col = j * kTopkThreads + tid;
+      const float uv = col < n_valid ? ub[col] : 0.f;
+      if (uv > 0.f && score_key(key_score(key[j]) + uv) >= tau) cmask |= 1u << j;
+    }
+    const uint32_t cnt = __builtin_popcount(cmask);
+    const uint32_t base = block_inclusive_scan(cnt, sh.wsum) - cnt;
+    uint32_t ncand = 0;
+    for (int w = 0; w < kTopkWaves; ++w) ncand += sh.wsum[w];
+    int32_t *list = reinterpret_cast<int32_t *>(cand);
+    const int64_t qrow0 = row * kRecH;  // rows of q, w and the q statistics: (b S + s) 64 + head
+    const int64_t kbrow0 = b * rc.kbs;
+    if (ncand > 0) {
+      for (int i = tid; i < kRecH * kRecC; i += kTopkThreads) {
+        const int h = i / kRecC, c = i % kRecC;
+        rs.q[h * kRecC + (c ^ (h & 15))] = *reinterpret_cast<const uint4 *>(rc.q + (qrow0 + h) * kRecD + 8 * c);
+      }
+      if (tid < kRecH) {
+        rs.w[tid] = rc.w[qrow0 + tid];
+        rs.qn[tid] = rc.qn[qrow0 + tid];
+        rs.qsp[tid] = rc.qsp[qrow0 + tid];
+      }
+    }
+    const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
+    float *srow = const_cast<float *>(src);
+    uint32_t n_exact = 0, n_unres = 0;
+    for (uint32_t b0 = 0; b0 < ncand; b0 += static_cast<uint32_t>(lcap)) {
+      const uint32_t nb = ncand - b0 < static_cast<uint32_t>(lcap) ? ncand - b0 : static_cast<uint32_t>(lcap);
+      uint32_t p = base, mm = cmask;
+      while (mm) {
+        const int j = __builtin_ctz(mm);
+        mm &= mm - 1;
+        if (p >= b0 && p < b0 + nb) list[p - b0] = j * kTopkThreads + tid;
+        ++p;
+      }
+      __syncthreads();
+      recompute_scores(list, static_cast<int>(nb), srow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0, n_exact, n_unres);
+      __syncthreads();  // the list is rewritten by the next batch; the recomputed scores are visible
+    }
+    // the row again, now exact wherever it can matter (the workgroup's waves share one L1: the barrier
+    // above orders the rewrites before these loads)
+    // (every key is reloaded, so that none stays live in registers through the recomputation)
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int col = j * kTopkThreads + tid;
+      key[j] = col < n_valid ? score_key(srow[col]) : 0u;
+    }
+    if (rc.stats != nullptr) {
+      if (n_exact) atomicAdd(&rc.stats[0], n_exact);
+      if (n_unres) atomicAdd(&rc.stats[1], n_unres);
+      if (rc.stats_ext && tid == 0) atomicAdd(&rc.stats[2], ncand);
+    }
+    // ---- exact selection; hist[0] was cleared by the second pass above
+    if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
+    __syncthreads();
+    select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh);
+  }
+
+  // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order)
+  for (int j = k_sel + tid; j < k; j += kTopkThreads)
+    store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
+}
+
+template <int KPT>
+int launch_topk_bounded(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
+                        int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, const TopkRecompute &rc,
+                        hipStream_t stream) {
+  int P = 2;
+  while (P < k) P <<= 1;
+  // dynamic LDS: the selection's 2P composites, or the recomputation list (4P columns)
+  const int lcap = 4 * P;
+  const size_t shmem = static_cast<size_t>(2 * P) * sizeof(uint64_t);
+  hipLaunchKernelGGL(topk_bounded_kernel<KPT>, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, stream,
+                     scores, ld, S, T, k, causal, start_pos, ratio, offset, out, out_i64, rc, lcap);
+  KS_CHECK_LAUNCH("topk_bounded_kernel");
+  return KS_OK;
+}
 }  // namespace
 }  // namespace ks
 
@@ -349,4 +668,24 @@ extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64
   if (T <= 16384) return ks::launch_topk<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   if (T <= 32768) return ks::launch_topk<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   return ks::launch_topk<64>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+}
+
+int ks::launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
+                                    int causal, int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
+                                    const TopkRecompute &rc, hipStream_t st) {
+  KS_CHECK_ARG(B >= 0 && S >= 0 && T >= 1 && T <= 65536 && k >= 1 && k <= T && k <= kTopkMaxK && ld >= T &&
+                   ratio >= 1 && start_pos >= 0,
+               "indexer top-k (bounded): bad arguments");
+  const int64_t rows = B * S;
+  if (rows == 0) return KS_OK;
+  KS_CHECK_ARG(rows < (int64_t(1) << 31), "indexer top-k (bounded): too many rows");
+  const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
+  const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
+  if (T <= 1024) return launch_topk_bounded<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  if (T <= 2048) return launch_topk_bounded<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  if (T <= 4096) return launch_topk_bounded<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  if (T <= 8192) return launch_topk_bounded<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  if (T <= 16384)
+    return launch_topk_bounded<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  return launch_topk_bounded<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
 }

@@ -274,3 +274,65 @@ def test_indexer_adversarial(device, dist):
     tab = workloads.freqs_table(64, 2048)
     print(f"[case] indexer adversarial {dist}", flush=True)
     _indexer_vs_oracle(q, k, w, tab, 256, True, 1024 - 16, 1, 0, 0, 64, True, 1024)
+
+
+def _dbg_indexer(q, k, w, tab, k_top, causal, start_pos, path, bound_c=3.0, T=None):
+    """ks_dbg_indexer: path 1 = exact scores, 2 = bounded scores with exact recomputation in the top-k.
+    Returns (indices, [exact dot recomputations, dots outside the exact range])."""
+    B, S, H, D = q.shape
+    T = k.shape[1] if T is None else T
+    qd, kd, wd, td = q.to("cuda"), k.to("cuda"), w.to("cuda"), tab.to("cuda")
+    ws = torch.empty(ops.indexer_workspace_size(B, S, H, D, T), dtype=torch.uint8, device="cuda")
+    kk = min(k_top, T)
+    out = torch.empty(B, S, kk, dtype=torch.int32, device="cuda")
+    st = torch.zeros(2, dtype=torch.int32, device="cuda")
+    rc = _lib.load().ks_dbg_indexer(qd.data_ptr(), kd.data_ptr(), wd.data_ptr(), 0, td.data_ptr(), tab.shape[0], 0, 64,
+                                    1, k_top, 1 if causal else 0, start_pos, 1, 0, out.data_ptr(), 0, B, S, H, D, T, T,
+                                    ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream, bound_c,
+                                    st.data_ptr(), path)
+    _lib.check(rc, "ks_dbg_indexer")
+    torch.cuda.synchronize()
+    return out.cpu().numpy().astype(np.int64), st.cpu().numpy()
+
+
+@pytest.mark.parametrize("S,T,k_top,start_pos", [(24, 3000, 64, 2976), (7, 700, 700, 0), (33, 1500, 512, 4000)])
+def test_indexer_bounded_recompute_everything(device, S, T, k_top, start_pos):
+    # a huge interval constant makes every positive dot a near tie: every score carries a bound, every key
+    # reaching the threshold is recomputed (the list is refilled in several batches), and the exact dots go
+    # through the double-precision path; the result must still be the oracle's, bit for bit
+    g = torch.Generator().manual_seed(S + T)
+    q = torch.randn(1, S, 64, 128, generator=g).bfloat16()
+    k = torch.randn(1, T, 128, generator=g).bfloat16()
+    w = torch.randn(1, S, 64, generator=g) / 8
+    tab = workloads.freqs_table(64, max(T, start_pos + S) + 1)
+    causal = start_pos < 4000
+    sp = start_pos if causal else 0
+    print(f"[case] bounded recompute-all S={S} T={T} k={k_top} causal={causal}", flush=True)
+    got, st = _dbg_indexer(q, k, w, tab, k_top, causal, sp, 2, bound_c=1e6)
+    want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), k_top, causal, sp, 1, 0, 0, 64, True)
+    np.testing.assert_array_equal(got, want)
+    assert st[0] > 0 and st[1] == 0
+
+
+@pytest.mark.parametrize("dist", ["normal", "scaled", "midpoints"])
+def test_indexer_bounded_equals_exact_path(device, dist):
+    # the two score paths select identical indices (and both equal the oracle's)
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(2, 20, 64, 128, generator=g)
+    k = torch.randn(2, 2048, 128, generator=g)
+    if dist == "scaled":
+        q = q * torch.exp2(torch.randint(-6, 7, (2, 20, 64, 1), generator=g).float())
+        k = k * torch.exp2(torch.randint(-6, 7, (2, 2048, 1), generator=g).float())
+    elif dist == "midpoints":
+        q = torch.randint(-3, 4, q.shape, generator=g).float()
+        k = torch.randint(-3, 4, k.shape, generator=g).float()
+    q, k = q.bfloat16(), k.bfloat16()
+    w = torch.randn(2, 20, 64, generator=g) / 8
+    tab = workloads.freqs_table(64, 2048)
+    print(f"[case] bounded vs exact path {dist}", flush=True)
+    exact, _ = _dbg_indexer(q, k, w, tab, 512, True, 2048 - 20, 1)
+    bounded, st = _dbg_indexer(q, k, w, tab, 512, True, 2048 - 20, 2)
+    np.testing.assert_array_equal(bounded, exact)
+    want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), 512, True, 2048 - 20, 1, 0, 0, 64, True)
+    np.testing.assert_array_equal(bounded, want)
+    print(f"[info] bounded path: {int(st[0])} exact dot recomputations", flush=True)

@@ -173,24 +173,43 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
     dev_med, dev_mean = _events_median(step, steps, warmup)
     wall_med, ms_step = _wall(step, steps, warmup)
 
-    # dominant kernel alone: exact scores on pre-rotated inputs
+    # the fused call's kernels alone, on pre-rotated inputs: the bounded score kernel (the dominant one), the
+    # bounded top-k (threshold, exact recomputation of the candidates, exact selection), and for reference
+    # the exact score kernel and the plain top-k of the other shapes
     qr = t["q"].clone()
     kr = t["k"].clone()
     ops.rope_inplace(qr, t["freqs"], rope_start=0, pos0=p["start_pos"])
     ops.rope_inplace(kr, t["freqs"], rope_start=0, pos0=0)
     stats = (ops.indexer_row_stats(qr), ops.indexer_row_stats(kr))
     out = torch.empty(B, S, T, dtype=torch.float32, device="cuda")
+    bnd = torch.empty(B, S, T, dtype=torch.float32, device="cuda")
+    kmax = torch.empty(B, (T + 255) // 256, dtype=torch.float32, device="cuda")
+    idx = torch.empty(B, S, min(p["k_top"], T), dtype=torch.int32, device="cuda")
     from kernelswift_amd import _lib
     lib = _lib.load()
     (qn, qs), (kn, ks_) = stats
     stream = torch.cuda.current_stream().cuda_stream
 
-    def scores():
+    def scores_bounded():
+        _lib.check(lib.ks_dbg_indexer_scores_bounded(qr.data_ptr(), kr.data_ptr(), t["w"].data_ptr(), qn.data_ptr(),
+                                                     qs.data_ptr(), kn.data_ptr(), ks_.data_ptr(), out.data_ptr(),
+                                                     bnd.data_ptr(), kmax.data_ptr(), B, S, T, 1, p["start_pos"],
+                                                     stream), "scores (bounded)")
+
+    def topk_bounded():
+        _lib.check(lib.ks_dbg_indexer_topk_bounded(out.data_ptr(), bnd.data_ptr(), kmax.data_ptr(), qr.data_ptr(),
+                                                   kr.data_ptr(), t["w"].data_ptr(), qn.data_ptr(), qs.data_ptr(),
+                                                   kn.data_ptr(), ks_.data_ptr(), B, S, T, p["k_top"], 1,
+                                                   p["start_pos"], idx.data_ptr(), stream), "top-k (bounded)")
+
+    def scores_exact():
         _lib.check(lib.ks_indexer_scores(qr.data_ptr(), kr.data_ptr(), t["w"].data_ptr(), 0, qn.data_ptr(),
                                          qs.data_ptr(), kn.data_ptr(), ks_.data_ptr(), out.data_ptr(), B, S, H, D, T,
                                          T, 1, p["start_pos"], 1, stream), "scores")
 
-    score_us = _events_avg(scores, steps, warmup)
+    score_us = _events_avg(scores_bounded, steps, warmup)
+    topkb_us = _events_avg(topk_bounded, steps, warmup)
+    exact_us = _events_avg(scores_exact, steps, warmup)
     sc = out.clone()
 
     def topk():
@@ -202,10 +221,13 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
     res = {
         "us_per_call": round(dev_med, 3), "us_per_call_mean": round(dev_mean, 3),
         "wall_us_per_call_sync": round(wall_med, 3), "ms_per_step": ms_step,
-        "kernels_us": {"indexer_scores_kernel": round(score_us, 3), "topk_rows_kernel": round(topk_us, 3)},
-        "roofline": {"bound": "mfma", "kernel": "indexer_scores_kernel", "achieved": round(achieved, 2),
+        "kernels_us": {"indexer_scores_kernel (bounded)": round(score_us, 3),
+                       "topk_bounded_kernel": round(topkb_us, 3),
+                       "indexer_scores_kernel (exact, other shapes)": round(exact_us, 3),
+                       "topk_rows_kernel (plain, other shapes)": round(topk_us, 3)},
+        "roofline": {"bound": "mfma", "kernel": "indexer_scores_kernel (bounded)", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic(f"indexer_scores_kernel@cfg{cfg}")},
+                     "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true>@cfg{cfg}")},
         "topk_score_GBps": round(S * T * 4 / (topk_us * 1e-6) / 1e9, 1),
     }
     if do_cpu:
@@ -293,7 +315,8 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
            "kernels_us": {"sparse_attn_kernel+combine": round(op_us, 3)},
            "roofline": {"bound": "mfma", "kernel": "sparse_attn_kernel (+ combine)", "achieved": round(achieved, 2),
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                        "traffic": _traffic(f"sparse_attn_kernel@cfg{cfg}"),
+                        "traffic": _traffic(("sparse_attn_kernel<128, 128, 1>" if cfg == 3
+                                             else "sparse_attn_kernel<576, 512, 8>") + f"@cfg{cfg}"),
                         "cache": ("warm (the 2 MiB kv fits in L2)" if cfg == 3
                                   else "kv 2.25 GiB: gathered rows come from HBM")},
            "gathered_GBps": round(gathered / (op_us * 1e-6) / 1e9, 1)}

@@ -137,6 +137,10 @@ int ks_indexer_row_stats(const uint16_t *x, int64_t rows, int64_t D, float *norm
  * 256-byte aligned.  Shapes as ks_indexer_scores: q bf16 [B, S, H, D] with
  * D in {64, 128} and H in {16, 32, 64}; batch b's T key rows start at
  * k + b*k_batch_stride*D; w [B, S, H]; T <= 65536.
+ * With H = 64, D = 128, fp32 weights, T <= 32768 and min(k_top, T) <= 2048
+ * the scores are computed with per-score bounds and only the scores that can
+ * reach the top k are recomputed exactly (inside the top-k kernel); the
+ * returned indices are those of the exact path.
  * ---------------------------------------------------------------------- */
 size_t ks_indexer_workspace_size(int64_t B, int64_t S, int64_t H, int64_t D,
                                  int64_t T);

@@ -617,3 +617,21 @@ extern "C" int ks_dbg_indexer_scores(const uint16_t *q, const uint16_t *k, const
                                    T, k_batch_stride, causal ? 1 : 0, start_pos, ratio, bound_c, stats,
                                    static_cast<hipStream_t>(stream));
 }
+
+// Diagnostic variant of the bounded score kernel (not part of the public header), for timing it alone:
+// as ks_dbg_indexer_scores with fp32 weights, 64 heads and D = 128, plus the per-score bounds [B, S, T]
+// and the key-block norm maxima [B, ceil(T / 256)].
+extern "C" int ks_dbg_indexer_scores_bounded(const uint16_t *q, const uint16_t *k, const float *w,
+                                             const float *q_norm, const int32_t *q_span, const float *k_norm,
+                                             const int32_t *k_span, float *scores, float *bounds, float *kmax,
+                                             int64_t B, int64_t S, int64_t T, int32_t causal, int64_t start_pos,
+                                             void *stream) {
+  ks::last_error().clear();
+  int rc = check_scores_args(q, k, w, q_norm, q_span, k_norm, k_span, scores, B, S, 64, 128, T, T, 1, start_pos);
+  if (rc != KS_OK) return rc;
+  KS_CHECK_ARG(bounds && kmax, "ks_dbg_indexer_scores_bounded: null pointer");
+  if (B * S == 0) return KS_OK;
+  return ks::launch_indexer_scores(q, k, w, 0, q_norm, q_span, k_norm, k_span, scores, B, S, 64, 128, T, T,
+                                   causal ? 1 : 0, start_pos, 1, ks::kScoreBoundC, nullptr,
+                                   static_cast<hipStream_t>(stream), bounds, kmax);
+}

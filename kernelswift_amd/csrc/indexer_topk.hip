@@ -515,7 +515,8 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
 // bucket edge, two radix passes deep, of the k-th largest lo: no exact score of the k largest lies below
 // it); every score with U > 0 whose upper end reaches tau is recomputed exactly (in batches of the list
 // capacity); the row's keys then hold exact scores wherever they can matter, and the exact selection runs
-// on them.  A score with U > 0 below tau keeps its stale value, which lies below tau as well.
+// on them.  A score with U > 0 whose upper end is below tau enters the selection as that upper end: below
+// tau, so below every exact score of the k largest, like the exact score itself.
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float *scores, int64_t ld,
                                                                    int64_t S, int T, int k, int causal,
@@ -539,15 +540,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
   const float *src = scores + row * ld;
   const float *ub = rc.bounds + row * ld;
 
-  uint32_t key[KPT], lok[KPT];
+  // keys of the lower and upper ends (equal, and exact, where the bound is 0)
+  uint32_t lok[KPT], hik[KPT];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const int col = j * kTopkThreads + tid;
     const bool v = col < n_valid;
     const float sv = v ? src[col] : 0.f;
     const float uv = v ? ub[col] : 0.f;
-    key[j] = v ? score_key(sv) : 0u;
     lok[j] = v ? score_key(uv > 0.f ? sv - uv : sv) : 0u;
+    hik[j] = v ? score_key(uv > 0.f ? sv + uv : sv) : 0u;
   }
   if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
   for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;
@@ -560,13 +562,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     radix_pass<KPT>(lok, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
     const uint32_t tau = (d1 << 21) | (sh.digit << 10);
     // ---- scores to recompute: U > 0 and score + U >= tau; list ranks from a block scan
-    uint32_t cmask = 0;  // (the bounds are read again: keeping them would double the row's registers)
+    uint32_t cmask = 0;
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const int col = j * kTopkThreads + tid;
-      const float uv = col < n_valid ? ub[col] : 0.f;
-      if (uv > 0.f && score_key(key_score(key[j]) + uv) >= tau) cmask |= 1u << j;
-    }
+    for (int j = 0; j < KPT; ++j)
+      if (lok[j] != hik[j] && hik[j] >= tau) cmask |= 1u << j;
     const uint32_t cnt = __builtin_popcount(cmask);
     const uint32_t base = block_inclusive_scan(cnt, sh.wsum) - cnt;
     uint32_t ncand = 0;
@@ -601,14 +600,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
       recompute_scores(list, static_cast<int>(nb), srow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0, n_exact, n_unres);
       __syncthreads();  // the list is rewritten by the next batch; the recomputed scores are visible
     }
-    // the row again, now exact wherever it can matter (the workgroup's waves share one L1: the barrier
-    // above orders the rewrites before these loads)
-    // (every key is reloaded, so that none stays live in registers through the recomputation)
+    // the selection's keys: recomputed scores from the row (the workgroup's waves share one L1: the
+    // barrier above orders the rewrites before these loads), exact scores where the bound is 0, and for
+    // the other bounded scores the upper end, which lies below tau like the score itself
+    uint32_t key[KPT];
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const int col = j * kTopkThreads + tid;
-      key[j] = col < n_valid ? score_key(srow[col]) : 0u;
-    }
+    for (int j = 0; j < KPT; ++j)
+      key[j] = ((cmask >> j) & 1u) ? score_key(srow[j * kTopkThreads + tid]) : hik[j];
     if (rc.stats != nullptr) {
       if (n_exact) atomicAdd(&rc.stats[0], n_exact);
       if (n_unres) atomicAdd(&rc.stats[1], n_unres);
@@ -688,4 +686,21 @@ int ks::launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, 
   if (T <= 16384)
     return launch_topk_bounded<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
   return launch_topk_bounded<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+}
+
+// Diagnostic entry (not part of the public header) of the bounded top-k, for timing it alone: scores and
+// bounds from ks_dbg_indexer_scores_bounded over rotated q / k (with their row statistics); the scores
+// that are recomputed are rewritten in place.  ratio 1, int32 output.
+extern "C" int ks_dbg_indexer_topk_bounded(float *scores, const float *bounds, const float *kmax, const uint16_t *q,
+                                           const uint16_t *k, const float *w, const float *q_norm,
+                                           const int32_t *q_span, const float *k_norm, const int32_t *k_span,
+                                           int64_t B, int64_t S, int64_t T, int64_t k_top, int32_t causal,
+                                           int64_t start_pos, void *out, void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(scores && bounds && kmax && q && k && w && q_norm && q_span && k_norm && k_span && out,
+               "ks_dbg_indexer_topk_bounded: null pointer");
+  KS_CHECK_ARG(T <= 32768 && k_top <= 2048, "ks_dbg_indexer_topk_bounded: T <= 32768 and k <= 2048");
+  const ks::TopkRecompute rc{bounds, kmax, q, k, w, q_norm, q_span, k_norm, k_span, T, ks::kScoreBoundC, nullptr, 0};
+  return ks::launch_indexer_topk_bounded(scores, T, B, S, T, k_top, causal ? 1 : 0, start_pos, 1, 0, out, 0, rc,
+                                         static_cast<hipStream_t>(stream));
 }

@@ -22,6 +22,8 @@
 //          nor transposed.
 // One range per query finalises in place (sink added, bf16 store); otherwise partial (O, max, sum) go to
 // the workspace and a combine kernel merges the ranges with the sink (one wave per output row).
+// MLA-shaped heads (Dqk 576, Dv 512, H a multiple of 32) use sparse_attn_mla_kernel below: 32 heads per
+// wave, one wave per SIMD, O accumulated in AGPRs.
 #include "common.h"
 
 namespace ks {
@@ -469,6 +471,346 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// MLA-shaped heads (Dqk = 576, Dv = 512, H = 32 NW): one work item per workgroup of NW waves, 32 heads per
+// wave (two 16-head tiles), one wave per SIMD.  Each K fragment and each V fragment read from LDS feeds two
+// MFMAs (one per head tile), which halves the LDS read traffic per flop of a 16-head wave, and a wave
+// alone on its SIMD has 512 registers: the 16 x 512 fp32 O accumulators of both tiles (256) and the q
+// B-fragments (144) fit with room left for reading fragments ahead.  The item's row indices are validated
+// once into LDS (-1 = invalid), so the only vector-memory operations in the chunk loop are the gathers,
+// and an NBUF-deep ring keeps NBUF - 1 chunks in flight with per-wave s_waitcnt vmcnt(n).
+template <int NW, int NBUF>
+struct MlaShape {
+  static constexpr int DQK = 576, DV = 512;
+  static constexpr int UPR = DQK / 8;       // 72 16-byte units per row
+  static constexpr int UNITS = kKC * UPR;   // 2304 per chunk
+  static constexpr int TI = UNITS / 64;     // 36 DMA instructions per chunk
+  static constexpr int NJ = TI / NW;        // per wave
+  static constexpr int BUF = UNITS * 8;     // bf16 elements per chunk buffer
+  static constexpr int QJ = DQK / 32;       // k-steps of the QK MFMA
+  static constexpr int CT = DV / 16;        // dv column tiles
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int KR_MAX = 2048;       // keys per work item (indices staged in LDS)
+  // q B-fragments: the first QREG k-steps of both head tiles in VGPRs, the last QL in LDS
+  static constexpr int QL = 4;
+  static constexpr int QREG = QJ - QL;
+  static_assert(TI % NW == 0, "every wave issues the same number of DMA instructions");
+  static constexpr int QS = QL > 0 ? NW * QL * 2 * 64 : 1;  // uint4 slots of q in LDS
+  static_assert(NBUF * BUF * 2 + KR_MAX * 4 + (QS + NW * 64) * 16 <= 160 * 1024, "LDS budget");
+  // same swizzle as SaShape<576, 512, *>: unit u of key k at k*UPR + (u ^ (k & 7)) for the low 3 bits
+  __device__ static __forceinline__ int slot(int k, int u_hi, int u_lo) { return k * UPR + u_hi + (u_lo ^ (k & 7)); }
+};
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// O += A B with the accumulator held in AGPRs ("+a"): the compiler would otherwise move the 256 accumulator
+// registers between the register files on every iteration.  Inline assembly is invisible to the compiler's
+// hazard tracking, so the callers order it with explicit NOPs: VALU writes of A, B or the accumulator
+// (P packing, rescaling) are followed by >= 2 wait states before the first such MFMA (mfma_agpr_enter),
+// and >= 19 wait states separate the last one from any read of its results (mfma_agpr_leave).
+__device__ __forceinline__ void mfma16_agpr(f32x4_t &acc, uint4 a, uint4 b) {
+  const u32x4_t va = {a.x, a.y, a.z, a.w}, vb = {b.x, b.y, b.z, b.w};
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(va), "v"(vb));
+}
+
+// acc[r] *= s[r] for an accumulator held in AGPRs (AGPRs are not VALU operands): the tuple moves to VGPRs
+// and back through the lane's 16-byte LDS slot `slot` (DS writes take AGPR data, ds_read_b128 fills AGPRs),
+// so the accumulator is only ever read and defined in the AGPR class; plain copies let the compiler hoist
+// the moves of all 256 accumulators out of the rarely taken rescale branch and spill.
+__device__ __forceinline__ void scale_agpr(f32x4_t &acc, const float (&s)[4], uint32_t slot) {
+  f32x4_t t;
+  asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(t)
+               : "v"(slot), "a"(acc)
+               : "memory");
+  t *= f32x4_t{s[0], s[1], s[2], s[3]};
+  asm volatile("ds_write_b128 %1, %2\n\ts_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+               : "=a"(acc)
+               : "v"(slot), "v"(t)
+               : "memory");
+}
+
+// The same with the accumulator in VGPRs (scores, read by the softmax): fenced by mfma_vgpr_enter/leave.
+__device__ __forceinline__ void mfma16_vgpr(f32x4_t &acc, uint4 a, uint4 b) {
+  const u32x4_t va = {a.x, a.y, a.z, a.w}, vb = {b.x, b.y, b.z, b.w};
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(va), "v"(vb));
+}
+__device__ __forceinline__ void mfma_vgpr_enter(f32x4_t (&st)[2][2]) {
+  asm volatile("s_nop 2" : "+v"(st[0][0]), "+v"(st[0][1]), "+v"(st[1][0]), "+v"(st[1][1]));
+}
+__device__ __forceinline__ void mfma_vgpr_leave(f32x4_t (&st)[2][2]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(st[0][0]), "+v"(st[0][1]), "+v"(st[1][0]), "+v"(st[1][1]));
+}
+
+// s_waitcnt vmcnt(n) for a run-time n in [0, 2 NJ] (the immediate must be a constant)
+template <int N>
+__device__ __forceinline__ void wait_vm_le(int n) {
+  if constexpr (N > 0) {
+    if (n >= N) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");
+      return;
+    }
+    wait_vm_le<N - 1>(n);
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
+
+// Hazard fences for mfma16_agpr over the O accumulators o[2][CT] (tied, so nothing that writes or reads
+// them moves across): 2 wait states after the VALU writes of P / O, 24 before reading the results.
+template <int CT>
+__device__ __forceinline__ void mfma_agpr_enter(f32x4_t (&o)[2][CT], uint4 (&pa)[2]) {
+  asm volatile("s_nop 2" : "+v"(pa[0].x), "+v"(pa[0].y), "+v"(pa[0].z), "+v"(pa[0].w), "+v"(pa[1].x),
+               "+v"(pa[1].y), "+v"(pa[1].z), "+v"(pa[1].w));
+#pragma unroll
+  for (int c = 0; c < CT; c += 4)
+    asm volatile("" : "+a"(o[0][c]), "+a"(o[0][c + 1]), "+a"(o[0][c + 2]), "+a"(o[0][c + 3]), "+a"(o[1][c]),
+                 "+a"(o[1][c + 1]), "+a"(o[1][c + 2]), "+a"(o[1][c + 3]));
+}
+template <int CT>
+__device__ __forceinline__ void mfma_agpr_leave(f32x4_t (&o)[2][CT]) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+  for (int c = 0; c < CT; c += 4)
+    asm volatile("" : "+a"(o[0][c]), "+a"(o[0][c + 1]), "+a"(o[0][c + 2]), "+a"(o[0][c + 3]), "+a"(o[1][c]),
+                 "+a"(o[1][c + 1]), "+a"(o[1][c + 2]), "+a"(o[1][c + 3]));
+}
+
+template <int NW, int NBUF>
+__global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kv, const float *__restrict__ sink,
+    const int32_t *__restrict__ idx, uint16_t *__restrict__ out, uint16_t *__restrict__ part_o,
+    float *__restrict__ part_ml, int64_t M, int H, int64_t N, int64_t K, int NS, int KR, float scale_log2) {
+  using Sh = MlaShape<NW, NBUF>;
+  constexpr int QJ = Sh::QJ, QREG = Sh::QREG, QL = Sh::QL, CT = Sh::CT, UPR = Sh::UPR, NJ = Sh::NJ;
+  __shared__ __attribute__((aligned(16))) uint16_t kb[NBUF][Sh::BUF];
+  __shared__ __attribute__((aligned(16))) uint4 qs[Sh::QS];  // [wave][k-step - QREG][head tile][lane]
+  __shared__ __attribute__((aligned(16))) uint4 rsc[NW][64];  // rescale bounce slots
+  __shared__ int32_t sidx[Sh::KR_MAX];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  // one item per workgroup (grid = items); the ranges of one query share an XCD (block id mod 8)
+  const int64_t nblk = gridDim.x;
+  const int64_t item = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int64_t qm = item / NS;
+  const int split = static_cast<int>(item % NS);
+  const int64_t b = qm / M;
+  const int k_begin = split * KR;
+  const int k_end = k_begin + KR < K ? k_begin + KR : static_cast<int>(K);
+  const int nch = (k_end - k_begin + kKC - 1) / kKC;  // >= 1: every range of the plan is non-empty
+  const uint16_t *kvb = uniform_ptr(kv + b * N * Sh::DQK);
+
+  // ---- stage the item's row indices (validated: -1 = outside the range or not in [0, N))
+  {
+    const int32_t *irow = idx + qm * K;
+    for (int t = tid; t < nch * kKC; t += Sh::THREADS) {
+      const int pos = k_begin + t;
+      const int32_t v = pos < k_end ? irow[pos] : -1;
+      sidx[t] = (v >= 0 && v < N) ? v : -1;
+    }
+  }
+  // ---- q B-fragments of both head tiles, Q[head][32j + 8g .. +7] with head = 32 wave + 16 ht + l16, all in
+  // VGPRs (the k-steps past QREG, if any, in LDS)
+  uint4 qf[2][QREG];
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+    const uint16_t *qrow = q + (qm * H + 32 * wave + 16 * ht + l16) * Sh::DQK + 8 * g;
+#pragma unroll
+    for (int j = 0; j < QJ; ++j) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(qrow + 32 * j);
+      if (j < QREG) qf[ht][j < QREG ? j : 0] = v;
+      else qs[((wave * QL + (j < QREG ? 0 : j - QREG)) * 2 + ht) * 64 + lane] = v;
+    }
+  }
+  // the q loads complete here, not at their first use inside the loop (where the wait would also drain
+  // the gathers in flight on every iteration)
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+    for (int j = 0; j < QREG; ++j)
+      asm volatile("" : "+v"(qf[ht][j].x), "+v"(qf[ht][j].y), "+v"(qf[ht][j].z), "+v"(qf[ht][j].w));
+  __syncthreads();  // indices (and q's LDS part) staged
+
+  // DMA slot 64 (wave + NW i) + lane of a chunk holds unit (slot % 72) ^ (key & 7) of key slot / 72
+  const uint32_t kb_lds = __builtin_amdgcn_readfirstlane(lds_addr(&kb[0][0]));
+  auto issue = [&](int c) {
+    const int buf = c % NBUF;
+    // one-wave workgroups (36 gathers) redo the slot arithmetic per chunk (opaque lane): kept live across
+    // the loop, their per-gather offsets would take 72 registers
+    int ln = lane;
+    if constexpr (NW == 1) asm volatile("" : "+v"(ln));
+    // index reads in batches of a divisor of NJ (36, 18, 12, 9): one LDS latency per batch
+    constexpr int BATCH = NJ <= 12 ? NJ : 9;
+    static_assert(NJ % BATCH == 0, "every batch lies inside the wave's NJ gathers");
+#pragma unroll
+    for (int i0 = 0; i0 < NJ; i0 += BATCH) {
+      int32_t r[BATCH];
+#pragma unroll
+      for (int i = 0; i < BATCH; ++i) r[i] = sidx[c * kKC + (64 * (wave + NW * (i0 + i)) + ln) / UPR];
+#pragma unroll
+      for (int i = 0; i < BATCH; ++i) {
+        const int jj = wave + NW * (i0 + i);
+        const int sl = 64 * jj + ln;
+        const int key = sl / UPR;
+        const uint32_t voff =
+            static_cast<uint32_t>(r[i] < 0 ? 0 : r[i]) * (Sh::DQK * 2) + ((sl % UPR) ^ (key & 7)) * 16;
+        dma16(kvb, voff, kb_lds + (buf * Sh::BUF + 64 * jj * 8) * 2);
+      }
+    }
+  };
+  const int npre = nch < NBUF - 1 ? nch : NBUF - 1;
+  for (int c = 0; c < npre; ++c) issue(c);
+
+  // per-lane LDS element offsets (see SaShape): QK key 16t + l16, unit 4j + g (two low-unit patterns);
+  // PV transpose reads keys 4g + (l16 >> 2) (+16), unit 2cc + ((l16 & 3) >> 1) (four patterns)
+  int qk_off[2][2], pv_off[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) qk_off[t][p] = Sh::slot(16 * t + l16, 0, 4 * p + g) * 8;
+    const int kv_key = 4 * g + (l16 >> 2) + 16 * t;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) pv_off[t][p] = Sh::slot(kv_key, 0, 2 * p + ((l16 & 3) >> 1)) * 8 + 4 * (l16 & 1);
+  }
+
+  float m_ref[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};  // per head (lane l16), replicated over g
+  f32x4_t o[2][CT];
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+    for (int c = 0; c < CT; ++c) o[ht][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int c = 0; c < nch; ++c) {
+    // this wave's part of chunk c has landed once at most (chunks issued after it) x NJ gathers remain
+    const int later = (nch - 1 - c) < (NBUF - 2) ? (nch - 1 - c) : (NBUF - 2);
+    wait_vm_le<(NBUF - 2) * NJ>(later * NJ);
+    __syncthreads();  // everyone's part of chunk c (and of q in LDS) is in place; chunk c - 1's buffer is free
+    if (c + NBUF - 1 < nch) issue(c + NBUF - 1);
+    const uint32_t vm = static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(sidx[c * kKC + (lane & 31)] >= 0));
+    const uint16_t *kbp = kb[c % NBUF];
+
+    // ---- S^T = K Q^T: key tiles t, head tiles ht; each K fragment feeds both head tiles
+    f32x4_t st[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht) st[t][ht] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    mfma_vgpr_enter(st);
+#pragma unroll
+    for (int j = 0; j < QJ; ++j) {
+      const int jl = j < QREG ? 0 : j - QREG;
+      const uint4 b0 = j < QREG ? qf[0][j < QREG ? j : 0] : qs[((wave * QL + jl) * 2 + 0) * 64 + lane];
+      const uint4 b1 = j < QREG ? qf[1][j < QREG ? j : 0] : qs[((wave * QL + jl) * 2 + 1) * 64 + lane];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(kbp + qk_off[t][j & 1] + ((4 * j) & ~7) * 8);
+        mfma16_vgpr(st[t][0], a, b0);
+        mfma16_vgpr(st[t][1], a, b1);
+      }
+    }
+    mfma_vgpr_leave(st);
+    // ---- online softmax per head tile (lane: head l16, keys 16t + 4g + r)
+    const uint32_t vbits = vm >> (4 * g);
+    float cmax[2];
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((vbits >> (16 * t + r)) & 1u) mx = fmaxf(mx, st[t][ht][r] * scale_log2);
+      cmax[ht] = rows_max(mx);
+    }
+    const bool need0 = cmax[0] > m_ref[0] + kRescaleTau, need1 = cmax[1] > m_ref[1] + kRescaleTau;
+    if (__builtin_amdgcn_ballot_w64(need0 || need1) != 0ull) {
+#pragma unroll
+      for (int ht = 0; ht < 2; ++ht) {
+        const bool need = ht == 0 ? need0 : need1;
+        // O is still zero for heads without a finite reference yet (the first valid chunk), so the
+        // accumulators are rescaled only when some head moves a finite reference
+        const bool move = need && m_ref[ht] != -INFINITY;
+        const float m_new = need ? cmax[ht] : m_ref[ht];
+        const float alpha = need ? (m_ref[ht] == -INFINITY ? 0.f : fast_exp2(m_ref[ht] - m_new)) : 1.f;
+        l_run[ht] *= alpha;
+        m_ref[ht] = m_new;
+        if (__builtin_amdgcn_ballot_w64(move) != 0ull) {
+          float ar[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, 64);
+          const uint32_t slot = lds_addr(&rsc[wave][lane]);
+#pragma unroll
+          for (int cc = 0; cc < CT; ++cc) scale_agpr(o[ht][cc], ar, slot);
+        }
+      }
+    }
+    uint4 pa[2];
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+      float p[8], csum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool ok = (vbits >> (16 * (i >> 2) + (i & 3))) & 1u;
+        p[i] = ok ? fast_exp2(st[i >> 2][ht][i & 3] * scale_log2 - m_ref[ht]) : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) csum += p[i];
+      l_run[ht] += rows_sum(csum);
+      pa[ht] = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                          pack_bf16x2(p[6], p[7]));
+    }
+    // ---- O += P V; each V fragment feeds both head tiles
+    mfma_agpr_enter(o, pa);
+#pragma unroll
+    for (int cc = 0; cc < CT; ++cc) {
+      const int hi = ((2 * cc) & ~7) * 8;
+      const uint2 b0 = lds_read_tr16(kbp + pv_off[0][cc & 3] + hi);
+      const uint2 b1 = lds_read_tr16(kbp + pv_off[1][cc & 3] + hi);
+      const uint4 vb = make_uint4(b0.x, b0.y, b1.x, b1.y);
+      mfma16_agpr(o[0][cc], pa[0], vb);
+      mfma16_agpr(o[1][cc], pa[1], vb);
+    }
+  }
+  mfma_agpr_leave(o);
+
+  // ---- finalise (one range per query: sink added, bf16 output) or write the partial range
+  const int64_t obase = NS == 1 ? qm : item;
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hr = 32 * wave + 16 * ht + 4 * g + r;
+      const float mx = __shfl(m_ref[ht], 4 * g + r, 64);
+      const float sm = __shfl(l_run[ht], 4 * g + r, 64);
+      float scale_o = 1.f;
+      if (NS == 1) {
+        const float sk = sink[hr] * kLog2e;
+        const float zmax = fmaxf(mx, sk);
+        scale_o = 0.f;
+        if (zmax != -INFINITY) {
+          const float e = (mx == -INFINITY) ? 0.f : exp2f(mx - zmax);
+          const float den = sm * e + exp2f(sk - zmax);
+          scale_o = den > 0.f ? e / den : 0.f;
+        }
+      }
+      uint16_t *orow = (NS == 1 ? out : part_o) + (obase * H + hr) * Sh::DV;
+#pragma unroll
+      for (int cc = 0; cc < CT; cc += 2) {  // one packed convert per two column tiles
+        const uint32_t pk = pack_bf16x2(o[ht][cc][r] * scale_o, o[ht][cc + 1][r] * scale_o);
+        orow[16 * cc + l16] = static_cast<uint16_t>(pk & 0xFFFFu);
+        orow[16 * (cc + 1) + l16] = static_cast<uint16_t>(pk >> 16);
+      }
+    }
+    if (NS > 1 && g == 0) {
+      float *pml = part_ml + (item * H + 32 * wave + 16 * ht + l16) * 2;
+      pml[0] = m_ref[ht];
+      pml[1] = l_run[ht];
+    }
+  }
+}
+
 // Merge the NS partial ranges of one (query, head) row with the sink: one wave per row, lane s reads
 // range s's (max, sum); every lane then accumulates DV/64 columns over the ranges.
 template <int DV>
@@ -553,6 +895,61 @@ int launch_sa_gw(const uint16_t *q, const uint16_t *kv, const float *sink, const
   return KS_OK;
 }
 
+// MLA kernel: H = 32 NW heads (NW <= 4), every range at most MlaShape::KR_MAX keys, ~one item per CU
+constexpr int kMlaTargetItems = 256;
+constexpr int kMlaBuffers = 3;
+inline bool use_mla(int64_t Dqk, int64_t Dv, int64_t H, int64_t K) {
+  return Dqk == 576 && Dv == 512 && H % 32 == 0 && H <= 128 && K <= 64 * 2048;
+}
+inline SaSplit mla_plan(int64_t B, int64_t M, int64_t K) {
+  const int64_t chunks = (K + kKC - 1) / kKC;
+  const int64_t bm = B * M > 0 ? B * M : 1;
+  int64_t ns = (kMlaTargetItems + bm - 1) / bm;
+  const int64_t cap = chunks / kMinChunks > 1 ? chunks / kMinChunks : 1;
+  if (ns > cap) ns = cap;
+  if (ns > 64) ns = 64;
+  const int64_t ns_min = (K + 2047) / 2048;  // ranges of at most 2048 keys (staged indices)
+  if (ns < ns_min) ns = ns_min;
+  if (ns < 1) ns = 1;
+  const int64_t kr = ((chunks + ns - 1) / ns) * kKC;
+  return SaSplit{static_cast<int>((K + kr - 1) / kr), static_cast<int>(kr)};
+}
+
+template <int NW>
+int launch_mla_nw(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
+                  int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
+  using Sh = MlaShape<NW, kMlaBuffers>;
+  const SaSplit sp = mla_plan(B, M, K);
+  const int64_t n_items = B * M * sp.ns;
+  uint16_t *part_o = nullptr;
+  float *part_ml = nullptr;
+  if (sp.ns > 1) {
+    part_ml = static_cast<float *>(ws);
+    part_o = reinterpret_cast<uint16_t *>(part_ml + n_items * H * 2);
+  }
+  hipLaunchKernelGGL((sparse_attn_mla_kernel<NW, kMlaBuffers>), dim3(static_cast<unsigned>(n_items)),
+                     dim3(Sh::THREADS), 0, stream, q, kv, sink, idx, out, part_o, part_ml, M, static_cast<int>(H), N,
+                     K, sp.ns, sp.kr, scale * kLog2e);
+  KS_CHECK_LAUNCH("sparse_attn_mla_kernel");
+  if (sp.ns > 1) {
+    const int64_t rows = B * M * H;
+    hipLaunchKernelGGL((sparse_attn_combine_kernel<512>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
+                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), sp.ns);
+    KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
+  }
+  return KS_OK;
+}
+
+int launch_mla(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out, int64_t B,
+               int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
+  switch (H / 32) {
+    case 1: return launch_mla_nw<1>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+    case 2: return launch_mla_nw<2>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+    case 3: return launch_mla_nw<3>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+    default: return launch_mla_nw<4>(q, kv, sink, idx, out, B, M, H, N, K, scale, ws, stream);
+  }
+}
+
 template <int DQK, int DV>
 int launch_sa(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
               int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
@@ -564,8 +961,8 @@ int launch_sa(const uint16_t *q, const uint16_t *kv, const float *sink, const in
   }
 }
 
-size_t sa_workspace(int64_t B, int64_t M, int64_t H, int64_t K, int64_t DV) {
-  const SaSplit sp = split_plan(B, M, H, K);
+size_t sa_workspace(int64_t B, int64_t M, int64_t H, int64_t DQK, int64_t K, int64_t DV) {
+  const SaSplit sp = use_mla(DQK, DV, H, K) ? mla_plan(B, M, K) : split_plan(B, M, H, K);
   if (sp.ns <= 1) return 0;
   return static_cast<size_t>(B * M * sp.ns * H) * (2 * sizeof(float) + DV * sizeof(uint16_t));
 }
@@ -574,9 +971,8 @@ size_t sa_workspace(int64_t B, int64_t M, int64_t H, int64_t K, int64_t DV) {
 }  // namespace ks
 
 extern "C" size_t ks_sparse_attn_workspace_size(int64_t B, int64_t M, int64_t H, int64_t Dqk, int64_t Dv, int64_t K) {
-  (void)Dqk;
   if (B <= 0 || M <= 0 || H <= 0 || K <= 0 || Dv <= 0) return 0;
-  return ks::sa_workspace(B, M, H, K, Dv);
+  return ks::sa_workspace(B, M, H, Dqk, K, Dv);
 }
 
 extern "C" int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx,
@@ -596,11 +992,12 @@ extern "C" int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float
   if (B * M == 0) return KS_OK;
   KS_CHECK_ARG(q && kv && sink && idx && out, "ks_sparse_attn: null pointer");
   KS_CHECK_ARG(ks::aligned(q, 16) && ks::aligned(kv, 16), "ks_sparse_attn: q and kv must be 16-byte aligned");
-  const size_t need = ks::sa_workspace(B, M, H, K, Dv);
+  const size_t need = ks::sa_workspace(B, M, H, Dqk, K, Dv);
   KS_CHECK_ARG(need == 0 || (workspace != nullptr && workspace_bytes >= need),
                "ks_sparse_attn: workspace of %zu bytes required, %zu given", need, workspace_bytes);
   KS_CHECK_ARG(need == 0 || ks::aligned(workspace, 16), "ks_sparse_attn: workspace must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (d128) return ks::launch_sa<128, 128>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
+  if (ks::use_mla(Dqk, Dv, H, K)) return ks::launch_mla(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
   return ks::launch_sa<576, 512>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
 }

@@ -56,7 +56,8 @@ def test_sparse_attn_reference_example_shape(device):
     np.testing.assert_allclose(got, want, **TOL)
 
 
-@pytest.mark.parametrize("Dqk,Dv,H", [(128, 128, 16), (128, 128, 64), (576, 512, 128), (576, 512, 32)])
+@pytest.mark.parametrize("Dqk,Dv,H", [(128, 128, 16), (128, 128, 64), (576, 512, 128), (576, 512, 32),
+                                      (576, 512, 48)])
 def test_sparse_attn_edges(device, Dqk, Dv, H):
     g = torch.Generator().manual_seed(Dqk + H)
     B, M, N, K = 2, 5, 300, 100
@@ -95,3 +96,65 @@ def test_sparse_attn_errors(device):
         ops.sparse_attn(q, kv, torch.zeros(16, device=device), idx, 0.1)  # D=64 unsupported
     with pytest.raises(RuntimeError):
         ops.sparse_attn(q.float(), kv, torch.zeros(16, device=device), idx, 0.1)
+
+
+# MLA-shaped heads (Dqk 576, Dv 512, H a multiple of 32) run the 32-heads-per-wave kernel: one range per query
+# (B*M >= 256, finalised in the kernel), split ranges with the combine, ranges capped at 2048 keys (K = 2049,
+# 4000), ragged chunks (K = 1, 33), every wave count (H = 32, 64, 96, 128)
+@pytest.mark.parametrize("H,B,M,K", [(32, 1, 256, 40), (64, 2, 3, 300), (96, 1, 2, 2049), (128, 2, 2, 4000),
+                                     (128, 3, 1, 1), (128, 1, 1, 33)])
+def test_sparse_attn_mla_shapes(device, H, B, M, K):
+    g = torch.Generator().manual_seed(H * 7 + K)
+    N = 3000
+    q = torch.randn(B, M, H, 576, generator=g).bfloat16()
+    kv = torch.randn(B, N, 576, generator=g).bfloat16()
+    idx = torch.randint(-3, N, (B, M, K), generator=g, dtype=torch.int32)  # a few invalid (-1..-3)
+    sink = torch.randn(H, generator=g)
+    got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), 576 ** -0.5, 512, f"mla H={H} K={K}")
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), idx.numpy(), 576 ** -0.5, 512)
+    np.testing.assert_allclose(got, want, **TOL)
+
+
+def _rising_case(g, H, K, jumps):
+    """Scores equal up to small noise, except keys at positions `jumps` whose scores exceed the running maximum
+    by ~9-13.5 (log2 units): each forces the online softmax to move its reference and rescale the accumulated
+    O by 2^-9 or less, while the ~(position) earlier keys keep a total weight comparable to the new one."""
+    N = 4096
+    u = torch.randn(576, generator=g)
+    scale = 576 ** -0.5
+    base = 0.5 * u + 0.05 * torch.randn(N, 576, generator=g)
+    step = 9.0 / (float(u @ u) * scale * 1.4426950408889634)  # +9 log2 units per jump at c = 1
+    pos = torch.randperm(N, generator=g)[:K].to(torch.int32)
+    for n, j in enumerate(jumps):
+        base[int(pos[j])] = (0.5 + (n + 1) * step) * u
+    c = 0.9 + 0.6 * torch.rand(H, generator=g)  # per-head gain: jumps of 8.1 .. 13.5
+    q = (c[:, None] * u[None, :]).expand(1, 1, H, 576).contiguous().bfloat16()
+    return q, base.unsqueeze(0).bfloat16(), pos.view(1, 1, K), scale
+
+
+@pytest.mark.parametrize("H,jumps", [(128, [300]), (64, [300]), (32, [300]), (128, [40, 200, 330, 470])])
+def test_sparse_attn_mla_rescale(device, H, jumps):
+    g = torch.Generator().manual_seed(11 + H)
+    K = 512
+    q, kv, idx, scale = _rising_case(g, H, K, jumps)
+    sink = torch.zeros(H)
+    got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), scale, 512, f"mla-rescale H={H}")
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), idx.numpy(), scale, 512)
+    np.testing.assert_allclose(got, want, **TOL)
+    if len(jumps) == 1:  # the ~500 earlier keys keep a weight comparable to the jump key's
+        top = oracle.bf16_to_f32(bits(kv)[0, int(idx[0, 0, jumps[0]])])[:512]
+        assert np.max(np.abs(want[0, 0] - top[None, :])) > 0.1
+
+
+def test_sparse_attn_mla_leading_invalid(device):
+    # the first chunks of every range are invalid: the references start at -inf without an O rescale
+    g = torch.Generator().manual_seed(5)
+    B, M, H, N, K = 1, 4, 128, 2000, 256
+    q = torch.randn(B, M, H, 576, generator=g).bfloat16()
+    kv = torch.randn(B, N, 576, generator=g).bfloat16()
+    idx = torch.randint(0, N, (B, M, K), generator=g, dtype=torch.int32)
+    idx[:, :, :100] = -1
+    sink = torch.randn(H, generator=g)
+    got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), 576 ** -0.5, 512, "mla-leading-invalid")
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), idx.numpy(), 576 ** -0.5, 512)
+    np.testing.assert_allclose(got, want, **TOL)

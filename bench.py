@@ -185,6 +185,7 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
     bnd = torch.empty(B, S, T, dtype=torch.float32, device="cuda")
     kmax = torch.empty(B, (T + 255) // 256, dtype=torch.float32, device="cuda")
     idx = torch.empty(B, S, min(p["k_top"], T), dtype=torch.int32, device="cuda")
+    part = torch.empty(B * S * 4 * 2048, dtype=torch.int64, device="cuda")  # the split top-k's slice lists
     from kernelswift_amd import _lib
     lib = _lib.load()
     (qn, qs), (kn, ks_) = stats
@@ -200,7 +201,8 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
         _lib.check(lib.ks_dbg_indexer_topk_bounded(out.data_ptr(), bnd.data_ptr(), kmax.data_ptr(), qr.data_ptr(),
                                                    kr.data_ptr(), t["w"].data_ptr(), qn.data_ptr(), qs.data_ptr(),
                                                    kn.data_ptr(), ks_.data_ptr(), B, S, T, p["k_top"], 1,
-                                                   p["start_pos"], idx.data_ptr(), stream), "top-k (bounded)")
+                                                   p["start_pos"], idx.data_ptr(), stream, part.data_ptr(),
+                                                   part.numel()), "top-k (bounded)")
 
     def scores_exact():
         _lib.check(lib.ks_indexer_scores(qr.data_ptr(), kr.data_ptr(), t["w"].data_ptr(), 0, qn.data_ptr(),
@@ -313,10 +315,11 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
     achieved = flops / (op_us * 1e-6) / 1e12
     res = {"us_per_call": round(dev_med, 3), "wall_us_per_call_sync": round(wall_med, 3), "ms_per_step": ms_step,
            "kernels_us": {"sparse_attn_kernel+combine": round(op_us, 3)},
-           "roofline": {"bound": "mfma", "kernel": "sparse_attn_kernel (+ combine)", "achieved": round(achieved, 2),
+           "roofline": {"bound": "mfma", "kernel": ("sparse_attn_kernel" if cfg == 3 else "sparse_attn_mla_kernel")
+                        + " (+ combine)", "achieved": round(achieved, 2),
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                         "traffic": _traffic(("sparse_attn_kernel<128, 128, 1>" if cfg == 3
-                                             else "sparse_attn_kernel<576, 512, 8>") + f"@cfg{cfg}"),
+                                             else "sparse_attn_mla_kernel<4, 3>") + f"@cfg{cfg}"),
                         "cache": ("warm (the 2 MiB kv fits in L2)" if cfg == 3
                                   else "kv 2.25 GiB: gathered rows come from HBM")},
            "gathered_GBps": round(gathered / (op_us * 1e-6) / 1e9, 1)}

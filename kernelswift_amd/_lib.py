@@ -45,7 +45,8 @@ DEBUG_SIGNATURES = {
     "ks_dbg_indexer_scores_bounded": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                                      _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_p]),
     "ks_dbg_indexer_topk_bounded": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
-                                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_p, _c_p]),
+                                                   _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_p, _c_p,
+                                                   _c_p, _c_i64]),
     "ks_dbg_indexer": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32,
                                       _c_i64, _c_i32, _c_i64, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                       _c_i64, _c_p, _c_sz, _c_p, _c_f, _c_p, _c_i32]),

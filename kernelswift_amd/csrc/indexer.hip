@@ -28,6 +28,8 @@ struct IndexerWs {
   float *scores;
   float *bounds;  // per-score bounds of the bounded path
   float *kmax;    // per key block norm maxima of the bounded path
+  uint64_t *part;  // the split top-k's per-slice lists (rows too few to fill the GPU)
+  int64_t part_cap;
   size_t bytes;
 };
 
@@ -50,6 +52,8 @@ IndexerWs carve(void *base, int64_t B, int64_t S, int64_t H, int64_t D, int64_t 
   w.scores = reinterpret_cast<float *>(take(size_t(B * S * T) * 4));
   w.bounds = reinterpret_cast<float *>(take(size_t(B * S * T) * 4));
   w.kmax = reinterpret_cast<float *>(take(size_t(B * ((T + ks::kScoreKeyBlock - 1) / ks::kScoreKeyBlock)) * 4));
+  w.part_cap = ks::topk_bounded_part_capacity(B * S);
+  w.part = reinterpret_cast<uint64_t *>(take(size_t(w.part_cap) * 8));
   w.bytes = off;
   return w;
 }
@@ -111,7 +115,8 @@ int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_
                                    ws.kmax);
     if (rc != KS_OK) return rc;
     const ks::TopkRecompute trc{ws.bounds, ws.kmax, ws.q_rot, ws.k_rot, static_cast<const float *>(w), ws.q_norm,
-                                ws.q_span, ws.k_norm, ws.k_span, T, bound_c, stats, path == 3 ? 1 : 0};
+                                ws.q_span, ws.k_norm, ws.k_span, T, bound_c, stats, path == 3 ? 1 : 0, ws.part,
+                                ws.part_cap};
     return ks::launch_indexer_topk_bounded(ws.scores, T, B, S, T, kk, causal ? 1 : 0, start_pos, ratio, offset, out,
                                            out_i64 ? 1 : 0, trc, st);
   }

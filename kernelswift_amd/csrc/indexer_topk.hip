@@ -149,7 +149,7 @@ __device__ __forceinline__ void wave_stage(uint64_t (&v)[E], int NT, int size) {
 // barriers.
 template <int E>
 __device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, int k, void *out, int out_i64,
-                               int causal, int64_t limit, int64_t offset) {
+                               int causal, int64_t limit, int64_t offset, uint64_t *part) {
   const int tid = threadIdx.x;
   const int NT = P / E < 64 ? 64 : P / E;  // active threads (at least one wave)
   const bool act = tid < NT;               // uniform per wave (NT is a multiple of 64)
@@ -211,8 +211,12 @@ __device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, in
     for (int r = 0; r < E; ++r) {
       const int e = r * NT + tid;
       if (e < k_sel) {
-        const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[r] & 0xFFFFFFFFull));
-        store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+        if (part != nullptr) {
+          part[e] = v[r];  // a slice's sorted list, for the merge
+        } else {
+          const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[r] & 0xFFFFFFFFull));
+          store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+        }
       }
     }
   }
@@ -222,7 +226,8 @@ __device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, in
 // sorted store.  sh.k_rem == k_sel and sh.hist[0] == 0 on entry, behind a barrier.
 template <int KPT>
 __device__ __forceinline__ void select_sort_store(const uint32_t (&key)[KPT], int k_sel, int64_t row, int k, void *out, int out_i64,
-                                  int causal, int64_t limit, int64_t offset, uint64_t *cand, SelShared &sh) {
+                                  int causal, int64_t limit, int64_t offset, uint64_t *cand, SelShared &sh,
+                                  int col0 = 0, uint64_t *part = nullptr) {
   const int tid = threadIdx.x;
   // ---- radix select of the k_sel-th largest key
   radix_pass<KPT>(key, 0u, 0u, 21, 2048, sh, 0);
@@ -244,7 +249,7 @@ __device__ __forceinline__ void select_sort_store(const uint32_t (&key)[KPT], in
   for (int j = 0; j < KPT; ++j) {
     const uint32_t kk = key[j];
     if (kk > kstar || (kk == kstar && take_eq == eq_total)) {
-      const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
+      const uint32_t col = static_cast<uint32_t>(col0 + j * kTopkThreads + tid);
       cand[pos++] = (static_cast<uint64_t>(kk) << 32) | static_cast<uint64_t>(~col);
     }
   }
@@ -257,7 +262,7 @@ __device__ __forceinline__ void select_sort_store(const uint32_t (&key)[KPT], in
       const uint32_t incl = block_inclusive_scan(f, sh.wsum);
       const uint32_t rank = base + incl - f;
       if (f && rank < take_eq) {
-        const uint32_t col = static_cast<uint32_t>(j * kTopkThreads + tid);
+        const uint32_t col = static_cast<uint32_t>(col0 + j * kTopkThreads + tid);
         cand[n_gt + rank] = (static_cast<uint64_t>(kstar) << 32) | static_cast<uint64_t>(~col);
       }
       // block total of this slice = sum of the per-wave totals left in wsum by the scan
@@ -273,11 +278,11 @@ __device__ __forceinline__ void select_sort_store(const uint32_t (&key)[KPT], in
   int P = 2;
   while (P < k_sel) P <<= 1;
   if (P <= kTopkThreads) {
-    sort_and_store<1>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+    sort_and_store<1>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset, part);
   } else if (P == 2 * kTopkThreads) {
-    sort_and_store<2>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+    sort_and_store<2>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset, part);
   } else {
-    sort_and_store<4>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset);
+    sort_and_store<4>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset, part);
   }
 }
 
@@ -517,12 +522,16 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
 // capacity); the row's keys then hold exact scores wherever they can matter, and the exact selection runs
 // on them.  A score with U > 0 whose upper end is below tau enters the selection as that upper end: below
 // tau, so below every exact score of the k largest, like the exact score itself.
+// Slice mode (part != null): workgroup (row, p) runs the same on columns [p W, p W + W) of the row and
+// writes its exact top k, sorted, as composites to part[(row P + p) k ..]: the row's top k is the top k of
+// the slices' lists (a column of the row's top k is in the top k of its slice).
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float *scores, int64_t ld,
                                                                    int64_t S, int T, int k, int causal,
                                                                    int64_t start_pos, int ratio, int64_t offset,
                                                                    void *__restrict__ out, int out_i64,
-                                                                   TopkRecompute rc, int lcap) {
+                                                                   TopkRecompute rc, int lcap, int W,
+                                                                   uint64_t *__restrict__ part) {
   extern __shared__ uint64_t cand[];  // the recomputation list first, then the selection's candidates
   __shared__ SelShared sh;
   __shared__ RecShared rs;
@@ -536,16 +545,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     limit = (start_pos + s + 1) / ratio;
     n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
   }
-  const int k_sel = k < n_valid ? k : n_valid;
-  const float *src = scores + row * ld;
-  const float *ub = rc.bounds + row * ld;
+  // the workgroup's columns: [c0, c0 + nv) of the row's valid prefix
+  const int c0 = static_cast<int>(blockIdx.y) * W;
+  const int nv = n_valid - c0 <= 0 ? 0 : (n_valid - c0 < W ? n_valid - c0 : W);
+  uint64_t *slice_out = part != nullptr ? part + (row * gridDim.y + blockIdx.y) * k : nullptr;
+  const int k_sel = k < nv ? k : nv;
+  const float *src = scores + row * ld + c0;
+  const float *ub = rc.bounds + row * ld + c0;
 
   // keys of the lower and upper ends (equal, and exact, where the bound is 0)
   uint32_t lok[KPT], hik[KPT];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    const int col = j * kTopkThreads + tid;
-    const bool v = col < n_valid;
+    const int col = j * kTopkThreads + tid;  // relative to c0
+    const bool v = col < nv;
     const float sv = v ? src[col] : 0.f;
     const float uv = v ? ub[col] : 0.f;
     lok[j] = v ? score_key(uv > 0.f ? sv - uv : sv) : 0u;
@@ -585,7 +598,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
       }
     }
     const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
-    float *srow = const_cast<float *>(src);
+    float *srow = const_cast<float *>(scores + row * ld);
     uint32_t n_exact = 0, n_unres = 0;
     for (uint32_t b0 = 0; b0 < ncand; b0 += static_cast<uint32_t>(lcap)) {
       const uint32_t nb = ncand - b0 < static_cast<uint32_t>(lcap) ? ncand - b0 : static_cast<uint32_t>(lcap);
@@ -593,7 +606,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
       while (mm) {
         const int j = __builtin_ctz(mm);
         mm &= mm - 1;
-        if (p >= b0 && p < b0 + nb) list[p - b0] = j * kTopkThreads + tid;
+        if (p >= b0 && p < b0 + nb) list[p - b0] = c0 + j * kTopkThreads + tid;
         ++p;
       }
       __syncthreads();
@@ -606,7 +619,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     uint32_t key[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; ++j)
-      key[j] = ((cmask >> j) & 1u) ? score_key(srow[j * kTopkThreads + tid]) : hik[j];
+      key[j] = ((cmask >> j) & 1u) ? score_key(srow[c0 + j * kTopkThreads + tid]) : hik[j];
     if (rc.stats != nullptr) {
       if (n_exact) atomicAdd(&rc.stats[0], n_exact);
       if (n_unres) atomicAdd(&rc.stats[1], n_unres);
@@ -615,27 +628,115 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     // ---- exact selection; hist[0] was cleared by the second pass above
     if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
     __syncthreads();
-    select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh);
+    select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh, c0, slice_out);
   }
 
-  // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order)
+  // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order); the merge
+  // writes it in slice mode
+  if (slice_out == nullptr)
+    for (int j = k_sel + tid; j < k; j += kTopkThreads)
+      store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
+}
+
+// The first m of the merge of two descending lists of unique composites x[0, nx) and y[0, ny): thread t
+// finds where its outputs t E .. t E + E - 1 start on the merge path (binary search), then merges E
+// steps.  emit(e, v) receives output e.
+template <typename Emit>
+__device__ __forceinline__ void merge_path(const uint64_t *x, int nx, const uint64_t *y, int ny, int m, Emit emit) {
+  const int E = (m + kTopkThreads - 1) / kTopkThreads;
+  const int d0 = static_cast<int>(threadIdx.x) * E;
+  if (d0 >= m) return;
+  // i = how many of the first d0 outputs come from x: the smallest i with x[i] < y[d0 - i - 1]
+  int lo = d0 - ny > 0 ? d0 - ny : 0, hi = d0 < nx ? d0 : nx;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (x[mid] > y[d0 - mid - 1]) lo = mid + 1;
+    else hi = mid;
+  }
+  int i = lo, j = d0 - lo;
+  for (int e = d0; e < d0 + E && e < m; ++e) {
+    const bool from_x = j >= ny || (i < nx && x[i] > y[j]);
+    emit(e, from_x ? x[i++] : y[j++]);
+  }
+}
+
+// Merge of the (at most 4) slices' sorted lists into the row's top k: slices 0 + 1 and 2 + 3 merge into two
+// lists of at most k, which merge into the output.  One workgroup per row; all lists in LDS.
+__global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(const uint64_t *__restrict__ part, int W, int T,
+                                                                 int k, int64_t S, int causal, int64_t start_pos,
+                                                                 int ratio, int64_t offset, void *__restrict__ out,
+                                                                 int out_i64) {
+  extern __shared__ uint64_t lists[];  // [4][k] slice lists, then [2][k] pair merges
+  const int64_t row = blockIdx.x;
+  const int64_t s = row % S;
+  const int tid = threadIdx.x;
+  const int NP = (T + W - 1) / W;
+  int64_t limit = INT64_MAX;
+  int n_valid = T;
+  if (causal) {
+    limit = (start_pos + s + 1) / ratio;
+    n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
+  }
+  const int k_sel = k < n_valid ? k : n_valid;
+  int len[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int nv = p < NP ? (n_valid - p * W <= 0 ? 0 : (n_valid - p * W < W ? n_valid - p * W : W)) : 0;
+    len[p] = k < nv ? k : nv;
+  }
+  const uint64_t *src = part + row * NP * k;
+  for (int p = 0; p < NP; ++p)
+    for (int i = tid; i < len[p]; i += kTopkThreads) lists[p * k + i] = src[p * k + i];
+  __syncthreads();
+  uint64_t *pair = lists + 4 * k;
+  const int na = len[0] + len[1] < k ? len[0] + len[1] : k, nb = len[2] + len[3] < k ? len[2] + len[3] : k;
+  merge_path(lists, len[0], lists + k, len[1], na, [&](int e, uint64_t v) { pair[e] = v; });
+  merge_path(lists + 2 * k, len[2], lists + 3 * k, len[3], nb, [&](int e, uint64_t v) { pair[k + e] = v; });
+  __syncthreads();
+  merge_path(pair, na, pair + k, nb, k_sel, [&](int e, uint64_t v) {
+    const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v & 0xFFFFFFFFull));
+    store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+  });
   for (int j = k_sel + tid; j < k; j += kTopkThreads)
     store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
 }
 
+// W: columns per workgroup (T for whole rows), NP = ceil(T / W) slices (part != null when NP > 1)
 template <int KPT>
 int launch_topk_bounded(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
                         int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, const TopkRecompute &rc,
-                        hipStream_t stream) {
+                        int W, int NP, uint64_t *part, hipStream_t stream) {
   int P = 2;
   while (P < k) P <<= 1;
   // dynamic LDS: the selection's 2P composites, or the recomputation list (4P columns)
   const int lcap = 4 * P;
   const size_t shmem = static_cast<size_t>(2 * P) * sizeof(uint64_t);
-  hipLaunchKernelGGL(topk_bounded_kernel<KPT>, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, stream,
-                     scores, ld, S, T, k, causal, start_pos, ratio, offset, out, out_i64, rc, lcap);
+  hipLaunchKernelGGL(topk_bounded_kernel<KPT>, dim3(static_cast<unsigned>(rows), static_cast<unsigned>(NP)),
+                     dim3(kTopkThreads), shmem, stream, scores, ld, S, T, k, causal, start_pos, ratio, offset, out,
+                     out_i64, rc, lcap, W, part);
   KS_CHECK_LAUNCH("topk_bounded_kernel");
   return KS_OK;
+}
+
+template <int KPT>
+int launch_topk_bounded_rows(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
+                             int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
+                             const TopkRecompute &rc, hipStream_t stream) {
+  return launch_topk_bounded<KPT>(scores, ld, rows, S, T, k, causal, start_pos, ratio, offset, out, out_i64, rc, T, 1,
+                                  nullptr, stream);
+}
+
+// Slices per row of the split selection: rows much longer than k (T > 8k: the load and the threshold
+// passes, which a slice shares out, dominate; shorter rows are bound by the sort of k and the candidates
+// near the threshold, which every slice repeats), enough workgroups for the 256 CUs, at most 4 (the merge
+// takes 4 lists), and at least 2k columns per slice.
+constexpr int kTopkMaxSlices = 4;
+inline int topk_slices(int64_t rows, int T, int k) {
+  if (rows >= 256 || T <= 8 * k) return 1;
+  int p = static_cast<int>((256 + rows - 1) / rows);
+  if (p > kTopkMaxSlices) p = kTopkMaxSlices;
+  while (p > 1 && T / p < 2 * k) --p;
+  return p;
 }
 }  // namespace
 }  // namespace ks
@@ -679,28 +780,60 @@ int ks::launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, 
   KS_CHECK_ARG(rows < (int64_t(1) << 31), "indexer top-k (bounded): too many rows");
   const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
   const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
-  if (T <= 1024) return launch_topk_bounded<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  if (T <= 2048) return launch_topk_bounded<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  if (T <= 4096) return launch_topk_bounded<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  if (T <= 8192) return launch_topk_bounded<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  const int np = topk_slices(rows, Ti, ki);
+  if (np > 1 && rc.part != nullptr && rows * np * k <= rc.part_cap) {
+    // slices of W columns: 1024 times a power of two (W / 1024 keys per thread cover a slice)
+    int W = kTopkThreads;
+    while (W * np < Ti) W <<= 1;
+    const int NP = (Ti + W - 1) / W;
+    int rcode;
+    switch (W / kTopkThreads) {
+      case 1: rcode = launch_topk_bounded<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
+      case 2: rcode = launch_topk_bounded<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
+      case 4: rcode = launch_topk_bounded<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
+      case 8: rcode = launch_topk_bounded<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
+      case 16: rcode = launch_topk_bounded<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
+      default: rcode = launch_topk_bounded<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
+    }
+    if (rcode != KS_OK) return rcode;
+    const size_t shmem = static_cast<size_t>(6) * k * sizeof(uint64_t);  // 4 slice lists + 2 pair merges
+    hipLaunchKernelGGL(topk_merge_kernel, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, st, rc.part, W,
+                       Ti, ki, S, c, start_pos, ratio, offset, out, o);
+    KS_CHECK_LAUNCH("topk_merge_kernel");
+    return KS_OK;
+  }
+  if (T <= 1024) return launch_topk_bounded_rows<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  if (T <= 2048) return launch_topk_bounded_rows<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  if (T <= 4096) return launch_topk_bounded_rows<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  if (T <= 8192) return launch_topk_bounded_rows<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
   if (T <= 16384)
-    return launch_topk_bounded<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  return launch_topk_bounded<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+    return launch_topk_bounded_rows<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+  return launch_topk_bounded_rows<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+}
+
+int64_t ks::topk_bounded_part_capacity(int64_t rows) {
+  if (rows <= 0 || rows >= 256) return 0;
+  int64_t p = (256 + rows - 1) / rows;
+  if (p > kTopkMaxSlices) p = kTopkMaxSlices;
+  return rows * p * 2048;
 }
 
 // Diagnostic entry (not part of the public header) of the bounded top-k, for timing it alone: scores and
 // bounds from ks_dbg_indexer_scores_bounded over rotated q / k (with their row statistics); the scores
-// that are recomputed are rewritten in place.  ratio 1, int32 output.
+// that are recomputed are rewritten in place.  ratio 1, int32 output.  part (optional, part_cap composites,
+// topk_bounded_part_capacity(B S) of them) enables the split selection.
 extern "C" int ks_dbg_indexer_topk_bounded(float *scores, const float *bounds, const float *kmax, const uint16_t *q,
                                            const uint16_t *k, const float *w, const float *q_norm,
                                            const int32_t *q_span, const float *k_norm, const int32_t *k_span,
                                            int64_t B, int64_t S, int64_t T, int64_t k_top, int32_t causal,
-                                           int64_t start_pos, void *out, void *stream) {
+                                           int64_t start_pos, void *out, void *stream, uint64_t *part,
+                                           int64_t part_cap) {
   ks::last_error().clear();
   KS_CHECK_ARG(scores && bounds && kmax && q && k && w && q_norm && q_span && k_norm && k_span && out,
                "ks_dbg_indexer_topk_bounded: null pointer");
   KS_CHECK_ARG(T <= 32768 && k_top <= 2048, "ks_dbg_indexer_topk_bounded: T <= 32768 and k <= 2048");
-  const ks::TopkRecompute rc{bounds, kmax, q, k, w, q_norm, q_span, k_norm, k_span, T, ks::kScoreBoundC, nullptr, 0};
+  const ks::TopkRecompute rc{bounds, kmax, q, k, w, q_norm, q_span, k_norm, k_span, T, ks::kScoreBoundC, nullptr, 0,
+                             part, part_cap};
   return ks::launch_indexer_topk_bounded(scores, T, B, S, T, k_top, causal ? 1 : 0, start_pos, 1, 0, out, 0, rc,
                                          static_cast<hipStream_t>(stream));
 }

@@ -336,3 +336,28 @@ def test_indexer_bounded_equals_exact_path(device, dist):
     want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), 512, True, 2048 - 20, 1, 0, 0, 64, True)
     np.testing.assert_array_equal(bounded, want)
     print(f"[info] bounded path: {int(st[0])} exact dot recomputations", flush=True)
+
+
+# Rows too few to fill the GPU and much longer than k split into column slices (each selects its own exact
+# top k; a merge combines the sorted lists): causal rows whose valid prefix ends inside the first slice (later slices empty, masked tail), a
+# prefix ending inside the second slice, slices of unequal width (T = 5000), and all-equal scores, whose
+# order across slices is decided by the column alone.
+@pytest.mark.parametrize("S,T,k_top,start_pos,causal,zero_q", [(8, 4096, 256, 0, True, False),
+                                                              (6, 4096, 256, 1490, True, False),
+                                                              (5, 5000, 300, 0, False, False),
+                                                              (4, 8192, 512, 0, False, True)])
+def test_indexer_split_topk(device, S, T, k_top, start_pos, causal, zero_q):
+    g = torch.Generator().manual_seed(S * T + k_top)
+    q = torch.randn(1, S, 64, 128, generator=g)
+    if zero_q:
+        q = torch.zeros_like(q)
+    q = q.bfloat16()
+    k = torch.randn(1, T, 128, generator=g).bfloat16()
+    w = torch.randn(1, S, 64, generator=g) / 8
+    tab = workloads.freqs_table(64, max(T, start_pos + S) + 1)
+    print(f"[case] split top-k S={S} T={T} k={k_top} start={start_pos} causal={causal} zero_q={zero_q}", flush=True)
+    got, _ = _dbg_indexer(q, k, w, tab, k_top, causal, start_pos, 2)
+    want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), k_top, causal, start_pos, 1, 0, 0, 64, True)
+    np.testing.assert_array_equal(got, want)
+    if zero_q:
+        assert np.array_equal(got[0, 0], np.arange(k_top))

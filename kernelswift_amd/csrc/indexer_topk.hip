@@ -9,9 +9,9 @@
 // converted to order-preserving uint32 keys.  A 3-pass LDS radix select (11 + 11 + 10 bits) finds the
 // k-th largest key K*; keys > K* are collected unordered (slots from a block scan), keys == K* are collected
 // in column order (ordered block scan) only when more of them exist than are needed.  The k winners are
-// then bitonic-sorted (descending) on the 64-bit composite (key, ~column), which is exactly (score desc,
-// column asc); the elements stay in registers, and only exchange distances between 64 and the number of
-// active threads go through LDS, so the network costs one barrier per such stage instead of per stage.
+// then sorted (descending) on the 64-bit composite (key, ~column), which is exactly (score desc, column
+// asc): every wave sorts runs of 128 in registers (bitonic, DPP / permlane exchanges), then merge-path
+// rounds through LDS double the runs, one barrier per round.
 //
 // Causal rows: columns >= limit = (start_pos + s + 1) / ratio are -inf by definition of the masked
 // scores (baseline/indexer.py:185-193), so they are never read: the valid prefix is selected and, when
@@ -123,101 +123,114 @@ __device__ __forceinline__ void store_index(void *out, int out_i64, int64_t at, 
   }
 }
 
-// One bitonic compare-exchange stage at distance S < 64: the partner (lane ^ S) is in the same wave and
-// its value arrives through DPP / permlane (no LDS).  A lane keeps the larger composite when it holds the
-// lower position of a descending pair or the upper position of an ascending one, so it takes the partner's
-// value exactly when (partner > own) == keep_max (on equality either value is the same).
-template <int E, int S>
-__device__ __forceinline__ void wave_stage(uint64_t (&v)[E], int NT, int size) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int r = 0; r < E; ++r) {
-    const int e = r * NT + tid;
-    const uint32_t lo = lane_xor<S>(static_cast<uint32_t>(v[r]));
-    const uint32_t hi = lane_xor<S>(static_cast<uint32_t>(v[r] >> 32));
-    const uint64_t pv = (static_cast<uint64_t>(hi) << 32) | lo;
-    const bool keep_max = ((e & size) == 0) == ((e & S) == 0);
-    v[r] = ((pv > v[r]) == keep_max) ? pv : v[r];
+// Outputs [d0, d1) of the merge of two descending lists of unique composites x[0, nx) and y[0, ny)
+// (d1 <= nx + ny): the start on the merge path by binary search, then sequential steps.  emit(e, v)
+// receives output e.
+template <typename Emit>
+__device__ __forceinline__ void merge_path(const uint64_t *x, int nx, const uint64_t *y, int ny, int d0, int d1,
+                                           Emit emit) {
+  // i = how many of the first d0 outputs come from x: the smallest i with x[i] < y[d0 - i - 1]
+  int lo = d0 - ny > 0 ? d0 - ny : 0, hi = d0 < nx ? d0 : nx;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (x[mid] > y[d0 - mid - 1]) lo = mid + 1;
+    else hi = mid;
+  }
+  int i = lo, j = d0 - lo;
+  for (int e = d0; e < d1; ++e) {
+    const bool from_x = j >= ny || (i < nx && x[i] > y[j]);
+    emit(e, from_x ? x[i++] : y[j++]);
   }
 }
 
-// Bitonic sort (descending) of the P composites cand[0..k_sel) (absent = 0 sorts last) and store of the
-// first k_sel in order.  Element e = r*NT + tid lives in registers; compare-exchange partners at distance
-// >= NT are in the same thread, at distance < 64 in the same wave (DPP / permlane, the six stages of a
-// merge step unrolled at compile time); only distances in between go through LDS (cand[0..2P) as two
-// alternating exchange buffers: one barrier per such stage).  Waves holding no elements only join the
-// barriers.
-template <int E>
-__device__ void sort_and_store(uint64_t *cand, int P, int k_sel, int64_t row, int k, void *out, int out_i64,
-                               int causal, int64_t limit, int64_t offset, uint64_t *part) {
-  const int tid = threadIdx.x;
-  const int NT = P / E < 64 ? 64 : P / E;  // active threads (at least one wave)
-  const bool act = tid < NT;               // uniform per wave (NT is a multiple of 64)
-  uint64_t v[E];
+// The first m outputs of that merge over the workgroup: thread t emits outputs [t E, t E + E), E = ceil(m / 1024).
+template <typename Emit>
+__device__ __forceinline__ void merge_first(const uint64_t *x, int nx, const uint64_t *y, int ny, int m, Emit emit) {
+  const int E = (m + kTopkThreads - 1) / kTopkThreads;
+  const int d0 = static_cast<int>(threadIdx.x) * E;
+  if (d0 < m) merge_path(x, nx, y, ny, d0, d0 + E < m ? d0 + E : m, emit);
+}
+
+// Bitonic sort (descending) of a wave's run of 128 composites, element r*64 + lane in v[r]: the exchange at
+// distance 64 stays in the lane, the others go through DPP / permlane.
+template <int SIZE, int S>
+__device__ __forceinline__ void run_stage(uint64_t (&v)[2], int lane) {
+  if constexpr (S == 64) {
+    const uint64_t a = v[0], c = v[1];  // SIZE == 128: one descending pair
+    v[0] = a > c ? a : c;
+    v[1] = a > c ? c : a;
+  } else {
 #pragma unroll
-  for (int r = 0; r < E; ++r) {
-    const int e = r * NT + tid;
-    v[r] = (act && e < k_sel) ? cand[e] : 0ull;
-  }
-  __syncthreads();  // the candidates are in registers; LDS becomes the exchange area
-  int phase = 0;
-  for (int size = 2; size <= P; size <<= 1) {
-    int stride = size >> 1;
-    for (; stride >= NT; stride >>= 1) {  // partner in this thread (E > 1)
-      if (act) {
-        const int rs = stride / NT;
-#pragma unroll
-        for (int r = 0; r < E; ++r) {
-          if ((r & rs) == 0) {
-            const int e = r * NT + tid;
-            const uint64_t a = v[r], c = v[r | rs];
-            const uint64_t hi = a > c ? a : c, lo = a > c ? c : a;
-            const bool desc = (e & size) == 0;
-            v[r] = desc ? hi : lo;
-            v[r | rs] = desc ? lo : hi;
-          }
-        }
-      }
+    for (int r = 0; r < 2; ++r) {
+      const int e = r * 64 + lane;
+      const uint32_t lo = lane_xor<S>(static_cast<uint32_t>(v[r]));
+      const uint32_t hi = lane_xor<S>(static_cast<uint32_t>(v[r] >> 32));
+      const uint64_t pv = (static_cast<uint64_t>(hi) << 32) | lo;
+      const bool keep_max = ((e & SIZE) == 0) == ((e & S) == 0);
+      v[r] = ((pv > v[r]) == keep_max) ? pv : v[r];
     }
-    for (; stride >= 64; stride >>= 1) {  // partner in another wave
-      uint64_t *xb = cand + (phase & 1) * P;
-      ++phase;
-      if (act) {
+  }
+  if constexpr (S > 1) run_stage<SIZE, S / 2>(v, lane);
+}
+template <int SIZE>
+__device__ __forceinline__ void run_sort(uint64_t (&v)[2], int lane) {
+  run_stage<SIZE, SIZE / 2>(v, lane);
+  if constexpr (SIZE < 128) run_sort<SIZE * 2>(v, lane);
+}
+
+// Sort (descending) of the composites cand[0, n) (absent = 0 sorts last; P = pow2 >= max(n, 128)) and
+// store of the first k_sel in order.  Every wave sorts runs of 128 in registers (run_sort, no barrier);
+// log2(P / 128) merge-path rounds then double the runs through the two halves of cand[0, 2P), one
+// barrier each, and the last round stores.  ~10 dependent LDS reads per round per thread, against the
+// bitonic network's log2(P) (log2(P) + 1) / 2 stages, of which those at distances >= 64 need a barrier.
+__device__ void sort_merge_store(uint64_t *cand, int P, int n, int k_sel, int64_t row, int k, void *out,
+                                 int out_i64, int causal, int64_t limit, int64_t offset, uint64_t *part) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto emit_final = [&](int e, uint64_t v) {
+    if (part != nullptr) {
+      part[e] = v;
+    } else {
+      const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v & 0xFFFFFFFFull));
+      store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+    }
+  };
+  const int runs = P / 128;
+  for (int rr = wave; rr < runs; rr += kTopkWaves) {
+    uint64_t v[2];
 #pragma unroll
-        for (int r = 0; r < E; ++r) xb[r * NT + tid] = v[r];
+    for (int r = 0; r < 2; ++r) {
+      const int e = rr * 128 + r * 64 + lane;
+      v[r] = e < n ? cand[e] : 0ull;
+    }
+    run_sort<2>(v, lane);
+    if (runs == 1) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        if (r * 64 + lane < k_sel) emit_final(r * 64 + lane, v[r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) cand[rr * 128 + r * 64 + lane] = v[r];
+    }
+  }
+  if (runs == 1) return;
+  __syncthreads();
+  uint64_t *src = cand, *dst = cand + P;
+  const int E = P > kTopkThreads ? P / kTopkThreads : 1;  // outputs per thread and round
+  for (int L = 128; L < P; L <<= 1) {  // every thread runs every round (P is uniform)
+    const int d = tid * E;
+    const int pair = d / (2 * L), d0 = d % (2 * L);
+    const uint64_t *x = src + pair * 2 * L;
+    if (2 * L == P) {  // the last round: the first k_sel outputs only
+      if (d < k_sel) merge_path(x, L, x + L, L, d0, d0 + (k_sel - d < E ? k_sel - d : E), emit_final);
+    } else {
+      if (d < P) {
+        uint64_t *z = dst + pair * 2 * L;
+        merge_path(x, L, x + L, L, d0, d0 + E, [&](int e, uint64_t v) { z[e] = v; });
       }
       __syncthreads();
-      if (act) {
-#pragma unroll
-        for (int r = 0; r < E; ++r) {
-          const int e = r * NT + tid;
-          const uint64_t pv = xb[e ^ stride];
-          const bool keep_max = ((e & size) == 0) == ((e & stride) == 0);
-          v[r] = ((pv > v[r]) == keep_max) ? pv : v[r];
-        }
-      }
-    }
-    if (act) {  // partner in this wave: strides min(size / 2, 32) .. 1
-      if (size >= 64) wave_stage<E, 32>(v, NT, size);
-      if (size >= 32) wave_stage<E, 16>(v, NT, size);
-      if (size >= 16) wave_stage<E, 8>(v, NT, size);
-      if (size >= 8) wave_stage<E, 4>(v, NT, size);
-      if (size >= 4) wave_stage<E, 2>(v, NT, size);
-      wave_stage<E, 1>(v, NT, size);
-    }
-  }
-  if (act) {
-#pragma unroll
-    for (int r = 0; r < E; ++r) {
-      const int e = r * NT + tid;
-      if (e < k_sel) {
-        if (part != nullptr) {
-          part[e] = v[r];  // a slice's sorted list, for the merge
-        } else {
-          const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[r] & 0xFFFFFFFFull));
-          store_index(out, out_i64, row * k + e, col, causal, limit, offset);
-        }
-      }
+      uint64_t *t = src;
+      src = dst;
+      dst = t;
     }
   }
 }
@@ -274,16 +287,10 @@ __device__ __forceinline__ void select_sort_store(const uint32_t (&key)[KPT], in
   }
   __syncthreads();
 
-  // ---- bitonic sort of the winners (descending composite), P = pow2 >= k_sel elements, E per thread
-  int P = 2;
+  // ---- sort of the winners (descending composite) and the store
+  int P = 128;
   while (P < k_sel) P <<= 1;
-  if (P <= kTopkThreads) {
-    sort_and_store<1>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset, part);
-  } else if (P == 2 * kTopkThreads) {
-    sort_and_store<2>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset, part);
-  } else {
-    sort_and_store<4>(cand, P, k_sel, row, k, out, out_i64, causal, limit, offset, part);
-  }
+  sort_merge_store(cand, P, k_sel, k_sel, row, k, out, out_i64, causal, limit, offset, part);
 }
 
 template <int KPT>
@@ -325,7 +332,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
 template <int KPT>
 int launch_topk(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal, int64_t start_pos,
                 int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream) {
-  int P = 2;
+  int P = 128;  // the sort's runs of 128
   while (P < k) P <<= 1;
   const size_t shmem = static_cast<size_t>(2 * P) * sizeof(uint64_t);  // candidates, then the exchange buffers
   hipLaunchKernelGGL(topk_rows_kernel<KPT>, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, stream,
@@ -638,28 +645,6 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
       store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
 }
 
-// The first m of the merge of two descending lists of unique composites x[0, nx) and y[0, ny): thread t
-// finds where its outputs t E .. t E + E - 1 start on the merge path (binary search), then merges E
-// steps.  emit(e, v) receives output e.
-template <typename Emit>
-__device__ __forceinline__ void merge_path(const uint64_t *x, int nx, const uint64_t *y, int ny, int m, Emit emit) {
-  const int E = (m + kTopkThreads - 1) / kTopkThreads;
-  const int d0 = static_cast<int>(threadIdx.x) * E;
-  if (d0 >= m) return;
-  // i = how many of the first d0 outputs come from x: the smallest i with x[i] < y[d0 - i - 1]
-  int lo = d0 - ny > 0 ? d0 - ny : 0, hi = d0 < nx ? d0 : nx;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (x[mid] > y[d0 - mid - 1]) lo = mid + 1;
-    else hi = mid;
-  }
-  int i = lo, j = d0 - lo;
-  for (int e = d0; e < d0 + E && e < m; ++e) {
-    const bool from_x = j >= ny || (i < nx && x[i] > y[j]);
-    emit(e, from_x ? x[i++] : y[j++]);
-  }
-}
-
 // Merge of the (at most 4) slices' sorted lists into the row's top k: slices 0 + 1 and 2 + 3 merge into two
 // lists of at most k, which merge into the output.  One workgroup per row; all lists in LDS.
 __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(const uint64_t *__restrict__ part, int W, int T,
@@ -690,10 +675,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(const uint64_t
   __syncthreads();
   uint64_t *pair = lists + 4 * k;
   const int na = len[0] + len[1] < k ? len[0] + len[1] : k, nb = len[2] + len[3] < k ? len[2] + len[3] : k;
-  merge_path(lists, len[0], lists + k, len[1], na, [&](int e, uint64_t v) { pair[e] = v; });
-  merge_path(lists + 2 * k, len[2], lists + 3 * k, len[3], nb, [&](int e, uint64_t v) { pair[k + e] = v; });
+  merge_first(lists, len[0], lists + k, len[1], na, [&](int e, uint64_t v) { pair[e] = v; });
+  merge_first(lists + 2 * k, len[2], lists + 3 * k, len[3], nb, [&](int e, uint64_t v) { pair[k + e] = v; });
   __syncthreads();
-  merge_path(pair, na, pair + k, nb, k_sel, [&](int e, uint64_t v) {
+  merge_first(pair, na, pair + k, nb, k_sel, [&](int e, uint64_t v) {
     const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v & 0xFFFFFFFFull));
     store_index(out, out_i64, row * k + e, col, causal, limit, offset);
   });
@@ -706,7 +691,7 @@ template <int KPT>
 int launch_topk_bounded(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
                         int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, const TopkRecompute &rc,
                         int W, int NP, uint64_t *part, hipStream_t stream) {
-  int P = 2;
+  int P = 128;  // the sort's runs of 128
   while (P < k) P <<= 1;
   // dynamic LDS: the selection's 2P composites, or the recomputation list (4P columns)
   const int lcap = 4 * P;

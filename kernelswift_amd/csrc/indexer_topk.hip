@@ -369,6 +369,7 @@ __device__ __forceinline__ uint4 rec_q(const RecShared &rs, int h, int c) { retu
 constexpr int kNearCap = 256;  // near-tie dots listed at a time (a tile has at most 64 x 16)
 struct RecWave {
   uint4 k[16 * kRecC];
+  int32_t ksp[16];         // the tile's key spans
   uint16_t ent[kNearCap];  // lane << 4 | head bit (4 m + r); overwritten by the dot's exact value
 };
 
@@ -396,6 +397,7 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
       kb[kk] = *reinterpret_cast<const uint4 *>(rc.k + krow * kRecD + 32 * kk + 8 * g);
       rw.k[l16 * kRecC + ((4 * kk + g) ^ l16)] = kb[kk];
     }
+    if (g == 0) rw.ksp[l16] = rc.ksp[krow];  // read by the near-tie dots below (same wave)
     const float knm = rc.kmax[kmax_row0 + col / kScoreKeyBlock];
     uint32_t pl[8];     // relu'd lower ends, heads 16m + 4g + (0, 1) | (2, 3): pl[2m], pl[2m + 1]
     uint32_t ntm = 0;   // bit 4m + r: head 16m + 4g + r is a near tie
@@ -421,7 +423,7 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
       const uint32_t incl = wave_incl_scan(cnt);
       const int nd = static_cast<int>(__builtin_amdgcn_readlane(incl, 63));
       const int pos0 = static_cast<int>(incl - cnt);
-      const int dq = lane >> 2, sub = lane & 3;
+      const int dq = lane >> 1, sub = lane & 1;  // a pair of lanes per dot, 8 of the 16 chunks each
       for (int s0 = 0; s0 < nd; s0 += kNearCap) {  // list segments of kNearCap dots
         const int ns = nd - s0 < kNearCap ? nd - s0 : kNearCap;
         {
@@ -436,35 +438,38 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        for (int b0 = 0; b0 < ns; b0 += 16) {
+        for (int b0 = 0; b0 < ns; b0 += 32) {
           const int e = rw.ent[min(b0 + dq, ns - 1)];
           const int sl = e >> 4, bit = e & 15;
           const int h = 16 * (bit >> 2) + 4 * (sl >> 4) + (bit & 3), kl = sl & 15;
-          const int li2 = 16 * t + kl;
-          const int64_t kr2 = kbrow0 + list[li2 < n ? li2 : n - 1];
-          const int span = rs.qsp[h] + rc.ksp[kr2];
+          const int span = rs.qsp[h] + rw.ksp[kl];
           const bool split = span > 52;
           double hi = 0.0, lo = 0.0;
           if (__builtin_amdgcn_ballot_w64(split) == 0ull) {
+            // four independent fma chains (every partial sum is exact when the span fits 52 bits)
+            double a[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const uint4 qv = rec_q(rs, h, 4 * sub + c);
-              const uint4 kv4 = rw.k[kl * kRecC + ((4 * sub + c) ^ kl)];
+            for (int c = 0; c < 8; ++c) {
+              const uint4 qv = rec_q(rs, h, 8 * sub + c);
+              const uint4 kv4 = rw.k[kl * kRecC + ((8 * sub + c) ^ kl)];
               const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
               const uint32_t kw[4] = {kv4.x, kv4.y, kv4.z, kv4.w};
 #pragma unroll
               for (int p = 0; p < 4; ++p) {
-                hi = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), hi);
-                hi = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), hi);
+                a[p] = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), a[p]);
+                a[p] = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), a[p]);
               }
             }
+            hi = (a[0] + a[1]) + (a[2] + a[3]);
           } else {
             // wide dynamic range (rare): products above / below 2^(top - 38) accumulate separately
+            const int li2 = 16 * t + kl;
+            const int64_t kr2 = kbrow0 + list[li2 < n ? li2 : n - 1];
             const double thr = split ? ldexp(1.0, frexp_exp(rs.qn[h]) + frexp_exp(rc.kn[kr2]) - 38) : 0.0;
 #pragma unroll 1
-            for (int c = 0; c < 4; ++c) {
-              const uint4 qv = rec_q(rs, h, 4 * sub + c);
-              const uint4 kv4 = rw.k[kl * kRecC + ((4 * sub + c) ^ kl)];
+            for (int c = 0; c < 8; ++c) {
+              const uint4 qv = rec_q(rs, h, 8 * sub + c);
+              const uint4 kv4 = rw.k[kl * kRecC + ((8 * sub + c) ^ kl)];
               const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
               const uint32_t kw[4] = {kv4.x, kv4.y, kv4.z, kv4.w};
 #pragma unroll
@@ -476,13 +481,13 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
               }
             }
           }
-          hi = quad_sum_f64(hi);
-          lo = quad_sum_f64(lo);
+          hi += dpp_f64<0xB1>(hi);  // the pair's two halves (quad_perm [1, 0, 3, 2])
+          lo += dpp_f64<0xB1>(lo);
           uint16_t v;
           if (!split && (hi == 0.0 || (fabs(hi) >= 0x1p-126 && fabs(hi) < 0x1p127))) v = round_to_bf16_fast(hi);
           else v = round2_to_bf16(hi, lo);
           const uint16_t rv = (v & 0x8000u) ? 0 : v;  // ReLU (also maps -0 to +0)
-          // each quad reads only its own entry before this write (the value replaces the entry)
+          // each pair reads only its own entry before this write (the value replaces the entry)
           if (sub == 0 && b0 + dq < ns) rw.ent[b0 + dq] = span <= 84 ? rv : 0xFFFFu;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

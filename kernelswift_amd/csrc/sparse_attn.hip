@@ -821,7 +821,11 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const uint16_t
                                                                  int NS) {
   constexpr int CPL = DV / 64;  // columns per lane
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  // the same XCD placement as the attention kernels (workgroup i on XCD i mod 8, consecutive logical
+  // blocks on one XCD): a query's rows are merged on the XCD whose L2 received its partial ranges
+  const int64_t nblk = gridDim.x;
+  const int64_t lb = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int64_t row = lb * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // uniform per wave
   const int64_t qm = row / H;
   const int h = static_cast<int>(row % H);

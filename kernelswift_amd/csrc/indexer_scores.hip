@@ -300,13 +300,6 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     L.qspan[wave][lane] = qsp[qrow0 + lane];
     L.qnorm[wave][lane] = qn[qrow0 + lane];
   }
-  uint4 qa[HT][KD / 32];
-#pragma unroll
-  for (int m = 0; m < HT; ++m)
-#pragma unroll
-    for (int kk = 0; kk < KD / 32; ++kk)
-      qa[m][kk] = s_ok ? *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g)
-                       : make_uint4(0, 0, 0, 0);
   // the workgroup's whole key block into LDS (zero rows past T)
 #pragma unroll 4
   for (int it = 0; it < kKR * kC / kThreads; ++it) {
@@ -316,7 +309,19 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     if (kr < nk) v = *reinterpret_cast<const uint4 *>(k + (krow0 + kr) * KD + ch * 8);
     L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = v;
   }
-  __syncthreads();  // the only barrier: from here on every wave runs independently
+  // the query rows are loaded after the key block: the loads complete in order, so the barrier waits for
+  // the key block only and the q rows arrive under it and the first tile's MFMAs (each waits for its own)
+  uint4 qa[HT][KD / 32];
+#pragma unroll
+  for (int m = 0; m < HT; ++m)
+#pragma unroll
+    for (int kk = 0; kk < KD / 32; ++kk)
+      qa[m][kk] = s_ok ? *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g)
+                       : make_uint4(0, 0, 0, 0);
+  // the only barrier (from here on every wave runs independently): LDS writes done, no wait for the q loads
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
   knm = L.red[0];
 #pragma unroll
   for (int i = 1; i < kQW; ++i) knm = fmaxf(knm, L.red[i]);

@@ -138,15 +138,24 @@ def _cpu_model():
 
 
 def _gpu_clocks():
-    """Shader-clock levels as rocm-smi reports them (best effort; None when the tool is unavailable)."""
-    import subprocess
-    try:
-        r = subprocess.run(["rocm-smi", "--showclocks", "--json"], capture_output=True, text=True, timeout=30)
-        d = json.loads(r.stdout)
-        card = next(iter(d.values()))
-        return {k: v for k, v in card.items() if "sclk" in k.lower() or "fclk" in k.lower() or "mclk" in k.lower()}
-    except Exception:
-        return None
+    """Current shader/memory/fabric clock levels from the amdgpu sysfs tables (best effort; None when absent).
+
+    Read from sysfs rather than by running rocm-smi: under rocprofv3 a child process inherits the profiler's
+    preload, initialises the GPU and would then exec its interpreter."""
+    import glob
+    for dev in sorted(glob.glob("/sys/class/drm/card*/device")):
+        out = {}
+        for clk in ("sclk", "mclk", "fclk"):
+            try:
+                with open(os.path.join(dev, "pp_dpm_" + clk)) as f:
+                    cur = [ln.strip() for ln in f if ln.strip().endswith("*")]
+            except OSError:
+                continue
+            if cur:
+                out[clk] = cur[0].rstrip("* ").split(":", 1)[-1].strip()
+        if out:
+            return out
+    return None
 
 
 def _cpu_threads():

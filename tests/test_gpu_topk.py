@@ -30,7 +30,7 @@ def _check(scores, k, causal=False, start_pos=0, ratio=1, offset=0, T=None, out_
 
 
 @pytest.mark.parametrize("T,k", [(1, 1), (7, 3), (100, 100), (1024, 128), (1500, 512), (4096, 512), (4096, 4096),
-                                 (8192, 2048), (20000, 1000), (32768, 2048)])
+                                 (8192, 2048), (20000, 1000), (32768, 2048), (40000, 129), (65536, 3000)])
 def test_topk_random_fp32(device, T, k):
     g = torch.Generator(device=device).manual_seed(T + k)
     s = torch.randn(2, 5, T, device=device, generator=g)

@@ -62,6 +62,7 @@ struct ScoresLds {
   float knorm[kKR];                  // the exact recomputation (no global loads there)
   int32_t qspan[kQW][64];
   float qnorm[kQW][64];
+  float w[kQW][64];                  // each wave's head weights (fp32)
   float red[kQW];
 };
 
@@ -246,6 +247,7 @@ struct ScoresLdsBound {
   int32_t kspan[kKR];
   int32_t qspan[kQW][64];
   float qnorm[kQW][64];
+  float w[kQW][64];
   float red[kQW];
 };
 
@@ -283,41 +285,57 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   const int64_t kbrow0 = b * kbs;        // first key row of batch b
   const int64_t krow0 = kbrow0 + kb0;    // first key row of this workgroup
 
-  // max key norm over this workgroup's range (the error bound uses it for every key)
-  float knm = 0.f;
-  for (int i = tid; i < kKR; i += kThreads) {
-    const float nv = i < nk ? kn[krow0 + i] : 0.f;
-    L.knorm[i] = nv;
-    L.kspan[i] = i < nk ? ksp[krow0 + i] : 0;
-    knm = fmaxf(knm, nv);
-  }
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
-  if (lane == 0) L.red[wave] = knm;
-  // query rows as MFMA A-fragments
+  // Every prologue load is issued before the first wait (loads complete in order, so each later wait is a
+  // partial one): the key statistics and this wave's query statistics and head weights, then the key
+  // block, then the q fragments.  Indices are clamped into range and the values masked afterwards, so no
+  // load sits behind a branch or a loop-carried wait.
+  // Statistics slots are written unconditionally: threads t and t + kKR (and lanes l and l + H) load and
+  // write the same entry, so no store (and no load the compiler could sink next to it) is behind a branch.
+  static_assert(kKR <= kThreads && (kKR & (kKR - 1)) == 0, "key statistics: a power-of-two block");
   const int64_t qrow0 = (b * S + (s_ok ? s : 0)) * H;
-  if (lane < H) {
-    L.qspan[wave][lane] = qsp[qrow0 + lane];
-    L.qnorm[wave][lane] = qn[qrow0 + lane];
-  }
-  // the workgroup's whole key block into LDS (zero rows past T)
-#pragma unroll 4
-  for (int it = 0; it < kKR * kC / kThreads; ++it) {
+  const int kt = tid & (kKR - 1);
+  const bool kin = kt < nk;
+  const int kst = kin ? kt : nk - 1;  // nk >= 1: the grid covers T with key blocks
+  const float kn_v = kn[krow0 + kst];
+  const int32_t ks_v = ksp[krow0 + kst];
+  const int hl = lane & (H - 1);
+  const int64_t hrow = qrow0 + hl;
+  const float qn_v = qn[hrow];
+  const int32_t qs_v = qsp[hrow];
+  const float w_v = WBF ? bf16_to_f32(static_cast<const uint16_t *>(w)[hrow]) : static_cast<const float *>(w)[hrow];
+  constexpr int kKL = kKR * kC / kThreads;  // 16-byte key chunks per thread
+  uint4 kv[kKL];
+#pragma unroll
+  for (int it = 0; it < kKL; ++it) {
     const int lin = it * kThreads + tid;
     const int kr = lin / kC, ch = lin % kC;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (kr < nk) v = *reinterpret_cast<const uint4 *>(k + (krow0 + kr) * KD + ch * 8);
-    L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = v;
+    kv[it] = *reinterpret_cast<const uint4 *>(k + (krow0 + (kr < nk ? kr : nk - 1)) * KD + ch * 8);
   }
-  // the query rows are loaded after the key block: the loads complete in order, so the barrier waits for
-  // the key block only and the q rows arrive under it and the first tile's MFMAs (each waits for its own)
+  // query rows as MFMA A-fragments (rows of query 0 for a wave past S, which leaves after the barrier); the
+  // barrier below waits for the key block only, so these arrive under it and the first tile's MFMAs
   uint4 qa[HT][KD / 32];
 #pragma unroll
   for (int m = 0; m < HT; ++m)
 #pragma unroll
     for (int kk = 0; kk < KD / 32; ++kk)
-      qa[m][kk] = s_ok ? *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g)
-                       : make_uint4(0, 0, 0, 0);
+      qa[m][kk] = *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g);
+  // max key norm over this workgroup's range (the error bound uses it for every key)
+  float knm = kin ? kn_v : 0.f;
+  L.knorm[kt] = knm;
+  L.kspan[kt] = kin ? ks_v : 0;
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
+  if (lane == 0) L.red[wave] = knm;
+  L.qspan[wave][hl] = qs_v;
+  L.qnorm[wave][hl] = qn_v;
+  L.w[wave][hl] = w_v;
+  // the workgroup's whole key block into LDS (zero rows past T)
+#pragma unroll
+  for (int it = 0; it < kKL; ++it) {
+    const int lin = it * kThreads + tid;
+    const int kr = lin / kC, ch = lin % kC;
+    L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = kr < nk ? kv[it] : make_uint4(0, 0, 0, 0);
+  }
   // the only barrier (from here on every wave runs independently): LDS writes done, no wait for the q loads
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
@@ -336,9 +354,9 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   for (int m = 0; m < HT; ++m)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t hr = qrow0 + 16 * m + 4 * g + r;
-      wv[m][r] = WBF ? bf16_to_f32(static_cast<const uint16_t *>(w)[hr]) : static_cast<const float *>(w)[hr];
-      dl[m][r] = bound_c * 0x1p-23f * qn[hr] * knm;
+      const int h = 16 * m + 4 * g + r;
+      wv[m][r] = L.w[wave][h];
+      dl[m][r] = bound_c * 0x1p-23f * L.qnorm[wave][h] * knm;
     }
 
   // BOUND: A-fragments holding bf16 upper bounds of |w| for the two 32-head halves.  With the relu'd

@@ -312,12 +312,17 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
   const int k_sel = k < n_valid ? k : n_valid;
   const float *src = scores + row * ld;
 
-  uint32_t key[KPT];
+  // every load is issued before the first wait: columns past the valid prefix read column 0 of the row (in
+  // bounds: T >= 1) and are masked afterwards, so no load sits behind a branch
+  float f[KPT];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const int col = j * kTopkThreads + tid;
-    key[j] = col < n_valid ? score_key(src[col]) : 0u;
+    f[j] = src[col < n_valid ? col : 0];
   }
+  uint32_t key[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) key[j] = j * kTopkThreads + tid < n_valid ? score_key(f[j]) : 0u;
   if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
   for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;
   __syncthreads();
@@ -566,15 +571,21 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
   const float *ub = rc.bounds + row * ld + c0;
 
   // keys of the lower and upper ends (equal, and exact, where the bound is 0)
-  uint32_t lok[KPT], hik[KPT];
+  // every load is issued before the first wait: columns past the slice's valid part read its column 0 (in
+  // bounds: c0 < T) and are masked afterwards, so no load sits behind a branch
+  float sv[KPT], uv[KPT];
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const int col = j * kTopkThreads + tid;  // relative to c0
-    const bool v = col < nv;
-    const float sv = v ? src[col] : 0.f;
-    const float uv = v ? ub[col] : 0.f;
-    lok[j] = v ? score_key(uv > 0.f ? sv - uv : sv) : 0u;
-    hik[j] = v ? score_key(uv > 0.f ? sv + uv : sv) : 0u;
+    sv[j] = src[col < nv ? col : 0];
+    uv[j] = ub[col < nv ? col : 0];
+  }
+  uint32_t lok[KPT], hik[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const bool v = j * kTopkThreads + tid < nv;
+    lok[j] = v ? score_key(uv[j] > 0.f ? sv[j] - uv[j] : sv[j]) : 0u;
+    hik[j] = v ? score_key(uv[j] > 0.f ? sv[j] + uv[j] : sv[j]) : 0u;
   }
   if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
   for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;

@@ -396,14 +396,15 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
     const bool kv = li < n;
     const int col = list[kv ? li : n - 1];
     const int64_t krow = kbrow0 + col;
+    // the tile's loads go out together (one round trip): key rows, key span, key-block norm maximum
     uint4 kb[kRecD / 32];
 #pragma unroll
-    for (int kk = 0; kk < kRecD / 32; ++kk) {
-      kb[kk] = *reinterpret_cast<const uint4 *>(rc.k + krow * kRecD + 32 * kk + 8 * g);
-      rw.k[l16 * kRecC + ((4 * kk + g) ^ l16)] = kb[kk];
-    }
-    if (g == 0) rw.ksp[l16] = rc.ksp[krow];  // read by the near-tie dots below (same wave)
+    for (int kk = 0; kk < kRecD / 32; ++kk) kb[kk] = *reinterpret_cast<const uint4 *>(rc.k + krow * kRecD + 32 * kk + 8 * g);
+    const int32_t ksv = rc.ksp[krow];
     const float knm = rc.kmax[kmax_row0 + col / kScoreKeyBlock];
+#pragma unroll
+    for (int kk = 0; kk < kRecD / 32; ++kk) rw.k[l16 * kRecC + ((4 * kk + g) ^ l16)] = kb[kk];
+    rw.ksp[l16] = ksv;  // the four lanes of a key write the same span; read by the near-tie dots below
     uint32_t pl[8];     // relu'd lower ends, heads 16m + 4g + (0, 1) | (2, 3): pl[2m], pl[2m + 1]
     uint32_t ntm = 0;   // bit 4m + r: head 16m + 4g + r is a near tie
 #pragma unroll
@@ -610,15 +611,18 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     const int64_t qrow0 = row * kRecH;  // rows of q, w and the q statistics: (b S + s) 64 + head
     const int64_t kbrow0 = b * rc.kbs;
     if (ncand > 0) {
-      for (int i = tid; i < kRecH * kRecC; i += kTopkThreads) {
-        const int h = i / kRecC, c = i % kRecC;
-        rs.q[h * kRecC + (c ^ (h & 15))] = *reinterpret_cast<const uint4 *>(rc.q + (qrow0 + h) * kRecD + 8 * c);
-      }
-      if (tid < kRecH) {
-        rs.w[tid] = rc.w[qrow0 + tid];
-        rs.qn[tid] = rc.qn[qrow0 + tid];
-        rs.qsp[tid] = rc.qsp[qrow0 + tid];
-      }
+      // one round trip: the q rows (one 16-byte chunk per thread) and the head weights and statistics (every
+      // thread loads and writes entry tid % 64: identical writes, so neither the loads nor the stores sit
+      // behind a branch)
+      static_assert(kRecH * kRecC == kTopkThreads, "one q chunk per thread");
+      const int h = tid / kRecC, c = tid % kRecC, hh = tid & (kRecH - 1);
+      const uint4 qv = *reinterpret_cast<const uint4 *>(rc.q + (qrow0 + h) * kRecD + 8 * c);
+      const float wv = rc.w[qrow0 + hh], qnv = rc.qn[qrow0 + hh];
+      const int32_t qsv = rc.qsp[qrow0 + hh];
+      rs.q[h * kRecC + (c ^ (h & 15))] = qv;
+      rs.w[hh] = wv;
+      rs.qn[hh] = qnv;
+      rs.qsp[hh] = qsv;
     }
     const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
     float *srow = const_cast<float *>(scores + row * ld);
@@ -639,10 +643,13 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     // the selection's keys: recomputed scores from the row (the workgroup's waves share one L1: the
     // barrier above orders the rewrites before these loads), exact scores where the bound is 0, and for
     // the other bounded scores the upper end, which lies below tau like the score itself
+    // (the loads go out together: non-candidates read column c0, a broadcast, and keep their upper end)
+    float rsv[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) rsv[j] = srow[c0 + (((cmask >> j) & 1u) ? j * kTopkThreads + tid : 0)];
     uint32_t key[KPT];
 #pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      key[j] = ((cmask >> j) & 1u) ? score_key(srow[c0 + j * kTopkThreads + tid]) : hik[j];
+    for (int j = 0; j < KPT; ++j) key[j] = ((cmask >> j) & 1u) ? score_key(rsv[j]) : hik[j];
     if (rc.stats != nullptr) {
       if (n_exact) atomicAdd(&rc.stats[0], n_exact);
       if (n_unres) atomicAdd(&rc.stats[1], n_unres);

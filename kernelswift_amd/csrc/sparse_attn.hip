@@ -370,6 +370,15 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
     static_assert(Sh::GROUPS * 16 * DV * 4 + Sh::GROUPS * 32 * 4 <= Sh::GROUPS * 2 * Sh::BUF * 2, "merge fits");
     float *mo = reinterpret_cast<float *>(&kb[0][0][0]);  // [GROUPS][16 heads][DV]
     float *mml = mo + Sh::GROUPS * 16 * DV;               // [GROUPS][16 heads][2]
+    // sink logits of the heads this thread finalises (used when the merge covers the query), loaded
+    // together ahead of the exchange
+    constexpr int kMit = (16 * DV + Sh::THREADS - 1) / Sh::THREADS;
+    float skm[kMit];
+#pragma unroll
+    for (int it = 0; it < kMit; ++it) {
+      const int hh = (tid + it * Sh::THREADS) / DV;
+      skm[it] = sink[hh < H ? hh : 0];
+    }
     __syncthreads();  // every wave is done reading its chunk buffers
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -384,7 +393,10 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
     const int64_t sitem = wg;         // merged range index: query qm = sitem / nsm
     const int64_t sq = sitem / nsm;
     if (sq >= n_items / NS) return;  // padding workgroup (uniform)
-    for (int e = tid; e < 16 * DV; e += Sh::THREADS) {
+#pragma unroll
+    for (int it = 0; it < kMit; ++it) {
+      const int e = tid + it * Sh::THREADS;
+      if (e >= 16 * DV) break;
       const int h = e / DV, d = e % DV;
       float z = -INFINITY;
 #pragma unroll
@@ -401,7 +413,7 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
       }
       if (h >= H) continue;
       if (nsm == 1) {
-        const float sk = sink[h] * kLog2e;
+        const float sk = skm[it] * kLog2e;
         const float zz = fmaxf(z, sk);
         float val = 0.f;
         if (zz != -INFINITY) {
@@ -430,13 +442,19 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
   if (!item_ok) return;
   // ---- finalise: O rows are heads 4g + r; their (max, sum) live in lanes 4g + r
   if (NS == 1) {
+    float skv[4];  // sink logits of the lane's output heads, loaded together (one round trip)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int hr = gw * 16 + 4 * g + r;
+      skv[r] = sink[hr < H ? hr : 0];
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int hr = gw * 16 + 4 * g + r;
       const float mx = __shfl(m_ref, 4 * g + r, 64);
       const float sm = __shfl(l_run, 4 * g + r, 64);
       if (hr < H) {
-        const float sk = sink[hr] * kLog2e;
+        const float sk = skv[r] * kLog2e;
         const float zmax = fmaxf(mx, sk);
         float scale_o = 0.f;
         if (zmax != -INFINITY) {
@@ -566,6 +584,18 @@ __device__ __forceinline__ void mfma_agpr_enter(f32x4_t (&o)[2][CT], uint4 (&pa)
   for (int c = 0; c < CT; c += 4)
     asm volatile("" : "+a"(o[0][c]), "+a"(o[0][c + 1]), "+a"(o[0][c + 2]), "+a"(o[0][c + 3]), "+a"(o[1][c]),
                  "+a"(o[1][c + 1]), "+a"(o[1][c + 2]), "+a"(o[1][c + 3]));
+}
+// The MFMAs that wrote O have finished 24 wait states after this: every one of them is issued before it
+// (the empty statements take all of O as inputs and are ordered with the NOPs), and nothing is tied, so
+// no register copy of O is needed to set it up.  At the end of each chunk this keeps register copies that
+// the compiler places at the loop exit or back edge behind the NOPs.
+template <int CT>
+__device__ __forceinline__ void mfma_agpr_settle(const f32x4_t (&o)[2][CT]) {
+#pragma unroll
+  for (int c = 0; c < CT; c += 4)
+    asm volatile("" ::"a"(o[0][c]), "a"(o[0][c + 1]), "a"(o[0][c + 2]), "a"(o[0][c + 3]), "a"(o[1][c]),
+                 "a"(o[1][c + 1]), "a"(o[1][c + 2]), "a"(o[1][c + 3]));
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 template <int CT>
 __device__ __forceinline__ void mfma_agpr_leave(f32x4_t (&o)[2][CT]) {
@@ -772,11 +802,17 @@ __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
       mfma16_agpr(o[0][cc], pa[0], vb);
       mfma16_agpr(o[1][cc], pa[1], vb);
     }
+    mfma_agpr_settle(o);
   }
   mfma_agpr_leave(o);
 
   // ---- finalise (one range per query: sink added, bf16 output) or write the partial range
   const int64_t obase = NS == 1 ? qm : item;
+  float skv[2][4];  // sink logits of the lane's output heads, loaded together (one round trip)
+#pragma unroll
+  for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) skv[ht][r] = NS == 1 ? sink[32 * wave + 16 * ht + 4 * g + r] : 0.f;
 #pragma unroll
   for (int ht = 0; ht < 2; ++ht) {
 #pragma unroll
@@ -786,7 +822,7 @@ __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
       const float sm = __shfl(l_run[ht], 4 * g + r, 64);
       float scale_o = 1.f;
       if (NS == 1) {
-        const float sk = sink[hr] * kLog2e;
+        const float sk = skv[ht][r] * kLog2e;
         const float zmax = fmaxf(mx, sk);
         scale_o = 0.f;
         if (zmax != -INFINITY) {

@@ -21,11 +21,14 @@ constexpr float kScoreBoundC = 3.0f;
 // -ffp-contract=off, so the products round separately, exactly like the CPU oracle).
 __device__ __forceinline__ uint4 rope_chunk(uint4 v, const float2 *__restrict__ cs) {
   uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float2 tc[4];  // the four (cos, sin) pairs are loaded together, ahead of the arithmetic (one round trip)
+#pragma unroll
+  for (int p = 0; p < 4; ++p) tc[p] = cs[p];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const float x0 = bf16_to_f32(static_cast<uint16_t>(w[p] & 0xFFFFu));
     const float x1 = bf16_to_f32(static_cast<uint16_t>(w[p] >> 16));
-    const float2 t = cs[p];
+    const float2 t = tc[p];
     const float y0 = x0 * t.x - x1 * t.y;
     const float y1 = x0 * t.y + x1 * t.x;
     w[p] = static_cast<uint32_t>(f32_to_bf16_rne(y0)) | (static_cast<uint32_t>(f32_to_bf16_rne(y1)) << 16);

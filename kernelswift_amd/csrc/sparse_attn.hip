@@ -865,13 +865,23 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const uint16_t
   if (row >= rows) return;  // uniform per wave
   const int64_t qm = row / H;
   const int h = static_cast<int>(row % H);
-  const float sk = sink[h] * kLog2e;
-  float m = -INFINITY, l = 0.f;
-  if (lane < NS) {
-    const float *ml = part_ml + ((qm * NS + lane) * H + h) * 2;
-    m = ml[0];
-    l = ml[1];
+  // every load of the first kPre ranges goes out before the first wait: the sink, the ranges' (max, sum)
+  // (lane s: range min(s, NS - 1), masked below) and their O columns, which do not depend on them
+  constexpr int kPre = 8;
+  const float sk_raw = sink[h];
+  const float *ml = part_ml + ((qm * NS + (lane < NS ? lane : NS - 1)) * H + h) * 2;
+  const float m_raw = ml[0], l_raw = ml[1];
+  const uint16_t *po = part_o + (qm * NS * H + h) * DV + lane * CPL;
+  uint32_t pre[kPre][CPL / 2];
+#pragma unroll
+  for (int s = 0; s < kPre; ++s) {
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(po + static_cast<int64_t>(s < NS ? s : NS - 1) * H * DV);
+#pragma unroll
+    for (int i = 0; i < CPL; i += 2) pre[s][i / 2] = src[i / 2];
   }
+  __builtin_amdgcn_sched_barrier(0);  // keep the loads above: the scheduler would sink them below the reduction
+  const float sk = sk_raw * kLog2e;
+  const float m = lane < NS ? m_raw : -INFINITY, l = lane < NS ? l_raw : 0.f;
   float z = m;
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) z = fmaxf(z, __shfl_xor(z, d, 64));
@@ -884,10 +894,20 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const uint16_t
   float acc[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) acc[i] = 0.f;
-  const uint16_t *po = part_o + (qm * NS * H + h) * DV + lane * CPL;
-  // empty ranges have w = 0 and O = 0, so every range is accumulated without a branch
+  // empty ranges have w = 0 and O = 0, so every range is accumulated without a branch (ranges past NS in
+  // the preloaded block get weight 0)
+#pragma unroll
+  for (int s = 0; s < kPre; ++s) {
+    const float ws = s < NS ? __shfl(w, s, 64) : 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; i += 2) {
+      const uint32_t v = pre[s][i / 2];
+      acc[i] += ws * __builtin_bit_cast(float, v << 16);
+      acc[i + 1] += ws * __builtin_bit_cast(float, v & 0xFFFF0000u);
+    }
+  }
 #pragma unroll 8
-  for (int s = 0; s < NS; ++s) {
+  for (int s = kPre; s < NS; ++s) {
     const float ws = __shfl(w, s, 64);
     const uint32_t *src = reinterpret_cast<const uint32_t *>(po + static_cast<int64_t>(s) * H * DV);
 #pragma unroll

@@ -75,6 +75,22 @@ __device__ __forceinline__ void permlane32_swap(uint32_t &a, uint32_t &b) {
 
 // Value of lane (lane ^ S) for S in {1, 2, 4, 8, 16, 32}, without the LDS crossbar: DPP quad permutes,
 // half-row mirror, row rotate, or a permlane swap.
+// 16 bytes from global memory into LDS: lane i of the wave writes lds_base + 16 i (lds_base wave-uniform).
+// Issued as inline assembly so that the compiler does not order the LDS reads of the other buffer behind
+// it; completion is awaited explicitly (s_waitcnt vmcnt) before the barrier that publishes the data.
+// base: wave-uniform 64-bit global address (SGPR pair), voff: per-lane byte offset, lds: LDS byte address.
+__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+// LDS byte address of a __shared__ object (an address-space cast of a known LDS pointer, done once).
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T *p) {
+  typedef __attribute__((address_space(3))) T lds_t;
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_t *)(p)));
+}
+
 template <int S>
 __device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
   if constexpr (S == 1) {

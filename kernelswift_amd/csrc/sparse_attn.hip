@@ -63,15 +63,6 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// 16 bytes from global memory into LDS: lane i of the wave writes lds_base + 16 i (lds_base wave-uniform).
-// Issued as inline assembly so that the compiler does not order the LDS reads of the other buffer behind
-// it; completion is awaited explicitly (s_waitcnt vmcnt(0)) before the barrier that publishes the chunk.
-// base: wave-uniform 64-bit global address (SGPR pair), voff: per-lane byte offset, lds: LDS byte address.
-__device__ __forceinline__ void dma16(const void *base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-               : "memory", "m0");
-}
-
 // A wave-uniform pointer moved to SGPRs (the compiler cannot prove uniformity of values derived from the
 // wave index).
 template <typename T>
@@ -80,13 +71,6 @@ __device__ __forceinline__ T *uniform_ptr(T *p) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
   const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
   return reinterpret_cast<T *>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// LDS byte address of a __shared__ object (an address-space cast of a known LDS pointer, done once).
-template <typename T>
-__device__ __forceinline__ uint32_t lds_addr(T *p) {
-  typedef __attribute__((address_space(3))) T lds_t;
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_t *)(p)));
 }
 
 // Reductions over the four 16-lane rows of the wave (lanes l, l^16, l^32, l^48), result in every lane:

@@ -361,3 +361,22 @@ def test_indexer_split_topk(device, S, T, k_top, start_pos, causal, zero_q):
     np.testing.assert_array_equal(got, want)
     if zero_q:
         assert np.array_equal(got[0, 0], np.arange(k_top))
+
+
+# Grids of several score workgroups per CU: batches, a query count that leaves idle waves in the last
+# group, a partial last key block, with and without the XCD tiling of the workgroups (180 per batch is not
+# a multiple of 8; 256 is), causal, and rows short enough for the split top-k.
+@pytest.mark.parametrize("B,S,T", [(4, 36, 9000), (2, 64, 8100)])
+def test_indexer_multi_item_grids(device, B, S, T):
+    g = torch.Generator().manual_seed(B * S + T)
+    q = torch.randn(B, S, 64, 128, generator=g).bfloat16()
+    k = torch.randn(B, T, 128, generator=g).bfloat16()
+    w = torch.randn(B, S, 64, generator=g) / 8
+    tab = workloads.freqs_table(64, T + 1)
+    k_top, start_pos = 300, T - S
+    print(f"[case] multi-item grid B={B} S={S} T={T}", flush=True)
+    got = ops.indexer(q.to(device), k.to(device), w.to(device), tab.to(device), k_top, True, start_pos, 1, 0, 0, 64,
+                      True)
+    torch.cuda.synchronize()
+    want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), k_top, True, start_pos, 1, 0, 0, 64, True)
+    np.testing.assert_array_equal(got.cpu().numpy().astype(np.int64), want)

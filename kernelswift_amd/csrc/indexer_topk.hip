@@ -571,6 +571,21 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
   const float *src = scores + row * ld + c0;
   const float *ub = rc.bounds + row * ld + c0;
 
+  // the recomputation's query (64 heads) with its weights and statistics, staged in LDS: issued with the
+  // score loads (one round trip for both) although the candidates are known only after the threshold (one
+  // 16-byte q chunk per thread; every thread writes head entry tid % 64, identical writes)
+  {
+    static_assert(kRecH * kRecC == kTopkThreads, "one q chunk per thread");
+    const int64_t qrow0 = row * kRecH;  // rows of q, w and the q statistics: (b S + s) 64 + head
+    const int h = tid / kRecC, c = tid % kRecC, hh = tid & (kRecH - 1);
+    const uint4 qv = *reinterpret_cast<const uint4 *>(rc.q + (qrow0 + h) * kRecD + 8 * c);
+    const float wv = rc.w[qrow0 + hh], qnv = rc.qn[qrow0 + hh];
+    const int32_t qsv = rc.qsp[qrow0 + hh];
+    rs.q[h * kRecC + (c ^ (h & 15))] = qv;
+    rs.w[hh] = wv;
+    rs.qn[hh] = qnv;
+    rs.qsp[hh] = qsv;
+  }
   // keys of the lower and upper ends (equal, and exact, where the bound is 0)
   // every load is issued before the first wait: columns past the slice's valid part read its column 0 (in
   // bounds: c0 < T) and are masked afterwards, so no load sits behind a branch
@@ -608,22 +623,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     uint32_t ncand = 0;
     for (int w = 0; w < kTopkWaves; ++w) ncand += sh.wsum[w];
     int32_t *list = reinterpret_cast<int32_t *>(cand);
-    const int64_t qrow0 = row * kRecH;  // rows of q, w and the q statistics: (b S + s) 64 + head
     const int64_t kbrow0 = b * rc.kbs;
-    if (ncand > 0) {
-      // one round trip: the q rows (one 16-byte chunk per thread) and the head weights and statistics (every
-      // thread loads and writes entry tid % 64: identical writes, so neither the loads nor the stores sit
-      // behind a branch)
-      static_assert(kRecH * kRecC == kTopkThreads, "one q chunk per thread");
-      const int h = tid / kRecC, c = tid % kRecC, hh = tid & (kRecH - 1);
-      const uint4 qv = *reinterpret_cast<const uint4 *>(rc.q + (qrow0 + h) * kRecD + 8 * c);
-      const float wv = rc.w[qrow0 + hh], qnv = rc.qn[qrow0 + hh];
-      const int32_t qsv = rc.qsp[qrow0 + hh];
-      rs.q[h * kRecC + (c ^ (h & 15))] = qv;
-      rs.w[hh] = wv;
-      rs.qn[hh] = qnv;
-      rs.qsp[hh] = qsv;
-    }
     const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
     float *srow = const_cast<float *>(scores + row * ld);
     uint32_t n_exact = 0, n_unres = 0;

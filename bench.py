@@ -194,7 +194,7 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
     bnd = torch.empty(B, S, T, dtype=torch.float32, device="cuda")
     kmax = torch.empty(B, (T + 255) // 256, dtype=torch.float32, device="cuda")
     idx = torch.empty(B, S, min(p["k_top"], T), dtype=torch.int32, device="cuda")
-    part = torch.empty(B * S * 4 * 2048, dtype=torch.int64, device="cuda")  # the split top-k's slice lists
+    part = torch.empty(B * S * 4 * (2048 + 1024), dtype=torch.int64, device="cuda")  # split top-k: lists, histograms
     from kernelswift_amd import _lib
     lib = _lib.load()
     (qn, qs), (kn, ks_) = stats

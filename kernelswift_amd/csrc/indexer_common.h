@@ -126,12 +126,14 @@ struct TopkRecompute {
   float bound_c;
   uint32_t *stats;  // optional: [0] += exact dot recomputations, [1] += dots outside the exact range
   int stats_ext;    // with stats: [2] += recomputed scores
-  // optional: room for rows x slices x k sorted composites.  With it, rows too few to fill the GPU are
-  // split into column slices, each selecting its own exact top k; a merge kernel ranks the slices' lists.
+  // optional: room for rows x slices x (k sorted composites + 2048 32-bit bucket counts).  With it, rows
+  // too few to fill the GPU are split into column slices, each selecting its own exact top k (candidates
+  // for recomputation taken against a threshold from the whole row's bucket counts, computed first); a
+  // merge kernel ranks the slices' lists.
   uint64_t *part;
-  int64_t part_cap;  // composites
+  int64_t part_cap;  // 64-bit slots
 };
-// Composites the split selection needs for `rows` rows (k <= 2048): the workspace reserved for rc.part.
+// Slots the split selection needs for `rows` rows (k <= 2048): the workspace reserved for rc.part.
 int64_t topk_bounded_part_capacity(int64_t rows);
 int launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
                                 int causal, int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,

@@ -608,11 +608,36 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
   __syncthreads();
 
   if (k_sel > 0) {
-    // ---- tau: lower edge of the 22-bit bucket holding the k_sel-th largest lower end
-    radix_pass<KPT>(lok, 0u, 0u, 21, 2048, sh, 0);
-    const uint32_t d1 = sh.digit;
-    radix_pass<KPT>(lok, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
-    const uint32_t tau = (d1 << 21) | (sh.digit << 10);
+    // ---- tau: lower edge of the 22-bit bucket holding the k_sel-th largest lower end; a slice takes the
+    // lower edge of the 11-bit bucket holding its row's k-th largest lower end (from topk_slice_hist_kernel's
+    // counts), which no exact score of the row's top k lies below (hist[0], cleared above, then stays clear
+    // for the selection)
+    uint32_t tau;
+    if (slice_out != nullptr) {
+      // the row's first-digit histogram: the sum of its slices' (stored after the slices' lists); bucket
+      // scan as in radix_pass, for the row's k_sel-th largest lower end
+      const int k_row = k < n_valid ? k : n_valid;
+      const uint32_t *rh = reinterpret_cast<const uint32_t *>(part + static_cast<int64_t>(gridDim.x) * gridDim.y * k) +
+                           row * gridDim.y * 2048;
+      const int hi = 2047 - 2 * tid;  // two buckets per thread, scanned from the top
+      uint32_t c_hi = 0, c_lo = 0;
+      for (int p = 0; p < static_cast<int>(gridDim.y); ++p) {
+        c_hi += rh[p * 2048 + hi];
+        c_lo += rh[p * 2048 + hi - 1];
+      }
+      const uint32_t mine = c_hi + c_lo;
+      const uint32_t incl = block_inclusive_scan<false>(mine, sh.wsum);
+      const uint32_t excl = incl - mine;
+      const uint32_t kr = static_cast<uint32_t>(k_row);
+      if (excl < kr && incl >= kr) sh.digit = static_cast<uint32_t>(excl + c_hi >= kr ? hi : hi - 1);
+      __syncthreads();
+      tau = sh.digit << 21;
+    } else {
+      radix_pass<KPT>(lok, 0u, 0u, 21, 2048, sh, 0);
+      const uint32_t d1 = sh.digit;
+      radix_pass<KPT>(lok, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
+      tau = (d1 << 21) | (sh.digit << 10);
+    }
     // ---- scores to recompute: U > 0 and score + U >= tau; list ranks from a block scan
     uint32_t cmask = 0;
 #pragma unroll
@@ -666,6 +691,51 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
   if (slice_out == nullptr)
     for (int j = k_sel + tid; j < k; j += kTopkThreads)
       store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
+}
+
+// First-digit histograms of a split row, computed before its slices run: workgroup (row, p) counts the top
+// 11 bits (2048 buckets) of the lower ends (score - U; the score itself where U = 0) of slice p's valid
+// columns and stores the counts.  Each slice of the row then sums the row's histograms and takes as its
+// recomputation threshold the lower edge of the bucket holding the row's k_sel-th largest lower end: no
+// exact score of the row's top k lies below it, and it lies far above a slice's own k-th largest (the
+// k-th of a quarter of the columns), so a slice recomputes far fewer candidates.
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void topk_slice_hist_kernel(const float *scores, const float *bounds,
+                                                                      int64_t ld, int64_t S, int T, int causal,
+                                                                      int64_t start_pos, int ratio, int W,
+                                                                      uint32_t *__restrict__ hist_out) {
+  __shared__ uint32_t hist[2048];
+  const int64_t row = blockIdx.x;
+  const int64_t s = row % S;
+  const int tid = threadIdx.x;
+  int n_valid = T;
+  if (causal) {
+    const int64_t limit = (start_pos + s + 1) / ratio;
+    n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
+  }
+  const int c0 = static_cast<int>(blockIdx.y) * W;
+  const int nv = n_valid - c0 <= 0 ? 0 : (n_valid - c0 < W ? n_valid - c0 : W);
+  const float *src = scores + row * ld + c0;
+  const float *ub = bounds + row * ld + c0;
+  float sv[KPT], uv[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {  // every load before the first wait (column 0 stands in past the prefix)
+    const int col = j * kTopkThreads + tid;
+    sv[j] = src[col < nv ? col : 0];
+    uv[j] = ub[col < nv ? col : 0];
+  }
+  for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if (j * kTopkThreads + tid < nv) {
+      const uint32_t kk = score_key(uv[j] > 0.f ? sv[j] - uv[j] : sv[j]);
+      if (kk != 0) atomicAdd(&hist[kk >> 21], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t *dst = hist_out + (row * gridDim.y + blockIdx.y) * 2048;
+  for (int i = tid; i < 2048; i += kTopkThreads) dst[i] = hist[i];
 }
 
 // Merge of the (at most 4) slices' sorted lists into the row's top k: slices 0 + 1 and 2 + 3 merge into two
@@ -789,11 +859,29 @@ int ks::launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, 
   const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
   const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
   const int np = topk_slices(rows, Ti, ki);
-  if (np > 1 && rc.part != nullptr && rows * np * k <= rc.part_cap) {
+  if (np > 1 && rc.part != nullptr && rows * np * (k + 1024) <= rc.part_cap) {
     // slices of W columns: 1024 times a power of two (W / 1024 keys per thread cover a slice)
     int W = kTopkThreads;
     while (W * np < Ti) W <<= 1;
     const int NP = (Ti + W - 1) / W;
+    // the slices' first-digit histograms first, into the slots after the slices' lists
+    uint32_t *hist = reinterpret_cast<uint32_t *>(rc.part + rows * NP * k);
+    const float *bnd = rc.bounds;
+    const int sc = c;
+    const dim3 hgrid(static_cast<unsigned>(rows), static_cast<unsigned>(NP));
+#define KS_HIST(KPT_)                                                                                            \
+  hipLaunchKernelGGL(topk_slice_hist_kernel<KPT_>, hgrid, dim3(kTopkThreads), 0, st, scores, bnd, ld, S, Ti, sc, \
+                     start_pos, ratio, W, hist)
+    switch (W / kTopkThreads) {
+      case 1: KS_HIST(1); break;
+      case 2: KS_HIST(2); break;
+      case 4: KS_HIST(4); break;
+      case 8: KS_HIST(8); break;
+      case 16: KS_HIST(16); break;
+      default: KS_HIST(32); break;
+    }
+#undef KS_HIST
+    KS_CHECK_LAUNCH("topk_slice_hist_kernel");
     int rcode;
     switch (W / kTopkThreads) {
       case 1: rcode = launch_topk_bounded<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
@@ -823,7 +911,7 @@ int64_t ks::topk_bounded_part_capacity(int64_t rows) {
   if (rows <= 0 || rows >= 256) return 0;
   int64_t p = (256 + rows - 1) / rows;
   if (p > kTopkMaxSlices) p = kTopkMaxSlices;
-  return rows * p * 2048;
+  return rows * p * (2048 + 1024);  // the slices' lists (k <= 2048), then their 2048-bucket histograms
 }
 
 // Diagnostic entry (not part of the public header) of the bounded top-k, for timing it alone: scores and

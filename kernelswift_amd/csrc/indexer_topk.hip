@@ -762,9 +762,25 @@ __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(const uint64_t
     const int nv = p < NP ? (n_valid - p * W <= 0 ? 0 : (n_valid - p * W < W ? n_valid - p * W : W)) : 0;
     len[p] = k < nv ? k : nv;
   }
+  // the (at most 4 x 2048) composites go out in one round trip: two per list and thread (k <= 2048 on the
+  // split path), absent entries reading composite 0 of the row
   const uint64_t *src = part + row * NP * k;
-  for (int p = 0; p < NP; ++p)
-    for (int i = tid; i < len[p]; i += kTopkThreads) lists[p * k + i] = src[p * k + i];
+  constexpr int kPer = 2048 / kTopkThreads;
+  uint64_t v[4][kPer];
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kTopkThreads;
+      v[p][j] = src[p < NP && i < len[p] ? p * k + i : 0];
+    }
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kTopkThreads;
+      if (p < NP && i < len[p]) lists[p * k + i] = v[p][j];
+    }
   __syncthreads();
   uint64_t *pair = lists + 4 * k;
   const int na = len[0] + len[1] < k ? len[0] + len[1] : k, nb = len[2] + len[3] < k ? len[2] + len[3] : k;
@@ -859,7 +875,7 @@ int ks::launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, 
   const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
   const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
   const int np = topk_slices(rows, Ti, ki);
-  if (np > 1 && rc.part != nullptr && rows * np * (k + 1024) <= rc.part_cap) {
+  if (np > 1 && k <= 2048 && rc.part != nullptr && rows * np * (k + 1024) <= rc.part_cap) {
     // slices of W columns: 1024 times a power of two (W / 1024 keys per thread cover a slice)
     int W = kTopkThreads;
     while (W * np < Ti) W <<= 1;

@@ -385,7 +385,7 @@ struct RecWave {
 // 64 heads; the tile's near-tie dots are then recomputed exactly, 16 at a time with a quad of lanes per dot
 // (q_h and the key row from LDS: exact_dot_bf16's arithmetic), and the fp32 fma head sum runs in the
 // canonical order over the corrected values.
-__device__ void recompute_scores(const int32_t *list, int n, float *srow, const TopkRecompute &rc,
+__device__ void recompute_scores(int32_t *list, int n, float *srow, const TopkRecompute &rc,
                                  const RecShared &rs, RecWave &rw, int64_t kbrow0, int64_t kmax_row0,
                                  uint32_t &n_exact, uint32_t &n_unres) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -530,7 +530,12 @@ __device__ void recompute_scores(const int32_t *list, int n, float *srow, const 
         G = __builtin_fmaf((r & 1) ? unpack_hi(p2) : unpack_lo(p2), rs.w[16 * m + 4 * g + r], G);
       }
     const float tot = combine_groups(G);
-    if (g == 0 && kv) srow[col] = tot;
+    // the score replaces its column in the list too (read back from LDS when the batch is the last one):
+    // the tile's lanes read their list slots (and lanes past n read slot n - 1, of this same tile) before
+    if (g == 0 && kv) {
+      srow[col] = tot;
+      list[li] = __builtin_bit_cast(int32_t, tot);
+    }
   }
 }
 
@@ -668,10 +673,22 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
     // the selection's keys: recomputed scores from the row (the workgroup's waves share one L1: the
     // barrier above orders the rewrites before these loads), exact scores where the bound is 0, and for
     // the other bounded scores the upper end, which lies below tau like the score itself
-    // (the loads go out together: non-candidates read column c0, a broadcast, and keep their upper end)
+    // (the loads go out together: non-candidates read column c0, a broadcast, and keep their upper end);
+    // with a single batch every recomputed score is still in its list slot in LDS
     float rsv[KPT];
+    if (ncand <= static_cast<uint32_t>(lcap)) {  // uniform
+      const float *listf = reinterpret_cast<const float *>(list);
+      uint32_t slot = base;
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) rsv[j] = srow[c0 + (((cmask >> j) & 1u) ? j * kTopkThreads + tid : 0)];
+      for (int j = 0; j < KPT; ++j) {
+        const bool cj = (cmask >> j) & 1u;
+        rsv[j] = cj ? listf[slot] : 0.f;
+        slot += cj ? 1u : 0u;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) rsv[j] = srow[c0 + (((cmask >> j) & 1u) ? j * kTopkThreads + tid : 0)];
+    }
     uint32_t key[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; ++j) key[j] = ((cmask >> j) & 1u) ? score_key(rsv[j]) : hik[j];

@@ -949,8 +949,9 @@ int64_t ks::topk_bounded_part_capacity(int64_t rows) {
 
 // Diagnostic entry (not part of the public header) of the bounded top-k, for timing it alone: scores and
 // bounds from ks_dbg_indexer_scores_bounded over rotated q / k (with their row statistics); the scores
-// that are recomputed are rewritten in place.  ratio 1, int32 output.  part (optional, part_cap composites,
-// topk_bounded_part_capacity(B S) of them) enables the split selection.
+// that are recomputed are rewritten in place.  ratio 1, int32 output.  part (optional, part_cap 64-bit slots,
+// topk_bounded_part_capacity(B S) of them: the slices' lists, then their bucket counts) enables the split
+// selection.
 extern "C" int ks_dbg_indexer_topk_bounded(float *scores, const float *bounds, const float *kmax, const uint16_t *q,
                                            const uint16_t *k, const float *w, const float *q_norm,
                                            const int32_t *q_span, const float *k_norm, const int32_t *k_span,

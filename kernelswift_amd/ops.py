@@ -33,7 +33,14 @@ def _on_gpu(*ts: torch.Tensor, contiguous: bool = True) -> None:
         _check(not contiguous or t.is_contiguous(), "tensors must be contiguous")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """The current HIP stream of t's device as a raw handle (torch's raw query when present: it skips building
+    a Stream object on every call, which host-bound small launches pay for)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -10,6 +10,7 @@ missing library or an unsupported shape raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import Optional
 
 import torch
@@ -147,6 +148,7 @@ def topk_mask(scores: torch.Tensor, causal: bool, ratio: int, actual_t: int, off
     return out
 
 
+@functools.lru_cache(maxsize=256)  # a pure function of the shape: cached so that calls pay no C round trip
 def indexer_workspace_size(B: int, S: int, H: int, D: int, T: int) -> int:
     return int(_lib.load().ks_indexer_workspace_size(B, S, H, D, T))
 
@@ -194,6 +196,7 @@ def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Opti
 
 
 # ---------------------------------------------------------------- sparse attention
+@functools.lru_cache(maxsize=256)  # a pure function of the shape
 def sparse_attn_workspace_size(B: int, M: int, H: int, Dqk: int, Dv: int, K: int) -> int:
     return int(_lib.load().ks_sparse_attn_workspace_size(B, M, H, Dqk, Dv, K))
 

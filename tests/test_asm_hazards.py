@@ -67,3 +67,44 @@ def test_mla_kernels_have_no_mfma_hazards(tmp_path):
     assert len(syms) >= 4, syms
     bad = [v for s in syms for v in asm_hazards.check(asm, s)]
     assert bad == [], "\n".join(bad[:10])
+
+
+def _m0_misuse(asm: str, symbol: str):
+    """Instructions of `symbol` that touch m0 other than the LDS-DMA helper's own sequence
+    (s_mov_b32 m0, ...; s_nop 0; global_load_lds_dwordx4): the helper declares m0 clobbered, which the
+    compiler does not honour for a reserved register, so no compiler-generated use of m0 may exist."""
+    blocks, _ = asm_hazards.parse_kernel(asm, symbol)
+    bad = []
+    for blk in blocks:
+        for i, ins in enumerate(blk):
+            if "m0" not in ins.operands:
+                continue
+            ok = (ins.op == "s_mov_b32" and ins.operands[0] == "m0" and i + 2 < len(blk)
+                  and blk[i + 1].op == "s_nop" and blk[i + 2].op == "global_load_lds_dwordx4")
+            if not ok:
+                bad.append(f"{symbol}: '{ins.text}'")
+    return bad
+
+
+def test_m0_checker_pins():
+    good = _prog("\ts_mov_b32 m0, s4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 v1, s[2:3]\n\ts_endpgm")
+    assert _m0_misuse(good, "_Zk") == []
+    bad = _prog("\ts_mov_b32 m0, s4\n\tv_movrels_b32 v0, v1\n\ts_endpgm")
+    assert len(_m0_misuse(bad, "_Zk")) == 1
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc is not installed")
+def test_lds_dma_kernels_use_m0_only_for_the_dma(tmp_path):
+    sys.path.insert(0, REPO)
+    from kernelswift_amd import build as ksbuild
+    src = os.path.join(REPO, "kernelswift_amd", "csrc", "sparse_attn.hip")
+    out = tmp_path / "sparse_attn_m0.s"
+    r = subprocess.run([ksbuild.HIPCC, *ksbuild.COMMON, "--cuda-device-only", "-S", src, "-o", str(out)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    asm = out.read_text()
+    syms = asm_hazards.kernel_symbols(asm, "sparse_attn")
+    assert syms
+    bad = [v for s in syms for v in _m0_misuse(asm, s)]
+    assert bad == [], "\n".join(bad[:10])

@@ -53,6 +53,7 @@ DEBUG_SIGNATURES = {
     "ks_dbg_indexer_scores": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
                                              _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32, _c_f, _c_p,
                                              _c_p]),
+    "ks_dbg_mfma_bf16_chain": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),
 }
 
 _lib = None

@@ -54,6 +54,8 @@ DEBUG_SIGNATURES = {
                                              _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32, _c_f, _c_p,
                                              _c_p]),
     "ks_dbg_mfma_bf16_chain": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),
+    "ks_dbg_exact_dot_wide": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_p]),
+    "ks_dbg_score_bound_c": (ctypes.c_float, []),
 }
 
 _lib = None

@@ -119,59 +119,89 @@ __device__ __forceinline__ uint16_t bf16_abs_round_up(float w) {
   return static_cast<uint16_t>((u + 0xFFFFu) >> 16);
 }
 
-// Exact dot product of two bf16 rows of length KD rounded once to bf16 (RNE), computed by a quad of lanes:
-// lane quarter `sub` multiplies elements KD/4 sub .. KD/4 (sub + 1) - 1 in double precision, and a DPP
-// quad reduction adds the quarters.  span_sum = span(q row) + span(k row) (row statistics) proves the
-// path exact: every partial sum is a multiple of the smallest product LSB and stays below 2^53 of it when
-// span_sum <= 52 (plain double sums); up to 84 the products above / below 2^(top - 38) accumulate
-// separately (top = exponent of norm_q * norm_k), each exactly, and one TwoSum-based rounding combines
-// them.  Beyond 84 the result is not exact: `exact` is cleared and the lower interval end is the caller's
-// choice.  FAST (wave-uniform): every quad of the wave has span_sum <= 52.
-template <int KD>
-__device__ uint16_t exact_dot_bf16(const uint16_t *__restrict__ qrow, const uint16_t *__restrict__ krow, int sub,
-                                   int span_sum, float qnorm, float knorm, bool fast, bool &exact) {
-  constexpr int kLC = KD / 32;  // 16-byte chunks per lane
-  exact = span_sum <= 84;
-  if (fast) {
-    const uint4 *qp = reinterpret_cast<const uint4 *>(qrow + (KD / 4) * sub);
-    const uint4 *kp = reinterpret_cast<const uint4 *>(krow + (KD / 4) * sub);
-    uint4 qc[kLC], kc[kLC];
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp_i64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u), CTRL, 0xF, 0xF, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, static_cast<uint32_t>(u >> 32), CTRL, 0xF, 0xF, false);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Exact dot product of two bf16 rows of length KD, rounded once to bf16 (RNE), for rows of any dynamic
+// range: a fixed-point integer accumulator whose bit i weighs 2^(i - 266).  Every bf16 value is m 2^l with
+// |m| < 2^8 and l >= -133, so every product is an integer multiple of 2^-266 below 2^256, and the sum of
+// 128 products stays below 2^540: 18 limbs of 30 bits, held in int64 so that carries can wait until the
+// end.  The PARTS (2 or 4) adjacent lanes of a group each add the products of KD / PARTS consecutive
+// elements (part = the lane's index in the group); DPP quad permutes sum the limbs.  qword(j) / kword(j)
+// return elements 2j and 2j + 1 of the rows packed in a uint32.  Slow (every product touches the limbs
+// through selects), and used only for dots whose spans exceed the double-precision paths.
+template <int KD, int PARTS, class QW, class KW>
+__device__ __attribute__((noinline)) uint16_t exact_dot_wide_bf16(QW qword, KW kword, int part) {
+  static_assert(PARTS == 2 || PARTS == 4, "pairs or quads of lanes");
+  constexpr int kNL = 18, kW = KD / 2 / PARTS;
+  int64_t L[kNL];
 #pragma unroll
-    for (int c = 0; c < kLC; ++c) {
-      qc[c] = qp[c];
-      kc[c] = kp[c];
-    }
-    double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-    for (int c = 0; c < kLC; ++c) {
-      const uint32_t qw[4] = {qc[c].x, qc[c].y, qc[c].z, qc[c].w};
-      const uint32_t kw[4] = {kc[c].x, kc[c].y, kc[c].z, kc[c].w};
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        a0 = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), a0);
-        a1 = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), a1);
-      }
-    }
-    const double sum = quad_sum_f64(a0 + a1);
-    const bool outside = sum != 0.0 && !(fabs(sum) >= 0x1p-126 && fabs(sum) < 0x1p127);
-    if (__builtin_amdgcn_ballot_w64(outside) == 0ull) return round_to_bf16_fast(sum);
-    return round_dir_to_bf16(sum, 0);
-  }
-  const int top_sum = frexp_exp(qnorm) + frexp_exp(knorm);
-  const bool split = span_sum > 52;
-  const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
-  double hi = 0.0, lo = 0.0;
-  const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qrow + (KD / 4) * sub);
-  const uint32_t *k32 = reinterpret_cast<const uint32_t *>(krow + (KD / 4) * sub);
+  for (int i = 0; i < kNL; ++i) L[i] = 0;
 #pragma unroll 1
-  for (int j = 0; j < KD / 8; ++j) {
-    const uint32_t qw = q32[j], kw = k32[j];
-    const double p0 = static_cast<double>(unpack_lo(qw)) * static_cast<double>(unpack_lo(kw));
-    const double p1 = static_cast<double>(unpack_hi(qw)) * static_cast<double>(unpack_hi(kw));
-    if (!split || fabs(p0) >= thr) hi += p0; else lo += p0;
-    if (!split || fabs(p1) >= thr) hi += p1; else lo += p1;
+  for (int j = part * kW; j < (part + 1) * kW; ++j) {
+    const uint32_t qw = qword(j), kw = kword(j);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t a = h ? (qw >> 16) : (qw & 0xFFFFu), b = h ? (kw >> 16) : (kw & 0xFFFFu);
+      if ((a & 0x7FFFu) == 0u || (b & 0x7FFFu) == 0u) continue;
+      const int ea = static_cast<int>((a >> 7) & 0xFFu), eb = static_cast<int>((b >> 7) & 0xFFu);
+      const int64_t ma = static_cast<int64_t>((a & 0x7Fu) | (ea ? 0x80u : 0u));
+      const int64_t mb = static_cast<int64_t>((b & 0x7Fu) | (eb ? 0x80u : 0u));
+      const int o = (ea ? ea - 134 : -133) + (eb ? eb - 134 : -133) + 266;  // 0 .. 506
+      const int li = o / 30, sh = o - 30 * li;
+      const int64_t v = (((a ^ b) & 0x8000u) ? -(ma * mb) : ma * mb) * (int64_t(1) << sh);  // |v| < 2^46
+      const int64_t lo = v & 0x3FFFFFFF, hi = v >> 30;  // v = hi 2^30 + lo, 0 <= lo < 2^30
+#pragma unroll
+      for (int i = 0; i < kNL; ++i) L[i] += (i == li ? lo : 0) + (i == li + 1 ? hi : 0);
+    }
   }
-  return round2_to_bf16(quad_sum_f64(hi), quad_sum_f64(lo));
+#pragma unroll
+  for (int i = 0; i < kNL; ++i) {
+    L[i] += dpp_i64<0xB1>(L[i]);                       // quad_perm [1, 0, 3, 2]: the pair
+    if constexpr (PARTS == 4) L[i] += dpp_i64<0x4E>(L[i]);  // quad_perm [2, 3, 0, 1]: the other pair
+  }
+  auto normalize = [&]() {  // limbs 0..16 into [0, 2^30), the signed remainder in limb 17
+#pragma unroll
+    for (int i = 0; i + 1 < kNL; ++i) {
+      const int64_t c = L[i] >> 30;
+      L[i] -= c * (int64_t(1) << 30);
+      L[i + 1] += c;
+    }
+  };
+  normalize();
+  const bool neg = L[kNL - 1] < 0;
+  if (neg) {
+#pragma unroll
+    for (int i = 0; i < kNL; ++i) L[i] = -L[i];
+    normalize();
+  }
+  int P = -1;  // position of the leading bit of the magnitude
+#pragma unroll
+  for (int i = kNL - 1; i >= 0; --i)
+    if (P < 0 && L[i] != 0) P = 30 * i + 63 - __builtin_clzll(static_cast<uint64_t>(L[i]));
+  if (P < 0) return 0;  // exact zero: +0
+  const int lbit = P - 7 > 133 ? P - 7 : 133;  // the bf16 result's last bit (2^-133 is bit 133)
+  const int s = lbit - 1, q = s / 30, r = s - 30 * q;  // rounding bit at bit r of limb q
+  uint64_t lq = 0, lq1 = 0;
+  bool sticky = false;
+#pragma unroll
+  for (int i = 0; i < kNL; ++i) {
+    const uint64_t li = static_cast<uint64_t>(L[i]);
+    lq = i == q ? li : lq;
+    lq1 = i == q + 1 ? li : lq1;
+    sticky = sticky || (i < q && li != 0u) || (i == q && (li & ((uint64_t(1) << r) - 1u)) != 0u);
+  }
+  const uint64_t w = (lq >> r) | (lq1 << (30 - r));  // bit 0: rounding bit; bits 1..8: the kept bits
+  uint32_t kept = static_cast<uint32_t>(w >> 1) & 0x1FFu;
+  if ((w & 1u) && (sticky || (kept & 1u))) ++kept;
+  uint32_t bits = P - 7 >= 133 ? (static_cast<uint32_t>(P - 139) << 7) + kept - 128u : kept;
+  if (bits >= 0x7F80u) bits = 0x7F80u;  // beyond the bf16 range: infinity
+  return static_cast<uint16_t>((neg ? 0x8000u : 0u) | bits);
 }
 
 }  // namespace

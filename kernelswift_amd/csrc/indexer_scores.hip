@@ -16,15 +16,17 @@
 // output layout lane l holds heads 16m + 4(l/16) + r (r = 0..3) of key l % 16, i.e. exactly the canonical
 // head group g = l/16, so the head sum runs in-lane and two permlane swaps finish ((G0+G1)+(G2+G3)).
 //
-// Exactness: the MFMA fp32 sum A differs from the exact dot by less than
-//   delta = C * 2^-23 * ||q_h|| * max_t ||k_t||   (C = kScoreBoundC, a measured error model),
-// so the relu'd bf16 value is exact when RNE(A - delta) and RNE(A + delta) agree after the ReLU (one packed
-// convert and one packed max per pair of dots and interval end).  Keys with a disagreeing ("near-tie") dot
-// are deferred: both interval ends of all their head groups go to a per-wave LDS list, and when the list
-// fills (and at the end) the near-tie dots are recomputed exactly, 16 at a time with 4 lanes per dot, and
-// the affected scores rewritten.  Per-row spans from the statistics pass prove every partial sum of the
-// exact dot representable in a double (span_q + span_k <= 52); up to 84 a hi/lo split keeps both halves
-// exact; beyond that the dot keeps the lower interval end and is counted as unresolved.
+// Exactness: the MFMA fp32 sum A differs from the exact dot by at most the half-width
+//   delta = C * 2^-23 * (||q_h|| + 2^-122)(max_t ||k_t|| + 2^-122) + 2^-144   (C = kScoreBoundC = 13),
+// derived from the instruction's accumulation (see dot_halfwidth), so the relu'd bf16 value is exact when
+// RNE(A - delta) and RNE(A + delta) agree after the ReLU (one packed convert and one packed max per pair of
+// dots and interval end).  Keys with a disagreeing ("near-tie") dot are deferred: both interval ends of all
+// their head groups go to a per-wave LDS list, and when the list fills (and at the end) the near-tie dots
+// are recomputed exactly, 16 at a time with 4 lanes per dot, and the affected scores rewritten.  Per-row
+// spans from the statistics pass prove every partial sum of the exact dot representable in a double
+// (span_q + span_k <= 52); up to 84 a hi/lo split keeps both halves exact; beyond that an integer
+// accumulator (exact_dot_wide_bf16) computes the dot.  A wave whose norms could overflow inside the MFMA
+// ((||q|| ||k|| >= 2^126) treats every dot as a near tie.
 #include "common.h"
 #include "indexer_common.h"
 #include "indexer_exact.h"
@@ -200,14 +202,21 @@ __device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, co
         }
         r = round2_to_bf16(quad_sum_f64(hi), quad_sum_f64(lo));
       }
+      if (scur > 84) {
+        // wider still (the whole quad takes this branch): the integer accumulator, any range
+        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(q + (qrow0 + h) * KD);
+        r = exact_dot_wide_bf16<KD, 4>(
+            [&](int j) { return q32[j]; },
+            [&](int j) {
+              return reinterpret_cast<const uint32_t *>(&L.k[kl * kC + ((j >> 2) ^ (kl & (kC - 1)))])[j & 3];
+            },
+            sub);
+      }
       const uint32_t rv = (r & 0x8000) ? 0u : r;  // ReLU (also maps -0 to +0)
       if (sub == 0 && b0 + dq < nd) {
-        if (scur <= 84) {
-          uint16_t *half = reinterpret_cast<uint16_t *>(&E[pr >> 2].pl[pr & 3][slot >> 1]) + (slot & 1);
-          *half = static_cast<uint16_t>(rv);
-        } else {
-          ++n_unres;
-        }
+        uint16_t *half = reinterpret_cast<uint16_t *>(&E[pr >> 2].pl[pr & 3][slot >> 1]) + (slot & 1);
+        *half = static_cast<uint16_t>(rv);
+        if (scur > 84) ++n_unres;  // counted: dots that needed the integer accumulator
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -356,8 +365,15 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     for (int r = 0; r < 4; ++r) {
       const int h = 16 * m + 4 * g + r;
       wv[m][r] = L.w[wave][h];
-      dl[m][r] = bound_c * 0x1p-23f * L.qnorm[wave][h] * knm;
+      dl[m][r] = dot_halfwidth(L.qnorm[wave][h], knm, bound_c);
     }
+  // a half-width of +inf (norms that could overflow inside the MFMA): every dot of the wave is a near tie
+  bool any_inf = false;
+#pragma unroll
+  for (int m = 0; m < HT; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) any_inf = any_inf || dl[m][r] == __builtin_inff();
+  const bool forced = __builtin_amdgcn_ballot_w64(any_inf) != 0ull;
 
   // BOUND: A-fragments holding bf16 upper bounds of |w| for the two 32-head halves.  With the relu'd
   // interval ends of a tile as B-fragments (lane (l16, g) holds heads 4g + 0..3 and 16 + 4g + 0..3 of
@@ -416,6 +432,14 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
         ph[2 * m + rp] = cvt_relu_pk(A0 + d0, A1 + d1);
         anyr |= __builtin_amdgcn_ballot_w64(pl[2 * m + rp] != ph[2 * m + rp]);
       }
+    if (forced) {  // wave-uniform and rare: A may not even be finite; the exact values replace everything
+#pragma unroll
+      for (int p = 0; p < 2 * HT; ++p) {
+        pl[p] = 0u;
+        ph[p] = 0x7F807F80u;
+      }
+      anyr = ~0ull;
+    }
     // canonical head sum of this lane's group, then ((G0+G1)+(G2+G3)) across the rows
     float G = 0.f;
 #pragma unroll
@@ -438,16 +462,18 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     if constexpr (BOUND) {
       // |exact score - tot| <= sum_h |w_h| (ph_h - pl_h) + (rounding of the canonical sum: 38 roundings of
       // at most 2^-24 of sum_h |w_h| ph_h, < 2^-18 of it) <= dph - dpl + 2^-16 (dph + dpl), dph / dpl the
-      // MFMA sums of w_up * ph / pl (64 nonnegative exact products: relative error < 63 * 2^-23 < 2^-17
-      // even with truncating additions).  The 2^-21 |tot| term lets tot -/+ bound be rounded to nearest and
-      // stay a bound.  Keys without a near-tie dot have bound 0 (tot is exact).
+      // MFMA sums of w_up * ph / pl (64 nonnegative exact products in 8 accumulation steps: relative error
+      // below (8 + 8) 2^-24 < 2^-19 by the step model of dot_halfwidth, the 2^-100 term covering subnormal
+      // operands).  The 2^-21 |tot| term lets tot -/+ bound be rounded to nearest and stay a bound.  Keys
+      // without a near-tie dot have bound 0 (tot is exact).
       f32x4_t dph = f32x4_t{0.f, 0.f, 0.f, 0.f}, dpl = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         dph = mfma16(wa[hh], make_uint4(ph[4 * hh], ph[4 * hh + 1], ph[4 * hh + 2], ph[4 * hh + 3]), dph);
         dpl = mfma16(wa[hh], make_uint4(pl[4 * hh], pl[4 * hh + 1], pl[4 * hh + 2], pl[4 * hh + 3]), dpl);
       }
-      const float u = (dph[0] - dpl[0]) + 0x1p-16f * (dph[0] + dpl[0]) + 0x1p-21f * fabsf(tot) + 0x1p-100f;
+      float u = (dph[0] - dpl[0]) + 0x1p-16f * (dph[0] + dpl[0]) + 0x1p-21f * fabsf(tot) + 0x1p-100f;
+      if (forced) u = __builtin_inff();  // score 0 with an infinite bound: always recomputed
       if (g == 0 && kvalid) urow[key] = (key < limit && ((km >> l16) & 1u)) ? u : 0.f;
     }
     return km;
@@ -623,6 +649,9 @@ extern "C" int ks_indexer_scores(const uint16_t *q, const uint16_t *k, const voi
                                    T, k_batch_stride, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC, nullptr,
                                    static_cast<hipStream_t>(stream));
 }
+
+// Diagnostic (not part of the public header): the interval constant the public entry points use.
+extern "C" float ks_dbg_score_bound_c(void) { return ks::kScoreBoundC; }
 
 // Diagnostic variant (not part of the public header): explicit error-bound constant and a device counter
 // pair stats[0] += exact recomputations, stats[1] += dots outside the provably exact range.

@@ -415,13 +415,15 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, const TopkRe
 #pragma unroll
       for (int rp = 0; rp < 2; ++rp) {
         const int h0 = 16 * m + 4 * g + 2 * rp;
-        const float d0 = rc.bound_c * 0x1p-23f * rs.qn[h0] * knm, d1 = rc.bound_c * 0x1p-23f * rs.qn[h0 + 1] * knm;
+        const float d0 = dot_halfwidth(rs.qn[h0], knm, rc.bound_c), d1 = dot_halfwidth(rs.qn[h0 + 1], knm, rc.bound_c);
         const uint32_t lo = cvt_relu_pk(acc[2 * rp] - d0, acc[2 * rp + 1] - d1);
         const uint32_t hi = cvt_relu_pk(acc[2 * rp] + d0, acc[2 * rp + 1] + d1);
         pl[2 * m + rp] = lo;
         const uint32_t x = lo ^ hi;
-        ntm |= ((x & 0xFFFFu) != 0u && kv ? 1u : 0u) << (4 * m + 2 * rp);
-        ntm |= ((x >> 16) != 0u && kv ? 1u : 0u) << (4 * m + 2 * rp + 1);
+        // an infinite half-width (norms that could overflow inside the MFMA) makes the dot a near tie even
+        // when A itself is not finite
+        ntm |= (((x & 0xFFFFu) != 0u || d0 == __builtin_inff()) && kv ? 1u : 0u) << (4 * m + 2 * rp);
+        ntm |= (((x >> 16) != 0u || d1 == __builtin_inff()) && kv ? 1u : 0u) << (4 * m + 2 * rp + 1);
       }
     }
     if (__builtin_amdgcn_ballot_w64(ntm != 0u) != 0ull) {
@@ -492,9 +494,17 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, const TopkRe
           uint16_t v;
           if (!split && (hi == 0.0 || (fabs(hi) >= 0x1p-126 && fabs(hi) < 0x1p127))) v = round_to_bf16_fast(hi);
           else v = round2_to_bf16(hi, lo);
+          if (span > 84) {
+            // wider still (the whole pair takes this branch): the integer accumulator, any range
+            v = exact_dot_wide_bf16<kRecD, 2>(
+                [&](int j) { return reinterpret_cast<const uint32_t *>(&rs.q[h * kRecC + ((j >> 2) ^ (h & 15))])[j & 3]; },
+                [&](int j) { return reinterpret_cast<const uint32_t *>(&rw.k[kl * kRecC + ((j >> 2) ^ kl)])[j & 3]; },
+                sub);
+            if (sub == 0 && b0 + dq < ns) ++n_unres;  // counted: dots that needed the integer accumulator
+          }
           const uint16_t rv = (v & 0x8000u) ? 0 : v;  // ReLU (also maps -0 to +0)
           // each pair reads only its own entry before this write (the value replaces the entry)
-          if (sub == 0 && b0 + dq < ns) rw.ent[b0 + dq] = span <= 84 ? rv : 0xFFFFu;
+          if (sub == 0 && b0 + dq < ns) rw.ent[b0 + dq] = rv;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -505,15 +515,11 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, const TopkRe
           mm &= mm - 1;
           if (p >= s0 && p < s0 + ns) {
             const uint16_t v = rw.ent[p - s0];
-            if (v != 0xFFFFu) {
-              const int m = bit >> 2, r = bit & 3;
-              const uint32_t sh = (r & 1) ? 16u : 0u;
-              uint32_t &word = pl[2 * m + (r >> 1)];
-              word = (word & ~(0xFFFFu << sh)) | (static_cast<uint32_t>(v) << sh);
-              ++n_exact;
-            } else {
-              ++n_unres;
-            }
+            const int m = bit >> 2, r = bit & 3;
+            const uint32_t sh = (r & 1) ? 16u : 0u;
+            uint32_t &word = pl[2 * m + (r >> 1)];
+            word = (word & ~(0xFFFFu << sh)) | (static_cast<uint32_t>(v) << sh);
+            ++n_exact;
           }
           ++p;
         }

@@ -14,6 +14,11 @@ from kernelswift_amd import _lib
 pytestmark = pytest.mark.gpu
 
 bits = workloads.bf16_bits
+BOUND_C = 13.0  # the interval constant derived for the MFMA accumulation (checked against the library below)
+
+
+def test_bound_constant_is_the_derived_one(device):
+    assert _lib.load().ks_dbg_score_bound_c() == BOUND_C
 
 
 def _u16(t):
@@ -68,7 +73,7 @@ def _scores_gpu(q, k, w, causal, start_pos, ratio=1, bound_c=None):
     rc = lib.ks_dbg_indexer_scores(qd.data_ptr(), kd.data_ptr(), wd.data_ptr(), 1 if w.dtype == torch.bfloat16 else 0,
                                    qn.data_ptr(), qs.data_ptr(), kn.data_ptr(), ks_.data_ptr(), out.data_ptr(),
                                    B, S, H, D, T, T, 1 if causal else 0, start_pos, ratio,
-                                   3.0 if bound_c is None else bound_c, st.data_ptr(),
+                                   BOUND_C if bound_c is None else bound_c, st.data_ptr(),
                                    torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "ks_dbg_indexer_scores")
     torch.cuda.synchronize()
@@ -156,20 +161,152 @@ def test_scores_adversarial_distributions(device, dist):
     assert st[1] == 0
 
 
-def test_scores_outside_exact_range_is_reported(device):
-    # x^3 of N(0,1) without flushing: row magnitudes span up to ~2^90, beyond the proven exact range
-    # (span_q + span_k <= 84).  The kernel must count every near-tie dot it could not resolve, and no
-    # score may differ from the oracle unless such a dot was reported.
+def test_scores_outside_double_range_exact(device):
+    # x^3 of N(0,1) without flushing: row magnitudes span up to ~2^90, beyond the double-precision paths
+    # (span_q + span_k <= 84); such near-tie dots go through the integer accumulator and every score must
+    # still be the oracle's, bit for bit
     g = torch.Generator().manual_seed(11)
     q = (torch.randn(1, 16, 64, 128, generator=g) ** 3).bfloat16()
     k = (torch.randn(1, 1024, 128, generator=g) ** 3).bfloat16()
     w = torch.randn(1, 16, 64, generator=g) / 8
-    print("[case] scores outside exact range", flush=True)
+    print("[case] scores outside the double-precision range", flush=True)
     got, st = _scores_gpu(q, k, w, True, 1024 - 16)
     want = _oracle_scores(q, k, w, True, 1024 - 16)
     mism = int((got.view(np.uint32) != want.view(np.uint32)).sum())
-    print(f"[info] unresolved near-tie dots {int(st[1])}, mismatching scores {mism}", flush=True)
-    assert mism <= int(st[1])
+    print(f"[info] integer-accumulator dots {int(st[1])}, mismatching scores {mism}", flush=True)
+    assert st[1] > 0
+    assert mism == 0
+
+
+def _extreme_rows(rng, n, D):
+    """Rows of bf16 bit patterns with extreme dynamic range: normals from 2^-126 to 2^120, subnormals, zeros,
+    exact cancellation and near-midpoint sums."""
+    rows_q, rows_k = [], []
+    for i in range(n):
+        kind = i % 6
+        if kind == 0:  # any exponent
+            q = rng.choice([-1.0, 1.0], D) * (1 + rng.random(D)) * 2.0 ** rng.integers(-126, 60, D)
+            k = rng.choice([-1.0, 1.0], D) * (1 + rng.random(D)) * 2.0 ** rng.integers(-126, 60, D)
+        elif kind == 1:  # bf16 subnormals next to normals
+            q = rng.standard_normal(D) * 2.0 ** rng.integers(-140, -120, D)
+            k = rng.standard_normal(D) * 2.0 ** rng.integers(-10, 10, D)
+        elif kind == 2:  # exact cancellation: the result is 0 or one tiny product
+            q = rng.standard_normal(D) * 2.0 ** rng.integers(-20, 20, D)
+            k = rng.standard_normal(D)
+            q[D // 2:] = -q[:D // 2]
+            k[D // 2:] = k[:D // 2]
+            q[-1] = 2.0 ** -100 * rng.choice([0.0, 1.0])
+        elif kind == 3:  # a bf16 midpoint from large terms, decided by a term 2^-90 times smaller
+            q = np.zeros(D)
+            k = np.zeros(D)
+            q[0], k[0] = 1.0, 1.0
+            q[1], k[1] = 2.0 ** -8, 1.0
+            q[2], k[2] = rng.choice([-1.0, 1.0]) * 2.0 ** -50, 2.0 ** -48
+        elif kind == 4:  # results beyond the bf16 range (infinity) and just inside it
+            q = rng.choice([-1.0, 1.0], D) * 2.0 ** rng.integers(55, 64, D)
+            k = np.abs(q) * np.sign(q) * rng.choice([0.5, 1.0], D)
+        else:  # results in the bf16 subnormal range
+            q = rng.standard_normal(D) * 2.0 ** -70
+            k = rng.standard_normal(D) * 2.0 ** -62
+        rows_q.append(q)
+        rows_k.append(k)
+    f = lambda x: torch.from_numpy(np.asarray(x, np.float32)).bfloat16()
+    return f(np.stack(rows_q)), f(np.stack(rows_k))
+
+
+@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("parts", [2, 4])
+def test_exact_dot_integer_accumulator(device, D, parts):
+    # the integer-accumulator exact dot (the path beyond the double-precision spans) against the oracle's
+    # big-integer dot, on rows of extreme dynamic range, subnormals, exact cancellation and overflow
+    rng = np.random.default_rng(D + parts)
+    q, k = _extreme_rows(rng, 600, D)
+    print(f"[case] integer-accumulator exact dot D={D} parts={parts}", flush=True)
+    qd, kd = q.to(device), k.to(device)
+    out = torch.empty(q.shape[0], dtype=torch.int16, device=device)
+    _lib.check(_lib.load().ks_dbg_exact_dot_wide(qd.data_ptr(), kd.data_ptr(), out.data_ptr(), q.shape[0], D, parts,
+                                                 torch.cuda.current_stream().cuda_stream), "exact dot")
+    got = out.cpu().numpy().view(np.uint16)
+    qb, kb = _u16(q), _u16(k)
+    want = np.array([oracle.dot_exact(qb[i], kb[i]) for i in range(q.shape[0])], np.uint16)
+    np.testing.assert_array_equal(got, want)
+
+
+def _adversarial_key_pair():
+    """Key 1's dot with the query is a dot whose MFMA accumulation lands above the bf16 midpoint 1 + 2^-8
+    while the exact value lies below it (tests/mfma_model.py: the earlier constant 3 certified the wrong
+    value); key 0's dot is exactly 1.0.  Exactly, both score alike and key 0 ranks first."""
+    from tests.test_mfma_model import adversarial_rows
+    qb, kb = adversarial_rows(22)
+    q = torch.from_numpy(qb.view(np.int16)).view(torch.bfloat16)
+    k1 = torch.from_numpy(kb.view(np.int16)).view(torch.bfloat16)
+    k0 = torch.zeros(128, dtype=torch.bfloat16)
+    k0[0] = 1.0  # q[0] = 1: dot exactly 1
+    return q, k0, k1
+
+
+def test_scores_adversarial_accumulation(device):
+    q1, k0, k1 = _adversarial_key_pair()
+    g = torch.Generator().manual_seed(5)
+    S, H, T = 4, 64, 64
+    q = torch.randn(1, S, H, 128, generator=g).bfloat16()
+    q[0, :, :] = q1  # every head of query 0: the adversarial row
+    k = torch.randn(1, T, 128, generator=g).bfloat16()
+    k[0, 0], k[0, 1] = k0, k1
+    w = (torch.rand(1, S, H, generator=g) + 0.5) / 8
+    print("[case] scores adversarial accumulation", flush=True)
+    got, st = _scores_gpu(q, k, w, False, 0)
+    want = _oracle_scores(q, k, w, False, 0)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert got[0, 0, 0] == got[0, 0, 1]  # the two keys tie exactly
+
+
+@pytest.mark.parametrize("path", [1, 2])
+def test_indexer_adversarial_accumulation(device, path):
+    # the same pair inside the fused indexer (no RoPE, so the rows stay as constructed): exact scores tie,
+    # so key 0 must come first, on the exact path and on the bounded path (recomputation in the top-k)
+    q1, k0, k1 = _adversarial_key_pair()
+    g = torch.Generator().manual_seed(6)
+    S, H, T = 8, 64, 512
+    q = torch.randn(1, S, H, 128, generator=g).bfloat16() * 0.25
+    q[0, :, :] = q1
+    k = torch.randn(1, T, 128, generator=g).bfloat16() * 0.25
+    k[0, 0], k[0, 1] = k0, k1
+    w = (torch.rand(1, S, H, generator=g) + 0.5) / 8
+    print(f"[case] indexer adversarial accumulation path={path}", flush=True)
+    B = 1
+    qd, kd, wd = q.to(device), k.to(device), w.to(device)
+    ws = torch.empty(ops.indexer_workspace_size(B, S, H, 128, T), dtype=torch.uint8, device=device)
+    out = torch.empty(B, S, 16, dtype=torch.int32, device=device)
+    rc = _lib.load().ks_dbg_indexer(qd.data_ptr(), kd.data_ptr(), wd.data_ptr(), 0, None, 0, 0, 0, 0, 16, 0, 0, 1, 0,
+                                    out.data_ptr(), 0, B, S, H, 128, T, T, ws.data_ptr(), ws.numel(),
+                                    torch.cuda.current_stream().cuda_stream, BOUND_C, None, path)
+    _lib.check(rc, "ks_dbg_indexer")
+    got = out.cpu().numpy().astype(np.int64)
+    want = oracle.indexer(_u16(q), _u16(k), w.numpy(), np.zeros((1, 1, 2), np.float32), 16, False, 0, 1, 0, 0, 0,
+                          False)
+    np.testing.assert_array_equal(got, want)
+    assert got[0, 0, 0] == 0 and got[0, 0, 1] == 1
+
+
+def test_scores_norms_beyond_overflow_guard(device):
+    # rows whose norm product reaches 2^126 (the MFMA could overflow): every dot of such a wave is
+    # recomputed exactly; sparse rows keep the exact dots finite
+    g = torch.Generator().manual_seed(9)
+    S, H, T = 3, 16, 96
+    q = torch.zeros(1, S, H, 128)
+    k = torch.randn(1, T, 128, generator=g)
+    idx = torch.randint(0, 128, (S, H, 3), generator=g)
+    for s in range(S):
+        for h in range(H):
+            q[0, s, h, idx[s, h]] = torch.randn(3, generator=g) * 2.0 ** 62
+    k[0, ::7] = k[0, ::7] * 2.0 ** 62
+    q, k = q.bfloat16(), k.bfloat16()
+    w = (torch.rand(1, S, H, generator=g) + 0.5) * 2.0 ** -30
+    print("[case] scores beyond the overflow guard", flush=True)
+    got, st = _scores_gpu(q, k, w, False, 0)
+    want = _oracle_scores(q, k, w, False, 0)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("cfg", [2, 4])
@@ -276,7 +413,7 @@ def test_indexer_adversarial(device, dist):
     _indexer_vs_oracle(q, k, w, tab, 256, True, 1024 - 16, 1, 0, 0, 64, True, 1024)
 
 
-def _dbg_indexer(q, k, w, tab, k_top, causal, start_pos, path, bound_c=3.0, T=None):
+def _dbg_indexer(q, k, w, tab, k_top, causal, start_pos, path, bound_c=None, T=None):
     """ks_dbg_indexer: path 1 = exact scores, 2 = bounded scores with exact recomputation in the top-k.
     Returns (indices, [exact dot recomputations, dots outside the exact range])."""
     B, S, H, D = q.shape
@@ -288,8 +425,8 @@ def _dbg_indexer(q, k, w, tab, k_top, causal, start_pos, path, bound_c=3.0, T=No
     st = torch.zeros(2, dtype=torch.int32, device="cuda")
     rc = _lib.load().ks_dbg_indexer(qd.data_ptr(), kd.data_ptr(), wd.data_ptr(), 0, td.data_ptr(), tab.shape[0], 0, 64,
                                     1, k_top, 1 if causal else 0, start_pos, 1, 0, out.data_ptr(), 0, B, S, H, D, T, T,
-                                    ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream, bound_c,
-                                    st.data_ptr(), path)
+                                    ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream,
+                                    BOUND_C if bound_c is None else bound_c, st.data_ptr(), path)
     _lib.check(rc, "ks_dbg_indexer")
     torch.cuda.synchronize()
     return out.cpu().numpy().astype(np.int64), st.cpu().numpy()

@@ -849,7 +849,7 @@ int launch_topk_bounded_rows(const float *scores, int64_t ld, int64_t rows, int6
 // takes 4 lists), and at least 2k columns per slice.
 constexpr int kTopkMaxSlices = 4;
 inline int topk_slices(int64_t rows, int T, int k) {
-  if (rows >= 256 || T <= 8 * k) return 1;
+  if (rows >= 256 || T <= 4 * k) return 1;
   int p = static_cast<int>((256 + rows - 1) / rows);
   if (p > kTopkMaxSlices) p = kTopkMaxSlices;
   while (p > 1 && T / p < 2 * k) --p;

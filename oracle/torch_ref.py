@@ -43,23 +43,36 @@ def rope_(x: torch.Tensor, cis: torch.Tensor) -> torch.Tensor:
     return x
 
 
-def indexer(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, cis: torch.Tensor, k_top: int, causal: bool,
-            start_pos: int, ratio: int = 1, offset: int = 0, rope_start: int = 0, rope_dim: int = 64,
-            rope_k: bool = True) -> torch.Tensor:
-    """q bf16 [B,S,H,D]; k bf16 [B,T,D]; w fp32 or bf16 [B,S,H]; cis complex64 [n_pos, rope_dim/2]."""
+def indexer_scores(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, cis: torch.Tensor, causal: bool,
+                   start_pos: int, ratio: int = 1, rope_start: int = 0, rope_dim: int = 64,
+                   rope_k: bool = True) -> torch.Tensor:
+    """Scores [B, S, T] by the reference's op sequence: complex RoPE, bf16 einsum, relu_, * w, sum over
+    heads, -inf mask (fp32 with fp32 weights, bf16 with bf16 weights, as torch computes them).
+
+    q bf16 [B,S,H,D]; k bf16 [B,T,D]; w fp32 or bf16 [B,S,H]; cis complex64 [n_pos, rope_dim/2]."""
     B, S, H, D = q.shape
     T = k.shape[1]
     q = q.clone()
     k = k.clone()
-    rope_(q[..., rope_start:rope_start + rope_dim], cis[start_pos:start_pos + S])
-    if rope_k:
-        rope_(k[..., rope_start:rope_start + rope_dim], cis[:T])
+    if rope_dim > 0:
+        rope_(q[..., rope_start:rope_start + rope_dim], cis[start_pos:start_pos + S])
+        if rope_k:
+            rope_(k[..., rope_start:rope_start + rope_dim], cis[:T])
     score = torch.einsum("bshd,btd->bsht", q, k)
     score = (score.relu_() * w.unsqueeze(-1)).sum(dim=2)
     if causal:
         kpos = torch.arange(T).repeat(S, 1)
         lim = (start_pos + torch.arange(1, S + 1)).unsqueeze(1) // ratio
         score += torch.where(kpos >= lim, float("-inf"), 0.0)
+    return score
+
+
+def indexer(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, cis: torch.Tensor, k_top: int, causal: bool,
+            start_pos: int, ratio: int = 1, offset: int = 0, rope_start: int = 0, rope_dim: int = 64,
+            rope_k: bool = True) -> torch.Tensor:
+    """q bf16 [B,S,H,D]; k bf16 [B,T,D]; w fp32 or bf16 [B,S,H]; cis complex64 [n_pos, rope_dim/2]."""
+    S, T = q.shape[1], k.shape[1]
+    score = indexer_scores(q, k, w, cis, causal, start_pos, ratio, rope_start, rope_dim, rope_k)
     kk = min(k_top, T)
     idx = score.topk(kk, dim=-1)[1]
     if causal:

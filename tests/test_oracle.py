@@ -330,3 +330,60 @@ def test_sparse_attn_matches_torch_cpu():
                            sink.numpy(), idx.numpy(), D ** -0.5, dv=48)
     b = torch_ref.sparse_attn(q, kv, sink, idx, D ** -0.5, dv=48).float().numpy()
     np.testing.assert_allclose(b, a, atol=1e-2, rtol=1e-2)
+
+
+# ------------------------------------------------------------------ agreement with the reference's arithmetic
+def test_agreement_with_reference_arithmetic_fp32_weights():
+    """Index lists of the canonical contract and of the reference's torch op sequence differ only where two
+    keys' scores lie within one rounding per dot of each other (tests/agreement.py states the tolerance)."""
+    from tests import agreement
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 48, 64, 128, generator=g).bfloat16()
+    k = torch.randn(1, 900, 128, generator=g).bfloat16()
+    w = torch.randn(1, 48, 64, generator=g) / 8
+    r = agreement.compare(q, k, w, oracle.freqs_table(64, 1024), 128, True, 900 - 48)
+    assert r["positions_within_rounding"] == r["mismatched_positions"]
+    assert r["set_differences_within_rounding"] == r["set_differences"]
+    assert r["set_overlap"] > 0.99
+
+
+def test_agreement_with_reference_arithmetic_bf16_weights():
+    """With bf16 weights (the drop-in's) the reference's scores are bf16; every position where the lists
+    differ holds two keys whose reference scores are exactly equal (CPU torch.topk orders ties arbitrarily)."""
+    from tests import agreement
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 64, 16, 64, generator=g).bfloat16()
+    k = torch.randn(1, 650, 64, generator=g).bfloat16()
+    w = (torch.randn(1, 64, 16, generator=g) / 8).bfloat16()
+    r = agreement.compare(q, k, w, oracle.freqs_table(32, 1024), 128, True, 650 - 64, 1, 32, 32, False)
+    assert r["mismatched_positions"] > 0  # ties do occur at this shape
+    assert r["positions_tied_in_reference_score"] == r["mismatched_positions"]
+    assert r["set_differences_within_rounding"] == r["set_differences"]
+
+
+def test_freqs_table_against_the_mathematics():
+    """oracle.freqs_table (baseline/indexer.py:226-235) against fp64 cos/sin: the fp32 inverse frequencies
+    are within 2^-22 of theta^(-2j/d), every angle is the fp32 rounding of position x inverse frequency,
+    the (cos, sin) pairs are within 2^-23 of the fp64 values of those angles, and within the angle's own
+    rounding of the textbook cos/sin(p theta^(-2j/d)); position 0 is (1, 0) exactly."""
+    d, n = 64, 4096
+    tab = oracle.freqs_table(d, n).astype(np.float64)
+    assert tab.shape == (n, d // 2, 2)
+    j = np.arange(d // 2)
+    inv_exact = 10000.0 ** (-2.0 * j / d)
+    inv32 = (1.0 / (10000.0 ** (torch.arange(0, d, 2).float() / d))).numpy()  # the reference's fp32 formula
+    assert np.all(np.abs(inv32.astype(np.float64) / inv_exact - 1) < 2.0 ** -22)
+    p = np.arange(n, dtype=np.float64)[:, None]
+    ang32 = (p.astype(np.float32) * inv32[None, :]).astype(np.float64)  # fp32 product, as torch.outer
+    np.testing.assert_allclose(tab[..., 0], np.cos(ang32), rtol=0, atol=2.0 ** -23)
+    np.testing.assert_allclose(tab[..., 1], np.sin(ang32), rtol=0, atol=2.0 ** -23)
+    ang = p * inv_exact[None, :]
+    err = np.abs(ang32 - ang) + 2.0 ** -23
+    assert np.all(np.abs(tab[..., 0] - np.cos(ang)) <= err + 2.0 ** -23)
+    assert np.all(np.abs(tab[..., 1] - np.sin(ang)) <= err + 2.0 ** -23)
+    np.testing.assert_array_equal(tab[0, :, 0], 1.0)
+    np.testing.assert_array_equal(tab[0, :, 1], 0.0)
+    # a table with a dropped factor of 2 in the exponent or swapped (cos, sin) fails the checks above
+    bad = np.stack([np.cos(p * 10000.0 ** (-1.0 * j / d)), np.sin(p * 10000.0 ** (-1.0 * j / d))], -1)
+    assert np.max(np.abs(bad - tab)) > 0.1
+    assert np.max(np.abs(tab[..., ::-1] - tab)) > 0.1

@@ -43,6 +43,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--configs", type=str, default="2,1,3,4,5")
     p.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
+    p.add_argument("--no-dropin", action="store_true", help="skip the ModelNew rows at the reference example shapes")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget per CPU baseline sample")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run the 512 MiB calibration copy kernel (for rocprofv3 FETCH/WRITE scaling)")
@@ -101,6 +102,20 @@ def _wall(fn, steps, warmup):
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t0) * 1e3
     return statistics.median(samples), total_ms / steps
+
+
+def _host_issue_us(fn, n=200):
+    """Host time (us) to issue one call: n calls back to back, timed before the final synchronize."""
+    import torch
+    for _ in range(20):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        fn()
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    return (t1 - t0) * 1e6 / n
 
 
 def _cpu_time(fn, budget_s, min_reps=3, max_reps=10):
@@ -175,12 +190,20 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
     T = t["k"].shape[1]
     ws = torch.empty(ops.indexer_workspace_size(B, S, H, D, T), dtype=torch.uint8, device="cuda")
 
-    def step():
+    from kernelswift_amd import _lib
+    tops = _lib.torch_ops()
+
+    def step():  # the torch operator (TORCH_LIBRARY ks_mi355x), as a caller of the op sees it
+        return tops.indexer(t["q"], t["k"], t["w"], t["freqs"], p["k_top"], p["causal"], p["start_pos"], p["ratio"],
+                            p["offset"], p["rope_start"], p["rope_dim"], p["rope_k"], False, None)
+
+    def step_ctypes():
         return ops.indexer(t["q"], t["k"], t["w"], t["freqs"], p["k_top"], p["causal"], p["start_pos"], p["ratio"],
                            p["offset"], p["rope_start"], p["rope_dim"], p["rope_k"], workspace=ws)
 
     dev_med, dev_mean = _events_median(step, steps, warmup)
     wall_med, ms_step = _wall(step, steps, warmup)
+    host = {"torch_op": round(_host_issue_us(step), 2), "ctypes": round(_host_issue_us(step_ctypes), 2)}
 
     # the fused call's kernels alone, on pre-rotated inputs: the bounded score kernel (the dominant one), the
     # bounded top-k (threshold, exact recomputation of the candidates, exact selection), and for reference
@@ -195,7 +218,6 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
     kmax = torch.empty(B, (T + 255) // 256, dtype=torch.float32, device="cuda")
     idx = torch.empty(B, S, min(p["k_top"], T), dtype=torch.int32, device="cuda")
     part = torch.empty(B * S * 4 * (2048 + 1024), dtype=torch.int64, device="cuda")  # split top-k: lists, histograms
-    from kernelswift_amd import _lib
     lib = _lib.load()
     (qn, qs), (kn, ks_) = stats
     stream = torch.cuda.current_stream().cuda_stream
@@ -239,7 +261,10 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
         "roofline": {"bound": "mfma", "kernel": "indexer_scores_kernel (bounded)", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true>@cfg{cfg}")},
-        "topk_score_GBps": round(S * T * 4 / (topk_us * 1e-6) / 1e9, 1),
+        # the product's bounded top-k reads a score and a bound (8 B) per column; the plain one 4 B
+        "topk_bounded_GBps": round(S * T * 8 / (topkb_us * 1e-6) / 1e9, 1),
+        "topk_plain_GBps": round(S * T * 4 / (topk_us * 1e-6) / 1e9, 1),
+        "host_issue_us_per_call": host,
     }
     if do_cpu:
         from oracle import torch_ref
@@ -268,8 +293,15 @@ def run_sinkhorn(steps, warmup, do_cpu, cpu_budget):
     def k():
         _lib.check(lib.ks_sinkhorn(x.data_ptr(), out.data_ptr(), x.shape[0], 10, 1e-6, stream), "sinkhorn")
 
-    dev_med, dev_mean = _events_median(lambda: ops.sinkhorn(x, 10, 1e-6), steps, warmup)
-    wall_med, ms_step = _wall(lambda: ops.sinkhorn(x, 10, 1e-6), steps, warmup)
+    tops = _lib.torch_ops()
+
+    def step():  # the torch operator (TORCH_LIBRARY ks_mi355x), as a caller of the op sees it
+        return tops.sinkhorn(x, 10, 1e-6)
+
+    dev_med, dev_mean = _events_median(step, steps, warmup)
+    wall_med, ms_step = _wall(step, steps, warmup)
+    ct_med, _ = _events_median(lambda: ops.sinkhorn(x, 10, 1e-6), steps, warmup)
+    host = {"torch_op": round(_host_issue_us(step), 2), "ctypes": round(_host_issue_us(lambda: ops.sinkhorn(x, 10, 1e-6)), 2)}
     kus = _events_avg(k, steps, warmup)
     # the reference's other configured iteration count (hc_sinkhorn_iters = 20)
     kus20 = _events_avg(lambda: _lib.check(lib.ks_sinkhorn(x.data_ptr(), out.data_ptr(), x.shape[0], 20, 1e-6, stream),
@@ -291,7 +323,8 @@ def run_sinkhorn(steps, warmup, do_cpu, cpu_budget):
            "roofline": {"bound": "hbm", "kernel": "sinkhorn4x4_kernel", "achieved": round(achieved, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                         "traffic": _traffic("sinkhorn4x4_kernel@cfg1"), "cache": "warm (2 MiB fits in L2)"},
-           "size_sweep_matrices": sweep, "repeat20_kernel_us": round(kus20, 3)}
+           "size_sweep_matrices": sweep, "repeat20_kernel_us": round(kus20, 3),
+           "ctypes_us_per_call": round(ct_med, 3), "host_issue_us_per_call": host}
     if do_cpu:
         from oracle import torch_ref
         xc = x.cpu()
@@ -313,12 +346,18 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
     ws_n = ops.sparse_attn_workspace_size(B, M, H, Dqk, dv, K)
     ws = torch.empty(max(ws_n, 1), dtype=torch.uint8, device="cuda")
 
-    def step():
+    from kernelswift_amd import _lib
+    tops = _lib.torch_ops()
+
+    def step():  # the torch operator (TORCH_LIBRARY ks_mi355x), as a caller of the op sees it
+        return tops.sparse_attn(t["q"], t["kv"], t["sink"], t["idx"], p["scale"], dv)
+
+    def kernels():  # the kernels alone (preallocated workspace)
         return ops.sparse_attn(t["q"], t["kv"], t["sink"], t["idx"], p["scale"], dv=dv, workspace=ws)
 
     dev_med, dev_mean = _events_median(step, steps, warmup)
     wall_med, ms_step = _wall(step, steps, warmup)
-    op_us = _events_avg(step, steps, warmup)
+    op_us = _events_avg(kernels, steps, warmup)
     flops = 2.0 * B * M * H * K * (Dqk + dv)
     gathered = B * M * K * Dqk * 2
     achieved = flops / (op_us * 1e-6) / 1e12
@@ -354,6 +393,28 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
     return res
 
 
+def run_dropin(steps, warmup):
+    """ModelNew at the reference's own example shapes (baseline/*.py get_inputs), timed like the reference
+    harness (perf_counter + synchronize per call, median): context beside BASELINE.md's published numbers,
+    which were measured on other hardware."""
+    import torch
+    from kernelswift_amd.optimized import indexer as ix, sinkhorn as sk, sparse_attention as sa
+    out = {}
+    for name, mod in (("sinkhorn [1,1024,4,4]", sk),
+                      ("indexer B=8 S=2600 H=16 D=64 ratio=4 k=128", ix),
+                      ("sparse_attention B=8 M=2600 H=64 N=32 D=128 K=16", sa)):
+        torch.manual_seed(42)
+        m = mod.ModelNew(*mod.get_init_inputs()).cuda().eval()
+        torch.manual_seed(42)
+        inp = [v.cuda() if isinstance(v, torch.Tensor) else v for v in mod.get_inputs()]
+        with torch.no_grad():
+            wall, _ = _wall(lambda: m(*inp), steps, warmup)
+        out[name] = {"wall_us_per_call_sync": round(wall, 2)}
+        del m, inp
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -373,6 +434,11 @@ def main():
         elif c in (3, 5):
             per[c] = run_sparse(c, args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
         print(f"[bench] config {c}: {json.dumps(per[c])}", file=sys.stderr, flush=True)
+    dropin = None
+    if not args.no_dropin:
+        dropin = run_dropin(min(args.steps, 100), min(args.warmup, 20))
+        print(f"[bench] drop-in ModelNew at the reference example shapes: {json.dumps(dropin)}", file=sys.stderr,
+              flush=True)
     if args.calib_copy:
         from kernelswift_amd import ops
         src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda").fill_(1)
@@ -403,6 +469,7 @@ def main():
         "cpu_baseline": head.get("cpu_baseline"),
         "wall_us_per_call_sync": head["wall_us_per_call_sync"],
         "per_config": {str(k): v for k, v in per.items()},
+        "dropin_example_shapes": dropin,
         "device": torch.cuda.get_device_name(0),
         "gpu_clocks": _gpu_clocks(),
         "host": {"cpu_model": _cpu_model(), "threads": _cpu_threads()},

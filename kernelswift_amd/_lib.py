@@ -11,6 +11,7 @@ import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libkswift_amd.so")
+TORCH_LIB_PATH = os.path.join(HERE, "libkswift_torch.so")
 
 _c_i64 = ctypes.c_int64
 _c_i32 = ctypes.c_int32
@@ -82,6 +83,25 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+_torch_ops = None
+
+
+def torch_ops():
+    """torch.ops.ks_mi355x, the TORCH_LIBRARY registration of libkswift_torch.so (loaded on first use).
+    Raises KsError when the library has not been built (there is no fallback)."""
+    global _torch_ops
+    if _torch_ops is not None:
+        return _torch_ops
+    with _lock:
+        if _torch_ops is None:
+            import torch
+            if not os.path.exists(TORCH_LIB_PATH):
+                raise KsError(f"{TORCH_LIB_PATH} is missing: build it with `python -m kernelswift_amd.build`")
+            torch.ops.load_library(TORCH_LIB_PATH)
+            _torch_ops = torch.ops.ks_mi355x
+    return _torch_ops
 
 
 def check(rc: int, what: str) -> None:

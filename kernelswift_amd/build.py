@@ -1,9 +1,11 @@
-"""Build libkswift_amd.so (gfx950 HIP kernels + the C ABI of include/kswift.h).
+"""Build libkswift_amd.so (gfx950 HIP kernels + the C ABI of include/kswift.h) and
+libkswift_torch.so (the TORCH_LIBRARY(ks_mi355x, ...) operator registration over that C ABI).
 
     python -m kernelswift_amd.build [-v]
 
 Each csrc/*.hip is compiled to an object with hipcc for gfx950, then linked into
-one shared library next to this file.  Flags:
+one shared library next to this file; csrc/torch_ops.cpp (host code only) is compiled
+against the installed PyTorch-ROCm headers and linked to it.  Flags:
   -ffp-contract=off      no implicit FMA contraction: every fused multiply-add in
                          the kernels is an explicit __builtin_fmaf, so the bit-exact
                          indexer contract cannot be broken by the compiler;
@@ -20,6 +22,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libkswift_amd.so")
+TORCH_LIB = os.path.join(HERE, "libkswift_torch.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -46,6 +49,27 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
+def build_torch_ops(verbose: bool = False) -> str:
+    """The torch operator library: host C++ over the C ABI, so g++ suffices (no device code)."""
+    import torch
+    from torch.utils import cpp_extension
+    tlib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-Wno-deprecated-declarations"]
+    cmd += [f"-I{p}" for p in cpp_extension.include_paths()] + ["-I/opt/rocm/include"]
+    cmd += [os.path.join(CSRC, "torch_ops.cpp"), f"-L{tlib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+            "-ltorch_hip", f"-L{HERE}", "-lkswift_amd", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}",
+            "-o", TORCH_LIB + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("g++ failed for torch_ops.cpp:\n" + r.stderr[-4000:])
+    os.replace(TORCH_LIB + ".tmp", TORCH_LIB)
+    return TORCH_LIB
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ_DIR, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -57,6 +81,7 @@ def build(verbose: bool = False) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    build_torch_ops(verbose)
     return LIB
 
 

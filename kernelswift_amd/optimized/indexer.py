@@ -5,7 +5,8 @@ freqs_cis) of the reference indexer (baseline/indexer.py:132-206; optimized/inde
 168-224), so a state dict of the baseline Model loads as is.  The two projections stay torch GEMMs, as in
 the reference; RoPE of q (last rope_head_dim dims), the exact score contraction with the ReLU * weight head
 reduction and the causal mask, and the exact sorted top-k with the -1 / +offset post-processing run as one
-call of the fused gfx950 operator (ks_indexer), without a transposed or padded copy of the cache.
+call of the fused gfx950 operator torch.ops.ks_mi355x.indexer (ks_indexer), without a transposed or padded copy
+of the cache.
 
 Semantics kept from the baseline: weights = weights_proj(x) * (head_dim^-0.5 * n_heads^-0.5) in bf16;
 keys are kv_cache[:B, :(start_pos + S) // ratio] (not rotated); the causal mask and the -1 post-processing
@@ -21,11 +22,12 @@ import torch.nn as nn
 
 
 def _ops():
+    """torch.ops.ks_mi355x (libkswift_torch.so), loaded on first use like the reference wrappers' extension."""
     root = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if root not in sys.path:
         sys.path.insert(0, root)
-    from kernelswift_amd import ops
-    return ops
+    from kernelswift_amd import _lib
+    return _lib.torch_ops()
 
 
 @dataclass
@@ -58,7 +60,6 @@ class ModelNew(nn.Module):
         self.compress_ratio = compress_ratio
         self.register_buffer("kv_cache", kv_cache)
         self.register_buffer("freqs_cis", freqs_cis)
-        self._ws = None
 
     def _freqs(self) -> torch.Tensor:
         """(cos, sin) float32 [rows, rope_head_dim/2, 2] from the complex table (or its real view)."""
@@ -78,13 +79,8 @@ class ModelNew(nn.Module):
             return torch.empty((bsz, seqlen, 0), dtype=torch.int64, device=x.device)
         q = self.wq_b(qr).unflatten(-1, (self.n_local_heads, self.head_dim)).contiguous()
         weights = (self.weights_proj(x) * (self.softmax_scale * self.n_heads ** -0.5)).contiguous()
-        need = ops.indexer_workspace_size(bsz, seqlen, self.n_heads, self.head_dim, T)
-        if self._ws is None or self._ws.numel() < need or self._ws.device != x.device:
-            self._ws = torch.empty(need, dtype=torch.uint8, device=x.device)
-        return ops.indexer(q, self.kv_cache[:bsz], weights, self._freqs(), k_top, start_pos == 0, start_pos,
-                           ratio, offset, rope_start=self.head_dim - self.rope_head_dim,
-                           rope_dim=self.rope_head_dim, rope_k=False, out_dtype=torch.int64,
-                           workspace=self._ws, T=T)
+        return ops.indexer(q, self.kv_cache[:bsz], weights, self._freqs(), k_top, start_pos == 0, start_pos, ratio,
+                           offset, self.head_dim - self.rope_head_dim, self.rope_head_dim, False, True, T)
 
 
 def _example_args() -> ModelArgs:

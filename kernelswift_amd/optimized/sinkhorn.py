@@ -1,7 +1,8 @@
 """Sinkhorn drop-in: ModelNew(repeat=10, eps=1e-6).forward(x).
 
 Signature of optimized/sinkhorn_project/sinkhorn.py:35-52 over baseline/sinkhorn.py:5-19; the whole
-normalisation (softmax + eps, then `repeat` row/column passes) is one gfx950 kernel (ks_sinkhorn).
+normalisation (softmax + eps, then `repeat` row/column passes) is one gfx950 kernel behind the torch operator
+torch.ops.ks_mi355x.sinkhorn (ks_sinkhorn).
 x: float32 [..., 4, 4] on the GPU; returns a new float32 tensor of the same shape.
 """
 import os
@@ -12,11 +13,12 @@ import torch.nn as nn
 
 
 def _ops():
+    """torch.ops.ks_mi355x (libkswift_torch.so), loaded on first use like the reference wrappers' extension."""
     root = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if root not in sys.path:
         sys.path.insert(0, root)
-    from kernelswift_amd import ops
-    return ops
+    from kernelswift_amd import _lib
+    return _lib.torch_ops()
 
 
 class ModelNew(nn.Module):

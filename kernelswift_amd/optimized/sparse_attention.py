@@ -2,8 +2,10 @@
 
 Signature and parameters of optimized/sparse_attention/sparse_attention.py:31-44 over
 baseline/sparse_attention.py:45-65 (attn_sink parameter, softmax_scale = head_dim ** -0.5).  Gather, QK,
-sink softmax and PV run in the gfx950 kernel behind ks_sparse_attn.
-q: bf16 [B, M, H, D]; kv: bf16 [B, N, D]; topk_idxs: int32 (or int64, converted) [B, M, K], -1 = invalid.
+sink softmax and PV run in the gfx950 kernels behind torch.ops.ks_mi355x.sparse_attn (ks_sparse_attn).
+q: bf16 [B, M, H, D]; kv: bf16 [B, N, D]; topk_idxs: int32 (or int64) [B, M, K], -1 = invalid.  Indices
+outside [0, N) are invalid (masked, as the kernel treats them); int64 values are mapped to -1 before they
+are narrowed to int32, so no out-of-range value can wrap onto a valid row.
 """
 import os
 import sys
@@ -13,11 +15,12 @@ import torch.nn as nn
 
 
 def _ops():
+    """torch.ops.ks_mi355x (libkswift_torch.so), loaded on first use like the reference wrappers' extension."""
     root = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     if root not in sys.path:
         sys.path.insert(0, root)
-    from kernelswift_amd import ops
-    return ops
+    from kernelswift_amd import _lib
+    return _lib.torch_ops()
 
 
 class ModelNew(nn.Module):
@@ -29,7 +32,9 @@ class ModelNew(nn.Module):
         self.attn_sink = nn.Parameter(torch.zeros(n_heads, dtype=torch.float32))
 
     def forward(self, q: torch.Tensor, kv: torch.Tensor, topk_idxs: torch.Tensor) -> torch.Tensor:
-        idx = topk_idxs if topk_idxs.dtype == torch.int32 else topk_idxs.to(torch.int32)
+        idx = topk_idxs
+        if idx.dtype != torch.int32:
+            idx = torch.where((idx < 0) | (idx >= kv.shape[1]), -1, idx).to(torch.int32)
         sink = self.attn_sink.detach()
         if sink.dtype != torch.float32:
             sink = sink.float()

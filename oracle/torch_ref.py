@@ -89,7 +89,7 @@ def sparse_attn(q: torch.Tensor, kv: torch.Tensor, sink: torch.Tensor, idx: torc
     K = idx.shape[-1]
     ok = idx >= 0
     safe = idx.clamp_min(0).long()
-    bi = torch.arange(B)[:, None, None].expand(B, M, K)
+    bi = torch.arange(B, device=idx.device)[:, None, None].expand(B, M, K)
     g = kv[bi, safe].masked_fill(~ok.unsqueeze(-1), 0.0)
     s = torch.einsum("bmhd,bmtd->bmht", q.float(), g.float()) * scale
     s = s.masked_fill(~ok.unsqueeze(2), float("-inf"))

@@ -103,9 +103,13 @@ int ks_rope_inplace(uint16_t *x, const float *freqs, int64_t B, int64_t S,
  * error and prove the exact recomputation of near-tie dots exact).
  * scores: f32 [B, S, T].  D must be 64 or 128 (the head dims the kernel is
  * built for); H in {16, 32, 64}; T >= 1.
- * Exactness holds for rows whose nonzero magnitudes span less than ~2^40 each
- * (span_q + span_k <= 84, see ks_indexer_row_stats); beyond that a near-tie dot
- * keeps its MFMA rounding.
+ * Exact for all finite inputs: the MFMA sum is trusted only when an interval of
+ * half-width 13 * 2^-23 * (||q|| + 2^-122)(||k|| + 2^-122) + 2^-144 around it
+ * rounds to one bf16 value (a bound derived from the instruction's accumulation);
+ * other dots are recomputed exactly (double precision, or an integer accumulator
+ * for rows of any dynamic range), and rows whose norm product reaches 2^126 are
+ * recomputed in full.  Scores must not come out NaN (an infinite dot times a zero
+ * weight, or opposite infinities); NaN and infinite inputs are outside the contract.
  * ---------------------------------------------------------------------- */
 int ks_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w,
                       int32_t w_bf16, const float *q_norm, const int32_t *q_span,

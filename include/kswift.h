@@ -207,6 +207,28 @@ int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float *sink,
                    void *stream);
 
 /* ------------------------------------------------------------------------
+ * ks_sparse_attn without a workspace: allocates nothing.
+ *
+ * No counterpart in the reference (whose torch op allocates its tiling tensors,
+ * optimized/sparse_attention/op_extension/sparse_attn_torch.cpp:80-94).  For callers
+ * that cannot allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  Same arguments and results as
+ * ks_sparse_attn, minus the workspace: the split partials live in a static device
+ * array of ks_sparse_attn_noalloc_max_scratch() bytes (64 MiB) that each GPU holds
+ * for the life of the process; its address on the stream's device is resolved on
+ * that device's first call.  Shapes whose ks_sparse_attn_workspace_size exceeds the
+ * maximum return KS_ERR_INVALID without launching.  Calls that overlap on one GPU
+ * (two streams, two threads) share the array and race: serialise them.  The array
+ * keeps the last call's contents; no call relies on them (every partial is written
+ * before it is read within the call).
+ * ---------------------------------------------------------------------- */
+size_t ks_sparse_attn_noalloc_max_scratch(void);
+int ks_sparse_attn_noalloc(const uint16_t *q, const uint16_t *kv, const float *sink,
+                           const int32_t *idx, uint16_t *out, int64_t B, int64_t M,
+                           int64_t H, int64_t Dqk, int64_t Dv, int64_t N, int64_t K,
+                           float scale, void *stream);
+
+/* ------------------------------------------------------------------------
  * Calibration helper (not an operator): copies n_bytes (multiple of 16) from
  * src to dst with one streaming kernel.  Used to scale rocprofv3 FETCH_SIZE /
  * WRITE_SIZE counters against a kernel of known traffic.

@@ -26,6 +26,9 @@
 // wave, one wave per SIMD, O accumulated in AGPRs.
 #include "common.h"
 
+#include <array>
+#include <mutex>
+
 namespace ks {
 namespace {
 
@@ -1044,4 +1047,65 @@ extern "C" int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float
   if (d128) return ks::launch_sa<128, 128>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
   if (ks::use_mla(Dqk, Dv, H, K)) return ks::launch_mla(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
   return ks::launch_sa<576, 512>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
+}
+
+// ---------------------------------------------------------------- the entry point that allocates nothing
+// Split partials of ks_sparse_attn_noalloc live in this file-scope device array instead of a caller
+// workspace.  Each GPU the library runs on holds its own copy (the code object's data on that device) for
+// the life of the process; host code never names the array in a launch or a copy (its name is a host-side
+// stand-in), only the device address hipGetSymbolAddress returns for the stream's device, resolved once per
+// device.  Every partial range is written by the attention kernels before the combine kernel reads it in
+// the same call, so nothing needs clearing; calls that overlap on one GPU share the array and race.
+namespace ks {
+constexpr size_t kSaScratchBytes = size_t(64) << 20;
+}
+static __device__ __align__(256) unsigned char scratch[ks::kSaScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::array<void *, kMaxDevices> g_scratch_ptr{};
+
+// The scratch address on the device of `st` (the current device for the null stream).
+int scratch_for_stream(hipStream_t st, void **ptr) {
+  int cur = 0;
+  KS_CHECK_HIP(hipGetDevice(&cur));
+  int dev = cur;
+  if (st != nullptr) {
+    hipDevice_t d = 0;
+    KS_CHECK_HIP(hipStreamGetDevice(st, &d));
+    dev = static_cast<int>(d);
+  }
+  KS_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "ks_sparse_attn_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur) KS_CHECK_HIP(hipSetDevice(dev));
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    KS_CHECK_HIP(e);
+    KS_CHECK_ARG(p != nullptr, "ks_sparse_attn_noalloc: no scratch address on device %d", dev);
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return KS_OK;
+}
+}  // namespace
+
+extern "C" size_t ks_sparse_attn_noalloc_max_scratch(void) { return ks::kSaScratchBytes; }
+
+extern "C" int ks_sparse_attn_noalloc(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx,
+                                      uint16_t *out, int64_t B, int64_t M, int64_t H, int64_t Dqk, int64_t Dv,
+                                      int64_t N, int64_t K, float scale, void *stream) {
+  ks::last_error().clear();
+  const size_t need = ks_sparse_attn_workspace_size(B, M, H, Dqk, Dv, K);
+  KS_CHECK_ARG(need <= ks::kSaScratchBytes,
+               "ks_sparse_attn_noalloc: this shape needs %zu bytes of split scratch, the maximum is %zu bytes "
+               "(call ks_sparse_attn with a workspace instead)", need, ks::kSaScratchBytes);
+  void *ws = nullptr;
+  if (need > 0 && B * M > 0) {
+    const int rc = scratch_for_stream(static_cast<hipStream_t>(stream), &ws);
+    if (rc != KS_OK) return rc;
+  }
+  return ks_sparse_attn(q, kv, sink, idx, out, B, M, H, Dqk, Dv, N, K, scale, ws, need, stream);
 }

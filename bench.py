@@ -41,7 +41,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--configs", type=str, default="2,1,3,4,5")
+    p.add_argument("--configs", type=str, default="2,1,3,4,5,mhc")
     p.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     p.add_argument("--no-dropin", action="store_true", help="skip the ModelNew rows at the reference example shapes")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget per CPU baseline sample")
@@ -393,6 +393,48 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
     return res
 
 
+def run_mhc(steps, warmup, do_cpu, cpu_budget, N=4096, C=4096, iters=20):
+    """mHC residual connection at hc_mult = 4, hc_sinkhorn_iters = 20 (baseline/indexer.py:48-50) over N tokens of
+    dim C: the residual update with the Sinkhorn fused in (ks_mhc_post) and the layer-input mix (ks_mhc_pre);
+    HBM-bound streams, judged on GB/s of their algorithmic bytes."""
+    import torch
+    from kernelswift_amd import ops
+    g = torch.Generator(device="cuda").manual_seed(42)
+    x = torch.randn(N, 4, C, generator=g, device="cuda").bfloat16()
+    f = torch.randn(N, C, generator=g, device="cuda").bfloat16()
+    res = torch.randn(N, 4, 4, generator=g, device="cuda")
+    post = torch.randn(N, 4, generator=g, device="cuda")
+    pre = torch.randn(N, 4, generator=g, device="cuda")
+    out = torch.empty_like(x)
+    post_us = _events_avg(lambda: ops.mhc_post(x, f, res, post, iters, 1e-6, out=out), steps, warmup)
+    wall_med, ms_step = _wall(lambda: ops.mhc_post(x, f, res, post, iters, 1e-6, out=out), steps, warmup)
+    pre_us = _events_avg(lambda: ops.mhc_pre(x, pre), steps, warmup)
+    post_bytes = N * (4 * C * 2 * 2 + C * 2 + 16 * 4 + 4 * 4)  # x read, out written, f read, logits
+    pre_bytes = N * (4 * C * 2 + C * 2 + 4 * 4)
+    gbs = post_bytes / (post_us * 1e-6) / 1e9
+    res_d = {"us_per_call": round(post_us, 3), "wall_us_per_call_sync": round(wall_med, 3), "ms_per_step": ms_step,
+             "workload": f"N={N} tokens, C={C}, hc_mult=4, sinkhorn_iters={iters}",
+             "kernels_us": {"mhc_post_kernel (Sinkhorn fused)": round(post_us, 3), "mhc_pre_kernel": round(pre_us, 3)},
+             "roofline": {"bound": "hbm", "kernel": "mhc_post_kernel", "achieved": round(gbs, 1),
+                          "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                          "bytes_per_launch": post_bytes},
+             "pre_GBps": round(pre_bytes / (pre_us * 1e-6) / 1e9, 1)}
+    if do_cpu:
+        from oracle import torch_ref
+        torch.set_num_threads(_cpu_threads())
+        nb = 256  # bounded sample of tokens; time scaled to N
+        xc, fc, rc, pc = x[:nb].cpu().float(), f[:nb].cpu().float(), res[:nb].cpu(), post[:nb].cpu()
+
+        def cpu_post():
+            S = torch_ref.sinkhorn(rc, iters, 1e-6)
+            return (torch.einsum("nij,njc->nic", S, xc) + 2 * torch.sigmoid(pc)[:, :, None] * fc[:, None, :]).bfloat16()
+
+        ms, reps = _cpu_time(cpu_post, cpu_budget)
+        res_d["cpu_baseline"] = {"value": round(ms * (N / nb) * 1e3, 1), "unit": "us/call", "cores": torch.get_num_threads(),
+                                 "kind": "port", "sample": f"{nb} of {N} tokens (scaled x{N // nb}), median of {reps}"}
+    return res_d
+
+
 def run_dropin(steps, warmup):
     """ModelNew at the reference's own example shapes (baseline/*.py get_inputs), timed like the reference
     harness (perf_counter + synchronize per call, median): context beside BASELINE.md's published numbers,
@@ -424,7 +466,7 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.set_device(0)
-    cfgs = [int(c) for c in args.configs.split(",") if c]
+    cfgs = [c if c == "mhc" else int(c) for c in args.configs.split(",") if c]
     per = {}
     for c in cfgs:
         if c in (2, 4):
@@ -433,6 +475,8 @@ def main():
             per[c] = run_sinkhorn(args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
         elif c in (3, 5):
             per[c] = run_sparse(c, args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
+        elif c == "mhc":
+            per[c] = run_mhc(args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
         print(f"[bench] config {c}: {json.dumps(per[c])}", file=sys.stderr, flush=True)
     dropin = None
     if not args.no_dropin:

@@ -207,6 +207,30 @@ int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float *sink,
                    void *stream);
 
 /* ------------------------------------------------------------------------
+ * mHC residual hyper-connections (hc_mult = 4 streams) with the Sinkhorn
+ * projection fused into the mixing that consumes it.
+ *
+ * No kernel counterpart in the reference: it configures hc_mult = 4,
+ * hc_sinkhorn_iters = 20 and hc_eps (baseline/indexer.py:48-50) and ships the
+ * 4x4 Sinkhorn as an operator of its own (baseline/sinkhorn.py, mhc = 4 there;
+ * ks_sinkhorn above).  Per token t, with residual streams x[t] (4 rows of C):
+ *   ks_mhc_pre:  h[t]    = sum_j sigmoid(pre_logits[t][j]) x[t][j]
+ *   ks_mhc_post: out[t][i] = sum_j S(res_logits[t])[i][j] x[t][j]
+ *                           + 2 sigmoid(post_logits[t][i]) f[t]
+ * where S is the Sinkhorn of ks_sinkhorn (repeat = sinkhorn_iters, eps) of the
+ * token's 4x4 logits, computed inside the kernel (the matrices never reach
+ * memory).  x: bf16 [N, 4, C], C a multiple of 8; f, h: bf16 [N, C];
+ * pre_logits, post_logits: f32 [N, 4]; res_logits: f32 [N, 4, 4];
+ * out: bf16 [N, 4, C], may alias x.  fp32 arithmetic, RNE to bf16; every
+ * buffer 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+int ks_mhc_pre(const uint16_t *x, const float *pre_logits, uint16_t *h, int64_t N,
+               int64_t C, void *stream);
+int ks_mhc_post(const uint16_t *x, const uint16_t *f, const float *res_logits,
+                const float *post_logits, uint16_t *out, int64_t N, int64_t C,
+                int32_t sinkhorn_iters, float eps, void *stream);
+
+/* ------------------------------------------------------------------------
  * ks_sparse_attn without a workspace: allocates nothing.
  *
  * No counterpart in the reference (whose torch op allocates its tiling tensors,

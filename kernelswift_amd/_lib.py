@@ -38,6 +38,8 @@ SIGNATURES = {
     "ks_sparse_attn_workspace_size": (_c_sz, [_c_i64] * 6),
     "ks_sparse_attn": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                       _c_i64, _c_f, _c_p, _c_sz, _c_p]),
+    "ks_mhc_pre": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p]),
+    "ks_mhc_post": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_f, _c_p]),
     "ks_sparse_attn_noalloc_max_scratch": (_c_sz, []),
     "ks_sparse_attn_noalloc": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                               _c_i64, _c_i64, _c_f, _c_p]),

@@ -16,42 +16,10 @@
 // true division after 20 normalisations (the reference needed a Newton step for its 10-bit reciprocal,
 // optimized/sinkhorn_project/design.md:51-52).
 #include "common.h"
+#include "sinkhorn_quad.h"
 
 namespace ks {
 namespace {
-
-// quad_perm encodings for DPP: [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E.
-template <int CTRL>
-__device__ __forceinline__ float dpp_quad(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over the 4 lanes of a quad; every lane receives the same value ((r0 + r1) + (r2 + r3)).
-__device__ __forceinline__ float quad_sum(float v) {
-  float a = v + dpp_quad<0xB1>(v);
-  return a + dpp_quad<0x4E>(a);
-}
-
-__device__ __forceinline__ float rcp(float v) { return __builtin_amdgcn_rcpf(v); }
-
-__device__ __forceinline__ void col_norm(float4 &v, float eps) {
-  const float r0 = rcp(quad_sum(v.x) + eps);
-  const float r1 = rcp(quad_sum(v.y) + eps);
-  const float r2 = rcp(quad_sum(v.z) + eps);
-  const float r3 = rcp(quad_sum(v.w) + eps);
-  v.x *= r0;
-  v.y *= r1;
-  v.z *= r2;
-  v.w *= r3;
-}
-
-__device__ __forceinline__ void row_norm(float4 &v, float eps) {
-  const float r = rcp(((v.x + v.y) + (v.z + v.w)) + eps);
-  v.x *= r;
-  v.y *= r;
-  v.z *= r;
-  v.w *= r;
-}
 
 __global__ __launch_bounds__(256) void sinkhorn4x4_kernel(const float4 *__restrict__ x, float4 *__restrict__ out,
                                                          int64_t n_rows, int repeat, float eps) {
@@ -61,19 +29,7 @@ __global__ __launch_bounds__(256) void sinkhorn4x4_kernel(const float4 *__restri
   const bool live = g < n_rows;
   float4 v = live ? x[g] : make_float4(0.f, 0.f, 0.f, 0.f);
 
-  // softmax over the row, then + eps (baseline/sinkhorn.py:14; no eps inside the softmax)
-  const float m = fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w));
-  const float e0 = expf(v.x - m), e1 = expf(v.y - m), e2 = expf(v.z - m), e3 = expf(v.w - m);
-  const float s = (e0 + e1) + (e2 + e3);
-  v.x = e0 / s + eps;
-  v.y = e1 / s + eps;
-  v.z = e2 / s + eps;
-  v.w = e3 / s + eps;
-  col_norm(v, eps);  // :15
-  for (int it = 1; it < repeat; ++it) {  // :16-18
-    row_norm(v, eps);
-    col_norm(v, eps);
-  }
+  v = sinkhorn_quad_row(v, repeat, eps);
   if (live) out[g] = v;
 }
 

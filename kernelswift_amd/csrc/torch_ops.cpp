@@ -179,6 +179,50 @@ at::Tensor sparse_attn(const at::Tensor& q, const at::Tensor& kv, const at::Tens
   return out;
 }
 
+// ---------------------------------------------------------------- mHC hyper-connections
+void check_streams(const at::Tensor& x) {
+  check_gpu(x, "x");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16");
+  TORCH_CHECK(x.dim() == 3 && x.size(1) == 4 && x.size(2) % 8 == 0, "x must be [N, 4, C] with C a multiple of 8");
+}
+
+at::Tensor mhc_pre(const at::Tensor& x, const at::Tensor& pre_logits) {
+  check_streams(x);
+  check_gpu(pre_logits, "pre_logits");
+  TORCH_CHECK(pre_logits.scalar_type() == at::kFloat && pre_logits.dim() == 2 && pre_logits.size(0) == x.size(0) &&
+                  pre_logits.size(1) == 4,
+              "pre_logits must be float32 [N, 4]");
+  at::Tensor h = at::empty({x.size(0), x.size(2)}, x.options());
+  check_rc(ks_mhc_pre(reinterpret_cast<const uint16_t*>(x.data_ptr()), pre_logits.data_ptr<float>(),
+                      reinterpret_cast<uint16_t*>(h.data_ptr()), x.size(0), x.size(2), current_stream(x)),
+           "ks_mi355x::mhc_pre");
+  return h;
+}
+
+at::Tensor mhc_post(const at::Tensor& x, const at::Tensor& f, const at::Tensor& res_logits,
+                    const at::Tensor& post_logits, int64_t sinkhorn_iters, double eps) {
+  check_streams(x);
+  check_gpu(f, "f");
+  check_gpu(res_logits, "res_logits");
+  check_gpu(post_logits, "post_logits");
+  const int64_t N = x.size(0), C = x.size(2);
+  TORCH_CHECK(f.scalar_type() == at::kBFloat16 && f.dim() == 2 && f.size(0) == N && f.size(1) == C,
+              "f must be bfloat16 [N, C]");
+  TORCH_CHECK(res_logits.scalar_type() == at::kFloat && res_logits.dim() == 3 && res_logits.size(0) == N &&
+                  res_logits.size(1) == 4 && res_logits.size(2) == 4,
+              "res_logits must be float32 [N, 4, 4]");
+  TORCH_CHECK(post_logits.scalar_type() == at::kFloat && post_logits.dim() == 2 && post_logits.size(0) == N &&
+                  post_logits.size(1) == 4,
+              "post_logits must be float32 [N, 4]");
+  at::Tensor out = at::empty_like(x);
+  check_rc(ks_mhc_post(reinterpret_cast<const uint16_t*>(x.data_ptr()), reinterpret_cast<const uint16_t*>(f.data_ptr()),
+                       res_logits.data_ptr<float>(), post_logits.data_ptr<float>(),
+                       reinterpret_cast<uint16_t*>(out.data_ptr()), N, C, static_cast<int32_t>(sinkhorn_iters),
+                       static_cast<float>(eps), current_stream(x)),
+           "ks_mi355x::mhc_post");
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(ks_mi355x, m) {
@@ -193,6 +237,9 @@ TORCH_LIBRARY(ks_mi355x, m) {
         "int? T=None) -> Tensor");
   m.def("sparse_attn(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, float softmax_scale, "
         "int? dv=None) -> Tensor");
+  m.def("mhc_pre(Tensor x, Tensor pre_logits) -> Tensor");
+  m.def("mhc_post(Tensor x, Tensor f, Tensor res_logits, Tensor post_logits, int sinkhorn_iters=20, "
+        "float eps=1e-06) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(ks_mi355x, CUDA, m) {
@@ -202,4 +249,6 @@ TORCH_LIBRARY_IMPL(ks_mi355x, CUDA, m) {
   m.impl("indexer_topk", &indexer_topk);
   m.impl("indexer", &indexer);
   m.impl("sparse_attn", &sparse_attn);
+  m.impl("mhc_pre", &mhc_pre);
+  m.impl("mhc_post", &mhc_post);
 }

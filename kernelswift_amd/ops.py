@@ -19,7 +19,7 @@ from . import _lib
 
 __all__ = [
     "sinkhorn", "rope_inplace", "indexer_row_stats", "indexer_scores", "topk_mask", "indexer",
-    "indexer_workspace_size", "sparse_attn", "sparse_attn_workspace_size", "copy_bytes",
+    "indexer_workspace_size", "sparse_attn", "sparse_attn_workspace_size", "mhc_pre", "mhc_post", "copy_bytes",
 ]
 
 
@@ -231,6 +231,45 @@ def sparse_attn(q: torch.Tensor, kv: torch.Tensor, attn_sink: torch.Tensor, topk
     _lib.check(_lib.load().ks_sparse_attn(_p(q), _p(kv), _p(attn_sink), _p(topk_idxs), _p(out), B, M, H, D, dv, N, K,
                                           float(softmax_scale), _p(workspace) if need else None, wsz, _stream(q)),
                "sparse_attn")
+    return out
+
+
+# ---------------------------------------------------------------- mHC hyper-connections
+def _mhc_streams(x: torch.Tensor) -> None:
+    _check(x.dtype == torch.bfloat16, "x must be bfloat16")
+    _on_gpu(x)
+    _check(x.dim() == 3 and x.shape[1] == 4 and x.shape[2] % 8 == 0, "x must be [N, 4, C] with C a multiple of 8")
+
+
+def mhc_pre(x: torch.Tensor, pre_logits: torch.Tensor) -> torch.Tensor:
+    """Layer input of an mHC block: h[t] = sum_j sigmoid(pre_logits[t, j]) x[t, j] (bf16 [N, C])."""
+    _mhc_streams(x)
+    _check(pre_logits.dtype == torch.float32 and tuple(pre_logits.shape) == (x.shape[0], 4),
+           "pre_logits must be float32 [N, 4]")
+    _on_gpu(pre_logits)
+    N, _, C = x.shape
+    h = torch.empty((N, C), dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.load().ks_mhc_pre(_p(x), _p(pre_logits), _p(h), N, C, _stream(x)), "mhc_pre")
+    return h
+
+
+def mhc_post(x: torch.Tensor, f: torch.Tensor, res_logits: torch.Tensor, post_logits: torch.Tensor,
+             sinkhorn_iters: int = 20, eps: float = 1e-6, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Residual update of an mHC block with the Sinkhorn fused in: out[t, i] = sum_j S(res_logits[t])[i, j] x[t, j]
+    + 2 sigmoid(post_logits[t, i]) f[t], S = the Sinkhorn of sinkhorn() (repeat = sinkhorn_iters).  out may be x."""
+    _mhc_streams(x)
+    N, _, C = x.shape
+    _check(f.dtype == torch.bfloat16 and tuple(f.shape) == (N, C), "f must be bfloat16 [N, C]")
+    _check(res_logits.dtype == torch.float32 and tuple(res_logits.shape) == (N, 4, 4),
+           "res_logits must be float32 [N, 4, 4]")
+    _check(post_logits.dtype == torch.float32 and tuple(post_logits.shape) == (N, 4),
+           "post_logits must be float32 [N, 4]")
+    _on_gpu(f, res_logits, post_logits)
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out.dtype == torch.bfloat16 and out.shape == x.shape and out.is_contiguous(), "out must match x")
+    _lib.check(_lib.load().ks_mhc_post(_p(x), _p(f), _p(res_logits), _p(post_logits), _p(out), N, C,
+                                       int(sinkhorn_iters), float(eps), _stream(x)), "mhc_post")
     return out
 
 

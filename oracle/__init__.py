@@ -254,3 +254,28 @@ def sparse_attn(q: np.ndarray, kv: np.ndarray, sink: np.ndarray, idx: np.ndarray
         p = e / den
         out[b] = np.einsum("mht,mtd->mhd", p, g[..., :dv])      # (:39-41)
     return out
+
+
+# ---------------------------------------------------------------- mHC hyper-connections
+def _sigmoid(z: np.ndarray) -> np.ndarray:
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def mhc_pre(x: np.ndarray, pre_logits: np.ndarray) -> np.ndarray:
+    """Layer input of an mHC block (hc_mult = 4; baseline/indexer.py:48-50 configures the connections):
+    h[t] = sum_j sigmoid(pre_logits[t, j]) x[t, j].  x: bf16 bits [N, 4, C]; returns float64 [N, C]."""
+    xf = bf16_to_f32(x).astype(np.float64)
+    g = _sigmoid(np.asarray(pre_logits, np.float64))
+    return np.einsum("nj,njc->nc", g, xf)
+
+
+def mhc_post(x: np.ndarray, f: np.ndarray, res_logits: np.ndarray, post_logits: np.ndarray,
+             sinkhorn_iters: int = 20, eps: float = 1e-6) -> np.ndarray:
+    """Residual update of an mHC block: out[t, i] = sum_j S[t, i, j] x[t, j] + 2 sigmoid(post_logits[t, i]) f[t],
+    S = sinkhorn(res_logits, repeat=sinkhorn_iters, eps) (baseline/sinkhorn.py:13-19, in fp64 above).
+    x: bf16 bits [N, 4, C]; f: bf16 bits [N, C]; returns float64 [N, 4, C]."""
+    xf = bf16_to_f32(x).astype(np.float64)
+    ff = bf16_to_f32(f).astype(np.float64)
+    S = sinkhorn(np.asarray(res_logits, np.float32), sinkhorn_iters, eps).astype(np.float64)
+    p = 2.0 * _sigmoid(np.asarray(post_logits, np.float64))
+    return np.einsum("nij,njc->nic", S, xf) + p[:, :, None] * ff[:, None, :]

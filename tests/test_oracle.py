@@ -387,3 +387,30 @@ def test_freqs_table_against_the_mathematics():
     bad = np.stack([np.cos(p * 10000.0 ** (-1.0 * j / d)), np.sin(p * 10000.0 ** (-1.0 * j / d))], -1)
     assert np.max(np.abs(bad - tab)) > 0.1
     assert np.max(np.abs(tab[..., ::-1] - tab)) > 0.1
+
+
+# ------------------------------------------------------------------ mHC hyper-connections
+def test_mhc_oracle_closed_forms():
+    rng = np.random.default_rng(5)
+    N, C = 6, 16
+    x = oracle.f32_to_bf16(rng.standard_normal((N, 4, C)).astype(np.float32))
+    f = oracle.f32_to_bf16(rng.standard_normal((N, C)).astype(np.float32))
+    xf = oracle.bf16_to_f32(x).astype(np.float64)
+    ff = oracle.bf16_to_f32(f).astype(np.float64)
+    # constant residual logits: the doubly stochastic matrix is 1/4 everywhere (up to eps) -> stream mean
+    out = oracle.mhc_post(x, f, np.zeros((N, 4, 4), np.float32), np.zeros((N, 4), np.float32), 20, 1e-6)
+    np.testing.assert_allclose(out, np.broadcast_to(xf.mean(1, keepdims=True) + ff[:, None, :], out.shape),
+                               rtol=1e-5, atol=1e-5)
+    # zero pre logits: sigmoid 1/2 on every stream
+    np.testing.assert_allclose(oracle.mhc_pre(x, np.zeros((N, 4), np.float32)), 0.5 * xf.sum(1), rtol=1e-12)
+    # very negative post logits switch the layer output off; a permutation of the residual logits' rows
+    # permutes the output streams (the Sinkhorn is equivariant)
+    res = rng.standard_normal((N, 4, 4)).astype(np.float32)
+    off = np.full((N, 4), -200.0, np.float32)
+    a = oracle.mhc_post(x, f, res, off, 20, 1e-6)
+    perm = [2, 0, 3, 1]
+    b = oracle.mhc_post(x, f, res[:, perm, :], off, 20, 1e-6)
+    np.testing.assert_allclose(b, a[:, perm, :], rtol=1e-12, atol=1e-12)
+    # the mixing matrix is the Sinkhorn oracle's, applied as a plain matrix product
+    S = oracle.sinkhorn(res, 20, 1e-6)
+    np.testing.assert_allclose(a, np.einsum("nij,njc->nic", S, xf), rtol=1e-12, atol=1e-12)

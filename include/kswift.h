@@ -157,6 +157,43 @@ int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf
                size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------
+ * FP8 block quantisation of bf16 rows (e4m3fn codes, one fp32 scale per block),
+ * for the quantised indexer of the reference's dtype = "fp8",
+ * scale_fmt = "ue8m0" configuration (baseline/indexer.py:14-17; the reference
+ * names the format but ships no kernel for it).  Per block of `block` elements
+ * of a row:
+ *   amax = max(max|x|, 1e-4);  s = amax * fp32(1/448)  (fp32, nearest even);
+ *   ue8m0 != 0: s = 2^ceil(log2 s)  (a power of two);
+ *   code = e4m3fn(clamp(x / s, -448, 448)), nearest even (IEEE division).
+ * x: bf16 [rows, D] (16-byte aligned); codes: [rows, D] bytes (8-byte aligned);
+ * scales: f32 [rows, D / block].  block in {8, 16, 32, 64, 128}, D % block == 0.
+ * Finite inputs only.
+ * ---------------------------------------------------------------------- */
+int ks_fp8_quant_rows(const uint16_t *x, int64_t rows, int64_t D, int64_t block,
+                      int32_t ue8m0, uint8_t *codes, float *scales, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Indexer on FP8 rows: scores -> top-k of ks_indexer (same contract, same
+ * exactness, same output) on the dequantised rows
+ *   q_h[d] = bf16(fp32(e4m3(q codes[d]) * q_scale)),  likewise k,
+ * one scale per row (a whole head of D elements: block = D in
+ * ks_fp8_quant_rows); with power-of-two (ue8m0) scales the dequantised values
+ * are exactly code * scale.  No RoPE: quantised rows are stored after it.
+ * q: [B, S, H, D] codes, q_scale: f32 [B, S, H]; k: batch b's T key rows of D
+ * codes start at k + b*k_batch_stride*D, k_scale: f32, batch b's scales start at
+ * k_scale + b*k_batch_stride.  Codes 8-byte aligned; no NaN codes.  Shapes,
+ * weights, outputs and workspace (ks_indexer_workspace_size) as ks_indexer.
+ * No reference counterpart (an FP8 configuration of baseline/indexer.py:14-17
+ * over the scoring of baseline/indexer.py:191-206).
+ * ---------------------------------------------------------------------- */
+int ks_indexer_fp8(const uint8_t *q, const float *q_scale, const uint8_t *k,
+                   const float *k_scale, const void *w, int32_t w_bf16,
+                   int64_t k_top, int32_t causal, int64_t start_pos, int32_t ratio,
+                   int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
+                   int64_t H, int64_t D, int64_t T, int64_t k_batch_stride,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------------
  * Exact sorted top-k per row with the reference post-processing.
  *
  * Replaces indexer_topk_kernel(blockDim, l2Ctrl, stream, scores, out, totalRows,

@@ -33,6 +33,10 @@ SIGNATURES = {
     "ks_indexer": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32,
                                   _c_i64, _c_i32, _c_i64, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                   _c_i64, _c_p, _c_sz, _c_p]),
+    "ks_fp8_quant_rows": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p]),
+    "ks_indexer_fp8": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i32, _c_i64,
+                                      _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_sz,
+                                      _c_p]),
     "ks_indexer_topk": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32, _c_i64,
                                        _c_p, _c_i32, _c_p]),
     "ks_sparse_attn_workspace_size": (_c_sz, [_c_i64] * 6),
@@ -59,7 +63,11 @@ DEBUG_SIGNATURES = {
     "ks_dbg_indexer_scores": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
                                              _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32, _c_f, _c_p,
                                              _c_p]),
+    "ks_dbg_indexer_fp8": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i32,
+                                          _c_i64, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p,
+                                          _c_sz, _c_p, _c_p, _c_i32]),
     "ks_dbg_mfma_bf16_chain": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),
+    "ks_dbg_mfma_fp8_chain": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),
     "ks_dbg_exact_dot_wide": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_p]),
     "ks_dbg_score_bound_c": (ctypes.c_float, []),
 }

@@ -1,4 +1,5 @@
-// Fused indexer entry: RoPE + row statistics of q and k (one launch) -> scores -> exact top-k.
+// Fused indexer entries: RoPE (or FP8 dequantisation) + row statistics of q and k (one launch) -> scores ->
+// exact top-k.
 //
 // Semantics of baseline/indexer.py:161-206 after the two projections (which stay in the caller):
 // RoPE on the configured segment of q (and k), score = sum_h w_h * relu(bf16(q_h . k)), causal mask,
@@ -66,49 +67,33 @@ extern "C" size_t ks_indexer_workspace_size(int64_t B, int64_t S, int64_t H, int
 }
 
 namespace {
-// path: 0 = bounded when the shape allows it, 1 = exact, 2 = bounded (error when the shape does not allow it)
-int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,
-                 int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
-                 int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64,
-                 int64_t B, int64_t S, int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
-                 size_t workspace_bytes, void *stream, float bound_c, uint32_t *stats, int path) {
-  ks::last_error().clear();
-  KS_CHECK_ARG(path >= 0 && path <= 3, "ks_indexer: path %d", path);
-  KS_CHECK_ARG(D == 128 || D == 64, "ks_indexer: D=%lld, the kernels are built for head_dim 64 and 128",
-               (long long)D);
-  KS_CHECK_ARG(H == 16 || H == 32 || H == 64, "ks_indexer: H=%lld must be 16, 32 or 64", (long long)H);
-  KS_CHECK_ARG(B >= 0 && S >= 0, "ks_indexer: negative B or S");
-  KS_CHECK_ARG(T >= 1 && T <= 65536, "ks_indexer: T=%lld must be in [1, 65536]", (long long)T);
-  KS_CHECK_ARG(k_batch_stride >= T, "ks_indexer: k_batch_stride < T");
-  KS_CHECK_ARG(ratio >= 1 && start_pos >= 0, "ks_indexer: ratio must be >= 1 and start_pos >= 0");
-  KS_CHECK_ARG(k_top >= 1, "ks_indexer: k_top must be >= 1");
-  KS_CHECK_ARG(rope_dim >= 0 && rope_dim % 8 == 0 && rope_start >= 0 && rope_start % 8 == 0 &&
-                   rope_start + rope_dim <= D,
-               "ks_indexer: rotated segment must be 8-aligned and inside the head");
-  if (rope_dim > 0) {
-    KS_CHECK_ARG(freqs != nullptr, "ks_indexer: freqs is null");
-    KS_CHECK_ARG(start_pos + S <= freq_rows, "ks_indexer: query positions exceed freqs rows");
-    KS_CHECK_ARG(!rope_k || T <= freq_rows, "ks_indexer: key positions exceed freqs rows");
-  }
+// Argument checks shared by the entries (fn names the entry in the messages).
+int check_indexer_args(const char *fn, int64_t k_top, int64_t start_pos, int32_t ratio, int64_t B, int64_t S,
+                       int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, int path) {
+  KS_CHECK_ARG(path >= 0 && path <= 3, "%s: path %d", fn, path);
+  KS_CHECK_ARG(D == 128 || D == 64, "%s: D=%lld, the kernels are built for head_dim 64 and 128", fn, (long long)D);
+  KS_CHECK_ARG(H == 16 || H == 32 || H == 64, "%s: H=%lld must be 16, 32 or 64", fn, (long long)H);
+  KS_CHECK_ARG(B >= 0 && S >= 0, "%s: negative B or S", fn);
+  KS_CHECK_ARG(T >= 1 && T <= 65536, "%s: T=%lld must be in [1, 65536]", fn, (long long)T);
+  KS_CHECK_ARG(k_batch_stride >= T, "%s: k_batch_stride < T", fn);
+  KS_CHECK_ARG(ratio >= 1 && start_pos >= 0, "%s: ratio must be >= 1 and start_pos >= 0", fn);
+  KS_CHECK_ARG(k_top >= 1, "%s: k_top must be >= 1", fn);
   const int64_t kk = k_top < T ? k_top : T;
-  KS_CHECK_ARG(kk <= 4096, "ks_indexer: min(k_top, T)=%lld exceeds 4096", (long long)kk);
-  if (B * S == 0) return KS_OK;
-  KS_CHECK_ARG(q && k && w && out, "ks_indexer: null pointer");
-  KS_CHECK_ARG(ks::aligned(q, 16) && ks::aligned(k, 16), "ks_indexer: q and k must be 16-byte aligned");
-  const IndexerWs ws = carve(workspace, B, S, H, D, T);
-  KS_CHECK_ARG(workspace != nullptr && workspace_bytes >= ws.bytes,
-               "ks_indexer: workspace of %zu bytes required, %zu given", ws.bytes, workspace_bytes);
-  KS_CHECK_ARG(ks::aligned(workspace, 256), "ks_indexer: workspace must be 256-byte aligned");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int rd = static_cast<int>(rope_dim);
-  // q rows at positions start_pos + s; k rows of every batch (stride k_batch_stride) at positions t
-  const ks::RowJob qjob{q, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H, H, S, start_pos, rd};
-  const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
-  int rc = ks::launch_rope_rows(qjob, kjob, freqs, static_cast<int>(D), static_cast<int>(rope_start), st);
-  if (rc != KS_OK) return rc;
+  KS_CHECK_ARG(kk <= 4096, "%s: min(k_top, T)=%lld exceeds 4096", fn, (long long)kk);
+  return KS_OK;
+}
+
+// Scores of the prepared rows (ws.q_rot / ws.k_rot with their statistics) -> exact top-k.
+// path: 0 = bounded when the shape allows it, 1 = exact, 2 = bounded (error when the shape does not allow
+// it), 3 = bounded with the extended counters.
+int indexer_select(const char *fn, const IndexerWs &ws, const void *w, int32_t w_bf16, int64_t k_top, int32_t causal,
+                   int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
+                   int64_t H, int64_t D, int64_t T, hipStream_t st, float bound_c, uint32_t *stats, int path) {
+  const int64_t kk = k_top < T ? k_top : T;
   const bool can_bound = H == 64 && D == 128 && !w_bf16 && T <= 32768 && kk <= 2048;
   KS_CHECK_ARG(path < 2 || can_bound,
-               "ks_indexer: the bounded path needs H = 64, D = 128, fp32 weights, T <= 32768 and k <= 2048");
+               "%s: the bounded path needs H = 64, D = 128, fp32 weights, T <= 32768 and k <= 2048", fn);
+  int rc;
   if (can_bound && path != 1) {
     rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span, ws.scores, B,
                                    S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, bound_c, nullptr, st, ws.bounds,
@@ -123,7 +108,67 @@ int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_
   rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, w_bf16 ? 1 : 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span,
                                  ws.scores, B, S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, bound_c, stats, st);
   if (rc != KS_OK) return rc;
-  return ks_indexer_topk(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, stream);
+  return ks_indexer_topk(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, st);
+}
+
+int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,
+                 int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
+                 int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64,
+                 int64_t B, int64_t S, int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
+                 size_t workspace_bytes, void *stream, float bound_c, uint32_t *stats, int path) {
+  ks::last_error().clear();
+  int rc = check_indexer_args("ks_indexer", k_top, start_pos, ratio, B, S, H, D, T, k_batch_stride, path);
+  if (rc != KS_OK) return rc;
+  KS_CHECK_ARG(rope_dim >= 0 && rope_dim % 8 == 0 && rope_start >= 0 && rope_start % 8 == 0 &&
+                   rope_start + rope_dim <= D,
+               "ks_indexer: rotated segment must be 8-aligned and inside the head");
+  if (rope_dim > 0) {
+    KS_CHECK_ARG(freqs != nullptr, "ks_indexer: freqs is null");
+    KS_CHECK_ARG(start_pos + S <= freq_rows, "ks_indexer: query positions exceed freqs rows");
+    KS_CHECK_ARG(!rope_k || T <= freq_rows, "ks_indexer: key positions exceed freqs rows");
+  }
+  if (B * S == 0) return KS_OK;
+  KS_CHECK_ARG(q && k && w && out, "ks_indexer: null pointer");
+  KS_CHECK_ARG(ks::aligned(q, 16) && ks::aligned(k, 16), "ks_indexer: q and k must be 16-byte aligned");
+  const IndexerWs ws = carve(workspace, B, S, H, D, T);
+  KS_CHECK_ARG(workspace != nullptr && workspace_bytes >= ws.bytes,
+               "ks_indexer: workspace of %zu bytes required, %zu given", ws.bytes, workspace_bytes);
+  KS_CHECK_ARG(ks::aligned(workspace, 256), "ks_indexer: workspace must be 256-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rd = static_cast<int>(rope_dim);
+  // q rows at positions start_pos + s; k rows of every batch (stride k_batch_stride) at positions t
+  const ks::RowJob qjob{q, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H, H, S, start_pos, rd};
+  const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
+  rc = ks::launch_rope_rows(qjob, kjob, freqs, static_cast<int>(D), static_cast<int>(rope_start), st);
+  if (rc != KS_OK) return rc;
+  return indexer_select("ks_indexer", ws, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B, S, H,
+                        D, T, st, bound_c, stats, path);
+}
+
+int indexer_fp8_impl(const uint8_t *q, const float *q_scale, const uint8_t *k, const float *k_scale, const void *w,
+                     int32_t w_bf16, int64_t k_top, int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset,
+                     void *out, int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D, int64_t T,
+                     int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream, float bound_c,
+                     uint32_t *stats, int path) {
+  ks::last_error().clear();
+  int rc = check_indexer_args("ks_indexer_fp8", k_top, start_pos, ratio, B, S, H, D, T, k_batch_stride, path);
+  if (rc != KS_OK) return rc;
+  if (B * S == 0) return KS_OK;
+  KS_CHECK_ARG(q && q_scale && k && k_scale && w && out, "ks_indexer_fp8: null pointer");
+  KS_CHECK_ARG(ks::aligned(q, 8) && ks::aligned(k, 8) && ks::aligned(q_scale, 4) && ks::aligned(k_scale, 4),
+               "ks_indexer_fp8: q and k codes must be 8-byte aligned, scales 4-byte aligned");
+  const IndexerWs ws = carve(workspace, B, S, H, D, T);
+  KS_CHECK_ARG(workspace != nullptr && workspace_bytes >= ws.bytes,
+               "ks_indexer_fp8: workspace of %zu bytes required, %zu given", ws.bytes, workspace_bytes);
+  KS_CHECK_ARG(ks::aligned(workspace, 256), "ks_indexer_fp8: workspace must be 256-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // q rows (scale per row) and k rows of every batch (stride k_batch_stride, scale per row, same stride)
+  const ks::Fp8RowJob qjob{q, q_scale, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H};
+  const ks::Fp8RowJob kjob{k, k_scale, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride};
+  rc = ks::launch_fp8_rows(qjob, kjob, static_cast<int>(D), st);
+  if (rc != KS_OK) return rc;
+  return indexer_select("ks_indexer_fp8", ws, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B, S,
+                        H, D, T, st, bound_c, stats, path);
 }
 }  // namespace
 
@@ -149,4 +194,24 @@ extern "C" int ks_dbg_indexer(const uint16_t *q, const uint16_t *k, const void *
   return indexer_impl(q, k, w, w_bf16, freqs, freq_rows, rope_start, rope_dim, rope_k, k_top, causal, start_pos, ratio,
                       offset, out, out_i64, B, S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, bound_c,
                       stats, path);
+}
+
+extern "C" int ks_indexer_fp8(const uint8_t *q, const float *q_scale, const uint8_t *k, const float *k_scale,
+                              const void *w, int32_t w_bf16, int64_t k_top, int32_t causal, int64_t start_pos,
+                              int32_t ratio, int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
+                              int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
+                              size_t workspace_bytes, void *stream) {
+  return indexer_fp8_impl(q, q_scale, k, k_scale, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B,
+                          S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, ks::kScoreBoundC, nullptr, 0);
+}
+
+// Diagnostic variant of ks_indexer_fp8 with the path choice and counters of ks_dbg_indexer.
+extern "C" int ks_dbg_indexer_fp8(const uint8_t *q, const float *q_scale, const uint8_t *k, const float *k_scale,
+                                  const void *w, int32_t w_bf16, int64_t k_top, int32_t causal, int64_t start_pos,
+                                  int32_t ratio, int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
+                                  int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
+                                  size_t workspace_bytes, void *stream, uint32_t *stats, int32_t path) {
+  return indexer_fp8_impl(q, q_scale, k, k_scale, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B,
+                          S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, ks::kScoreBoundC, stats,
+                          path);
 }

@@ -68,6 +68,21 @@ __device__ __forceinline__ void chunk_stats(uint4 v, float &ss, int &lsb) {
   }
 }
 
+// Sum and minimum over the CPR lanes of a row (CPR in {8, 16}: an aligned lane group) with DPP exchanges.
+template <int CPR>
+__device__ __forceinline__ void row_reduce(float &ss, int &lsb) {
+#define KS_STEP(S)                                                                 \
+  ss += __builtin_bit_cast(float, lane_xor<S>(__builtin_bit_cast(uint32_t, ss)));  \
+  lsb = min(lsb, static_cast<int>(lane_xor<S>(static_cast<uint32_t>(lsb))));
+  KS_STEP(1)
+  KS_STEP(2)
+  KS_STEP(4)
+  if constexpr (CPR == 16) {
+    KS_STEP(8)
+  }
+#undef KS_STEP
+}
+
 // Norm upper bound and span from a row's sum of squares and smallest LSB exponent: an fp32 sum of at most
 // 128 exact squares has relative error < 2^-16 and sqrt adds < 1 ulp; the 2^-12 pad covers both.
 __device__ __forceinline__ void row_norm_span(float ss, int lsb, float &norm, int32_t &span) {
@@ -111,6 +126,21 @@ struct RowJob {
 // otherwise.  Rotated dims [rope_start, rope_start + job.rope_dim), freqs = (cos, sin) per position.
 int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
                      hipStream_t stream);
+
+// One set of e4m3 rows for the dequantisation / row-statistics launch: row r is source row
+// (r / rows_per_batch) * src_batch_rows + r % rows_per_batch of src (D code bytes) with fp32 scale
+// scale[source row]; destination row r of dst receives bf16(fp32(value * scale)), norm/span its statistics.
+struct Fp8RowJob {
+  const uint8_t *src;
+  const float *scale;
+  uint16_t *dst;
+  float *norm;
+  int32_t *span;
+  int64_t rows, rows_per_batch, src_batch_rows;
+};
+
+// Both jobs in one launch (job1.rows may be 0); D in {64, 128}.
+int launch_fp8_rows(const Fp8RowJob &job0, const Fp8RowJob &job1, int D, hipStream_t stream);
 
 // Exact scores (bounds == nullptr), or, with bounds (H = 64, D = 128, fp32 weights), the canonical score from
 // the lower interval end of every dot plus a per-score bound U: the exact score lies in [score - U,

@@ -46,21 +46,6 @@ RowJobK kernel_job(const RowJob &j) {
   return k;
 }
 
-// Sum and minimum over the CPR lanes of a row (CPR in {8, 16}: an aligned lane group) with DPP exchanges.
-template <int CPR>
-__device__ __forceinline__ void row_reduce(float &ss, int &lsb) {
-#define KS_STEP(S)                                                                 \
-  ss += __builtin_bit_cast(float, lane_xor<S>(__builtin_bit_cast(uint32_t, ss)));  \
-  lsb = min(lsb, static_cast<int>(lane_xor<S>(static_cast<uint32_t>(lsb))));
-  KS_STEP(1)
-  KS_STEP(2)
-  KS_STEP(4)
-  if constexpr (CPR == 16) {
-    KS_STEP(8)
-  }
-#undef KS_STEP
-}
-
 // One thread per 16-byte chunk; blocks [0, blocks0) take job 0 and the rest job 1 (a uniform choice, so
 // each field is selected separately from the kernel arguments, never through a pointer to them).
 // CPR: chunks per row, 8 or 16 with statistics (0: any D, no statistics).

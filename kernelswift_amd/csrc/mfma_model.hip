@@ -36,6 +36,33 @@ __global__ __launch_bounds__(64) void mfma_chain_kernel(const uint16_t *__restri
   for (int i = 0; i < 4; ++i) d[t * 256 + (4 * g + i) * 16 + r] = acc[i];
 }
 
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+
+// v_mfma_scale_f32_16x16x128_f8f6f4 on OCP e4m3 operands with unit block scales (E8M0 127 = 2^0).
+__device__ __forceinline__ f32x4_t mfma16_fp8(i32x8_t a, i32x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// As mfma_chain_kernel for the fp8 instruction: a [t][nchain][16 rows][128 k] e4m3, bt [t][nchain][16][128];
+// lane l holds row l % 16, k = 32 (l / 16) .. + 31.
+__global__ __launch_bounds__(64) void mfma_fp8_chain_kernel(const uint8_t *__restrict__ a, const uint8_t *__restrict__ bt,
+                                                           const float *__restrict__ c, float *__restrict__ d,
+                                                           int nchain) {
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+  f32x4_t acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = c[t * 256 + (4 * g + i) * 16 + r];
+  for (int j = 0; j < nchain; ++j) {
+    const int64_t base = (t * nchain + j) * 2048;
+    const i32x8_t av = *reinterpret_cast<const i32x8_t *>(a + base + r * 128 + 32 * g);
+    const i32x8_t bv = *reinterpret_cast<const i32x8_t *>(bt + base + r * 128 + 32 * g);
+    acc = mfma16_fp8(av, bv, acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[t * 256 + (4 * g + i) * 16 + r] = acc[i];
+}
+
 // out[i] = exact_dot_wide_bf16 of rows q[i] and k[i] (length D), PARTS lanes per dot.
 template <int D, int PARTS>
 __global__ __launch_bounds__(64) void exact_dot_wide_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
@@ -75,6 +102,21 @@ extern "C" int ks_dbg_exact_dot_wide(const uint16_t *q, const uint16_t *k, uint1
   else
     hipLaunchKernelGGL((ks::exact_dot_wide_kernel<64, 2>), dim3(blocks), dim3(64), 0, st, q, k, out, n);
   KS_CHECK_LAUNCH("exact_dot_wide_kernel");
+  return KS_OK;
+}
+
+// Not part of the public header (a test instrument): the fp8 (e4m3) instruction, as ks_dbg_mfma_bf16_chain.
+extern "C" int ks_dbg_mfma_fp8_chain(const uint8_t *a, const uint8_t *bt, const float *c, float *d, int64_t ntests,
+                                     int32_t nchain, void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(ntests >= 0 && ntests < (int64_t(1) << 31), "ks_dbg_mfma_fp8_chain: ntests out of range");
+  KS_CHECK_ARG(nchain >= 1 && nchain <= 64, "ks_dbg_mfma_fp8_chain: nchain must be in [1, 64]");
+  if (ntests == 0) return KS_OK;
+  KS_CHECK_ARG(a && bt && c && d, "ks_dbg_mfma_fp8_chain: null pointer");
+  KS_CHECK_ARG(ks::aligned(a, 32) && ks::aligned(bt, 32), "ks_dbg_mfma_fp8_chain: operands must be 32-byte aligned");
+  hipLaunchKernelGGL(ks::mfma_fp8_chain_kernel, dim3(static_cast<unsigned>(ntests)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), a, bt, c, d, static_cast<int>(nchain));
+  KS_CHECK_LAUNCH("mfma_fp8_chain_kernel");
   return KS_OK;
 }
 

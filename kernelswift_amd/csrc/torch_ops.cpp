@@ -150,6 +150,65 @@ at::Tensor indexer(const at::Tensor& q, const at::Tensor& k, const at::Tensor& w
   return out;
 }
 
+// ---------------------------------------------------------------- FP8 indexer
+std::tuple<at::Tensor, at::Tensor> fp8_quant(const at::Tensor& x, int64_t block, bool ue8m0) {
+  check_gpu(x, "x");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16, "x must be bfloat16");
+  TORCH_CHECK(x.dim() >= 1 && block > 0 && x.size(-1) % block == 0, "the last dim must be a multiple of block");
+  const int64_t D = x.size(-1);
+  const int64_t rows = D ? x.numel() / D : 0;
+  at::Tensor codes = at::empty(x.sizes(), x.options().dtype(at::kFloat8_e4m3fn));
+  std::vector<int64_t> ss(x.sizes().begin(), x.sizes().end());
+  ss.back() = D / block;
+  at::Tensor scales = at::empty(ss, x.options().dtype(at::kFloat));
+  check_rc(ks_fp8_quant_rows(reinterpret_cast<const uint16_t*>(x.data_ptr()), rows, D, block, ue8m0 ? 1 : 0,
+                             reinterpret_cast<uint8_t*>(codes.data_ptr()), scales.data_ptr<float>(), current_stream(x)),
+           "ks_mi355x::fp8_quant");
+  return {codes, scales};
+}
+
+void check_codes(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.scalar_type() == at::kFloat8_e4m3fn || t.scalar_type() == at::kByte, name,
+              " must be float8_e4m3fn (or its uint8 bits)");
+}
+
+at::Tensor indexer_fp8(const at::Tensor& q, const at::Tensor& q_scale, const at::Tensor& k, const at::Tensor& k_scale,
+                       const at::Tensor& weights, int64_t k_top, bool causal, int64_t start_pos, int64_t ratio,
+                       int64_t offset, bool out_i64, c10::optional<int64_t> T_opt) {
+  check_gpu(q, "q");
+  check_gpu(q_scale, "q_scale");
+  check_gpu(weights, "weights");
+  check_gpu(k, "k", false);
+  check_gpu(k_scale, "k_scale", false);
+  check_codes(q, "q");
+  check_codes(k, "k");
+  TORCH_CHECK(q_scale.scalar_type() == at::kFloat && k_scale.scalar_type() == at::kFloat, "scales must be float32");
+  const int32_t wbf = weights_bf16(weights);
+  TORCH_CHECK(q.dim() == 4 && k.dim() == 3 && weights.dim() == 3, "q [b,s,h,d], k [b,t,d], weights [b,s,h]");
+  const int64_t B = q.size(0), S = q.size(1), H = q.size(2), D = q.size(3);
+  TORCH_CHECK(k.size(0) >= B && k.size(2) == D, "k shape mismatch");
+  TORCH_CHECK(weights.size(0) == B && weights.size(1) == S && weights.size(2) == H, "weights shape mismatch");
+  TORCH_CHECK(q_scale.dim() == 3 && q_scale.size(0) == B && q_scale.size(1) == S && q_scale.size(2) == H,
+              "q_scale must be [b, s, h]");
+  TORCH_CHECK(k.stride(2) == 1 && k.stride(1) == D && k.stride(0) % D == 0, "k rows must be contiguous");
+  TORCH_CHECK(k_scale.dim() == 2 && k_scale.size(0) >= B && k_scale.size(1) == k.size(1) && k_scale.stride(1) == 1,
+              "k_scale must be [b, t] with contiguous rows");
+  const int64_t T = T_opt.value_or(k.size(1));
+  TORCH_CHECK(T >= 1 && T <= k.size(1), "T out of range");
+  const int64_t kbs = B > 1 ? k.stride(0) / D : std::max(k.size(1), T);
+  TORCH_CHECK(B <= 1 || k_scale.stride(0) == kbs, "k_scale must have the batch stride of k (in rows)");
+  const size_t need = ks_indexer_workspace_size(B, S, H, D, T);
+  at::Tensor ws = at::empty({static_cast<int64_t>(std::max<size_t>(need, 1))}, q.options().dtype(at::kByte));
+  const int64_t kk = std::min(k_top, T);
+  at::Tensor out = at::empty({B, S, kk}, q.options().dtype(out_i64 ? at::kLong : at::kInt));
+  check_rc(ks_indexer_fp8(reinterpret_cast<const uint8_t*>(q.data_ptr()), q_scale.data_ptr<float>(),
+                          reinterpret_cast<const uint8_t*>(k.data_ptr()), k_scale.data_ptr<float>(), weights.data_ptr(),
+                          wbf, k_top, causal ? 1 : 0, start_pos, static_cast<int32_t>(ratio), offset, out.data_ptr(),
+                          out_i64 ? 1 : 0, B, S, H, D, T, kbs, ws.data_ptr(), ws.numel(), current_stream(q)),
+           "ks_mi355x::indexer_fp8");
+  return out;
+}
+
 // ---------------------------------------------------------------- sparse attention
 at::Tensor sparse_attn(const at::Tensor& q, const at::Tensor& kv, const at::Tensor& attn_sink,
                        const at::Tensor& topk_idxs, double softmax_scale, c10::optional<int64_t> dv_opt) {
@@ -237,6 +296,9 @@ TORCH_LIBRARY(ks_mi355x, m) {
         "int? T=None) -> Tensor");
   m.def("sparse_attn(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, float softmax_scale, "
         "int? dv=None) -> Tensor");
+  m.def("fp8_quant(Tensor x, int block=128, bool ue8m0=True) -> (Tensor, Tensor)");
+  m.def("indexer_fp8(Tensor q, Tensor q_scale, Tensor k, Tensor k_scale, Tensor weights, int k_top, bool causal, "
+        "int start_pos, int ratio=1, int offset=0, bool out_i64=False, int? T=None) -> Tensor");
   m.def("mhc_pre(Tensor x, Tensor pre_logits) -> Tensor");
   m.def("mhc_post(Tensor x, Tensor f, Tensor res_logits, Tensor post_logits, int sinkhorn_iters=20, "
         "float eps=1e-06) -> Tensor");
@@ -249,6 +311,8 @@ TORCH_LIBRARY_IMPL(ks_mi355x, CUDA, m) {
   m.impl("indexer_topk", &indexer_topk);
   m.impl("indexer", &indexer);
   m.impl("sparse_attn", &sparse_attn);
+  m.impl("fp8_quant", &fp8_quant);
+  m.impl("indexer_fp8", &indexer_fp8);
   m.impl("mhc_pre", &mhc_pre);
   m.impl("mhc_post", &mhc_post);
 }

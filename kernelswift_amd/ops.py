@@ -19,7 +19,8 @@ from . import _lib
 
 __all__ = [
     "sinkhorn", "rope_inplace", "indexer_row_stats", "indexer_scores", "topk_mask", "indexer",
-    "indexer_workspace_size", "sparse_attn", "sparse_attn_workspace_size", "mhc_pre", "mhc_post", "copy_bytes",
+    "indexer_workspace_size", "fp8_quant", "indexer_fp8", "sparse_attn", "sparse_attn_workspace_size", "mhc_pre",
+    "mhc_post", "copy_bytes",
 ]
 
 
@@ -192,6 +193,70 @@ def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Opti
                                       1 if causal else 0, start_pos, ratio, offset, _p(out),
                                       1 if out_dtype == torch.int64 else 0, B, S, H, D, T, kbs, _p(workspace),
                                       workspace.numel(), _stream(q)), "indexer")
+    return out
+
+
+def fp8_quant(x: torch.Tensor, block: int = 128, ue8m0: bool = True):
+    """FP8 block quantisation of bf16 rows (the dtype = "fp8", scale_fmt = "ue8m0" configuration of
+    baseline/indexer.py:14-17): per block of `block` elements of the last dim, s = max(amax, 1e-4) * fp32(1/448)
+    (a power of two 2^ceil(log2 s) under ue8m0), codes = e4m3fn(clamp(x / s, -448, 448)) nearest even.
+
+    x: bf16 [..., D].  Returns (codes float8_e4m3fn [..., D], scales float32 [..., D / block])."""
+    _check(x.dtype == torch.bfloat16, "x must be bfloat16")
+    _on_gpu(x)
+    D = x.shape[-1]
+    _check(D % block == 0, "the last dim must be a multiple of block")
+    rows = x.numel() // D if D else 0
+    codes = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    scales = torch.empty((*x.shape[:-1], D // block), dtype=torch.float32, device=x.device)
+    _lib.check(_lib.load().ks_fp8_quant_rows(_p(x), rows, D, block, 1 if ue8m0 else 0, _p(codes), _p(scales),
+                                             _stream(x)), "fp8_quant")
+    return codes, scales
+
+
+def _fp8_codes(t: torch.Tensor) -> None:
+    _check(t.dtype in (torch.float8_e4m3fn, torch.uint8), "codes must be float8_e4m3fn (or their uint8 bits)")
+
+
+def indexer_fp8(q: torch.Tensor, q_scale: torch.Tensor, k: torch.Tensor, k_scale: torch.Tensor,
+                weights: torch.Tensor, k_top: int, causal: bool, start_pos: int, ratio: int = 1, offset: int = 0,
+                out_dtype: torch.dtype = torch.int32, workspace: Optional[torch.Tensor] = None,
+                T: Optional[int] = None) -> torch.Tensor:
+    """Indexer scores -> exact top-k on FP8 rows (as `indexer`, without RoPE: quantised rows are stored after
+    it), with q_h = bf16(fp32(e4m3(q) * q_scale)) and k likewise, one scale per row.
+
+    q: e4m3 [B, S, H, D], q_scale float32 [B, S, H]; k: e4m3 [B, Tk, D] with contiguous rows (batch-strided
+    views accepted), k_scale float32 [B, Tk] with the same batch stride in rows; weights float32/bf16 [B, S, H].
+    Returns [B, S, min(k_top, T)] int32 (default) or int64."""
+    _fp8_codes(q)
+    _fp8_codes(k)
+    _check(q_scale.dtype == torch.float32 and k_scale.dtype == torch.float32, "scales must be float32")
+    _check(weights.dtype in (torch.float32, torch.bfloat16), "weights must be float32 or bfloat16")
+    _on_gpu(q, q_scale, weights)
+    _on_gpu(k, k_scale, contiguous=False)
+    _check(q.dim() == 4 and k.dim() == 3 and weights.dim() == 3, "q [b,s,h,d], k [b,t,d], weights [b,s,h]")
+    B, S, H, D = q.shape
+    _check(k.shape[0] >= B and k.shape[2] == D, "k shape mismatch")
+    _check(tuple(weights.shape) == (B, S, H) and tuple(q_scale.shape) == (B, S, H), "weights / q_scale shape")
+    _check(q.is_contiguous() and q_scale.is_contiguous() and weights.is_contiguous(),
+           "q, q_scale and weights must be contiguous")
+    _check(k.stride(2) == 1 and k.stride(1) == D and k.stride(0) % D == 0, "k rows must be contiguous")
+    _check(k_scale.dim() == 2 and k_scale.shape[0] >= B and k_scale.shape[1] == k.shape[1]
+           and k_scale.stride(1) == 1, "k_scale [b, t] with contiguous rows")
+    T = k.shape[1] if T is None else T
+    _check(1 <= T <= k.shape[1], "T out of range")
+    kbs = k.stride(0) // D if B > 1 else max(k.shape[1], T)
+    _check(B <= 1 or k_scale.stride(0) == kbs, "k_scale must have the batch stride of k (in rows)")
+    need = indexer_workspace_size(B, S, H, D, T)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    kk = min(k_top, T)
+    out = torch.empty((B, S, kk), dtype=out_dtype, device=q.device)
+    _lib.check(_lib.load().ks_indexer_fp8(_p(q), _p(q_scale), _p(k), _p(k_scale), _p(weights),
+                                          1 if weights.dtype == torch.bfloat16 else 0, k_top, 1 if causal else 0,
+                                          start_pos, ratio, offset, _p(out), 1 if out_dtype == torch.int64 else 0,
+                                          B, S, H, D, T, kbs, _p(workspace), workspace.numel(), _stream(q)),
+               "indexer_fp8")
     return out
 
 

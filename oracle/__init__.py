@@ -20,6 +20,12 @@ Pinning (what checks each function beyond restating it; see tests/test_oracle.py
                   recomputation of the canonical order on tiny shapes, mask closed form.
   topk_stable     brute force over all permutations of tiny rows, ties and -inf.
   postprocess     integer closed form of baseline/indexer.py:198-206.
+  e4m3_encode     torch's float8_e4m3fn conversion (a library routine) over every bf16
+                  value in range and every tie midpoint, and nearest-value brute force.
+  e4m3_decode     torch's float8_e4m3fn -> float32 over all 256 codes.
+  fp8_quant_rows  closed forms (ue8m0 scales are powers of two with amax/s in (224, 448];
+                  the largest element maps to a code of the top binade; all-zero rows
+                  take the 1e-4 floor), torch's cast of the scaled rows.
   sparse_attn     closed forms: all-invalid -> 0; equal scores -> k/(k+e^(sink-z)) *
                   mean(V); single valid index with sink -> -inf gives that V row;
                   duplicates counted with multiplicity.
@@ -222,6 +228,76 @@ def indexer(q: np.ndarray, k: np.ndarray, w: np.ndarray, freqs: np.ndarray, k_to
         kr = rope_bf16(k.reshape(B, T, 1, D), freqs, rope_start, rope_dim, pos0=0).reshape(B, T, D)
     sc = indexer_scores(qr, kr, w, causal, start_pos, ratio, threads=threads)
     kk = min(k_top, T)
+    return postprocess(topk_stable(sc, kk), causal, start_pos, ratio, offset)
+
+
+# ---------------------------------------------------------------- FP8 (e4m3fn) rows
+# The reference names an FP8 configuration of its DeepSeek-style model (dtype = "fp8", scale_fmt = "ue8m0";
+# baseline/indexer.py:14-17) but ships no kernel for it; these functions state the quantised indexer that the
+# library implements: block quantisation to e4m3fn with per-block fp32 scales, and the indexer run on the
+# dequantised rows (the scoring of baseline/indexer.py:191-206 without RoPE, which precedes quantisation).
+_INV448 = np.float32(1.0) / np.float32(448.0)
+
+
+def e4m3_encode(y) -> np.ndarray:
+    """e4m3fn codes (uint8) of float32 values with |y| <= 448, rounded to nearest even (ties to the even
+    code); -0 and negative values that round to zero keep the sign bit."""
+    y = np.asarray(y, dtype=np.float32)
+    sign = ((y.view(np.uint32) >> 24) & 0x80).astype(np.int64)
+    a = np.abs(y).astype(np.float64)
+    _, ex = np.frexp(a)  # a = m 2^ex, 0.5 <= m < 1: the exponent of a is ex - 1
+    e = ex.astype(np.int64) - 1
+    sub = a < 2.0 ** -6
+    q_sub = np.rint(a * 512.0).astype(np.int64)            # multiples of 2^-9 (q = 8 is 2^-6 itself)
+    es = np.where(sub, 0, e)
+    q_nrm = np.rint(np.ldexp(a, 3 - es)).astype(np.int64)  # a / 2^(e-3) in [8, 16]; 16 carries
+    code = np.where(sub, q_sub, ((es + 7) << 3) + q_nrm - 8)
+    return (sign | code).astype(np.uint8)
+
+
+def e4m3_decode(c) -> np.ndarray:
+    """Values (float32, exact) of e4m3fn codes; the NaN codes 0x7F / 0xFF give NaN."""
+    c = np.asarray(c, dtype=np.uint8).astype(np.int64)
+    e = (c >> 3) & 15
+    m = c & 7
+    a = np.where(e == 0, m * 2.0 ** -9, (8 + m) * np.ldexp(1.0, e - 10))
+    a = np.where((c & 0x7F) == 0x7F, np.nan, a)
+    return np.where(c & 0x80, -a, a).astype(np.float32)
+
+
+def fp8_quant_rows(x: np.ndarray, block: int, ue8m0: bool = True):
+    """Block quantisation of bf16 rows: per block of `block` elements of the last dim,
+    amax = max(max|x|, fp32(1e-4)), s = fp32(amax * fp32(1/448)), under ue8m0 s = 2^ceil(log2 s), and
+    code = e4m3fn(clip(fp32(x / s), -448, 448)).  x: bf16 bits [..., D].
+    Returns (codes uint8 [..., D], scales float32 [..., D / block])."""
+    x = np.asarray(x, dtype=np.uint16)
+    D = x.shape[-1]
+    assert D % block == 0
+    xf = bf16_to_f32(x).reshape(*x.shape[:-1], D // block, block)
+    amax = np.maximum(np.abs(xf).max(axis=-1), np.float32(1e-4)).astype(np.float32)
+    s = (amax * _INV448).astype(np.float32)
+    if ue8m0:
+        m, ex = np.frexp(s.astype(np.float64))   # s = m 2^ex: ceil(log2 s) = ex - 1 when m == 1/2, else ex
+        s = np.ldexp(1.0, np.where(m == 0.5, ex - 1, ex)).astype(np.float32)
+    y = np.clip((xf / s[..., None]).astype(np.float32), np.float32(-448.0), np.float32(448.0))
+    return e4m3_encode(y).reshape(x.shape), s
+
+
+def fp8_dequant_rows(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """bf16 bits of bf16(fp32(value(code) * scale)) with one scale per row (scales: codes.shape[:-1])."""
+    v = e4m3_decode(codes) * np.asarray(scales, dtype=np.float32)[..., None]
+    return f32_to_bf16(v.astype(np.float32))
+
+
+def indexer_fp8(qc: np.ndarray, qs: np.ndarray, kc: np.ndarray, ks: np.ndarray, w: np.ndarray, k_top: int,
+                causal: bool, start_pos: int, ratio: int = 1, offset: int = 0,
+                threads: Optional[int] = None) -> np.ndarray:
+    """Indexer on FP8 rows: canonical scores of the dequantised q [B, S, H, D] and k [B, T, D] (one scale
+    per row: qs [B, S, H], ks [B, T]) -> stable top-k -> post-processing.  Returns int64 [B, S, min(k_top, T)]."""
+    q = fp8_dequant_rows(qc, qs)
+    k = fp8_dequant_rows(kc, ks)
+    sc = indexer_scores(q, k, w, causal, start_pos, ratio, threads=threads)
+    kk = min(k_top, k.shape[1])
     return postprocess(topk_stable(sc, kk), causal, start_pos, ratio, offset)
 
 

@@ -414,3 +414,84 @@ def test_mhc_oracle_closed_forms():
     # the mixing matrix is the Sinkhorn oracle's, applied as a plain matrix product
     S = oracle.sinkhorn(res, 20, 1e-6)
     np.testing.assert_allclose(a, np.einsum("nij,njc->nic", S, xf), rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------ FP8 rows
+def _torch_e4m3(y):
+    return torch.from_numpy(np.ascontiguousarray(y, np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def _e4m3_values():
+    """All finite e4m3fn values (nonnegative codes 0x00..0x7E), by their definition."""
+    out = []
+    for c in range(0x7F):
+        e, m = c >> 3, c & 7
+        out.append(Fraction(m, 512) if e == 0 else Fraction(8 + m, 8) * Fraction(2) ** (e - 7))
+    return out
+
+
+def test_e4m3_encode_against_torch_and_bruteforce():
+    # every bf16 value in range
+    b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = oracle.bf16_to_f32(b)
+    y = f[np.isfinite(f) & (np.abs(f) <= 448)]
+    np.testing.assert_array_equal(oracle.e4m3_encode(y), _torch_e4m3(y))
+    # every midpoint between neighbouring codes (a tie: the even code wins), and its fp32 neighbours
+    vals = _e4m3_values()
+    mids = np.array([float((a + c) / 2) for a, c in zip(vals[:-1], vals[1:])], np.float32)
+    near = np.concatenate([mids, np.nextafter(mids, np.float32(0)), np.nextafter(mids, np.float32(1e9))])
+    near = np.concatenate([near, -near])
+    np.testing.assert_array_equal(oracle.e4m3_encode(near), _torch_e4m3(near))
+    # brute force: nearest value, ties to the even code (pure Python over a sample)
+    rng = np.random.default_rng(7)
+    sample = np.concatenate([mids[::3], (rng.random(300) * 448).astype(np.float32),
+                             (2.0 ** rng.uniform(-12, -5, 200)).astype(np.float32)])
+    for v in sample:
+        x = Fraction(float(v))
+        best = min(range(0x7F), key=lambda c: (abs(vals[c] - x), c & 1))
+        assert int(oracle.e4m3_encode(np.float32(v))) == best, v
+    assert int(oracle.e4m3_encode(np.float32(-0.0))) == 0x80
+    assert int(oracle.e4m3_encode(np.float32(448.0))) == 0x7E
+
+
+def test_e4m3_decode_all_codes():
+    c = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(c.copy()).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(oracle.e4m3_decode(c), want)  # NaN codes compare equal as NaN
+    vals = _e4m3_values()
+    assert [Fraction(float(v)) for v in oracle.e4m3_decode(c[:0x7F])] == vals
+
+
+@pytest.mark.parametrize("block,ue8m0", [(128, True), (128, False), (32, True), (8, False)])
+def test_fp8_quant_rows_closed_forms(block, ue8m0):
+    rng = np.random.default_rng(block + ue8m0)
+    rows, D = 64, 256
+    x = rng.standard_normal((rows, D)) * 2.0 ** rng.integers(-20, 20, (rows, 1))
+    x[3] = 0.0                                      # all-zero row: the 1e-4 floor
+    x[4, :block] = 1.0 + 1.0 / 16                   # e4m3 ties once scaled by a power of two
+    xb = oracle.f32_to_bf16(x.astype(np.float32))
+    codes, s = oracle.fp8_quant_rows(xb, block, ue8m0)
+    assert codes.shape == (rows, D) and s.shape == (rows, D // block) and s.dtype == np.float32
+    xf = oracle.bf16_to_f32(xb).reshape(rows, D // block, block)
+    amax = np.maximum(np.abs(xf).max(-1), np.float32(1e-4))
+    if ue8m0:
+        m, _ = np.frexp(s)
+        assert (m == 0.5).all()                     # powers of two
+        r = amax / s
+        assert (r > 224 * (1 - 2.0 ** -20)).all() and (r <= 448 * (1 + 2.0 ** -20)).all()
+    else:
+        np.testing.assert_array_equal(s, (amax * np.float32(1 / np.float32(448))).astype(np.float32))
+    # the codes are torch's cast of the clipped, scaled rows
+    y = np.clip((xf / s[..., None]).astype(np.float32), -448, 448)
+    np.testing.assert_array_equal(codes.reshape(rows, D // block, block), _torch_e4m3(y))
+    # the element of largest magnitude lands in the top binade [256, 448]
+    big = np.abs(oracle.e4m3_decode(codes).reshape(rows, D // block, block)).max(-1)
+    live = np.abs(xf).max(-1) >= 1e-4
+    assert (big[live] >= 224).all() and (big[live] <= 448).all()
+    assert (codes[3] == 0).all()
+    # dequantisation with power-of-two scales is exact: value(code) * s lands on the e4m3 grid times s
+    if ue8m0:
+        c2 = codes.reshape(-1, block)
+        deq = oracle.bf16_to_f32(oracle.fp8_dequant_rows(c2, s.reshape(-1)))
+        exact = [float(v) * float(sc) for v, sc in zip(oracle.e4m3_decode(c2).ravel(), np.repeat(s.ravel(), block))]
+        np.testing.assert_array_equal(deq.ravel().astype(np.float64), np.array(exact))

@@ -1,6 +1,6 @@
 """Benchmark of the KernelSwift operators on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,1,3,4,5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 2,1,3,4,5,mhc,fp8] [--no-cpu] [--no-dropin]
 
 Headline (the JSON "value"): BASELINE.json configs[1] = config 2, the indexer at S_q=128, S_kv=4096,
 64 heads, top-512: one step = one fused indexer call (RoPE of q and k + row statistics, exact MFMA
@@ -18,7 +18,9 @@ cpu_baseline: the torch-CPU op-for-op restatement of the reference baseline (ora
 kind "port") timed on this host's cores over a bounded sample of the same workload.
 
 The other configs (Sinkhorn, sparse attention prefill, indexer long, MLA decode) are measured the same
-way and reported under "per_config".
+way and reported under "per_config", with two rows beyond the BASELINE.json configs: "mhc" (the mHC
+residual update with the Sinkhorn fused in, HBM-bound) and "fp8" (the indexer on e4m3 rows at config 2's
+shape, with the HBM-bound quantiser as its roofline).
 """
 from __future__ import annotations
 
@@ -41,7 +43,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--configs", type=str, default="2,1,3,4,5,mhc")
+    p.add_argument("--configs", type=str, default="2,1,3,4,5,mhc,fp8")
     p.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     p.add_argument("--no-dropin", action="store_true", help="skip the ModelNew rows at the reference example shapes")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget per CPU baseline sample")
@@ -435,6 +437,69 @@ def run_mhc(steps, warmup, do_cpu, cpu_budget, N=4096, C=4096, iters=20):
     return res_d
 
 
+def run_fp8(steps, warmup, do_cpu, cpu_budget):
+    """The indexer on FP8 rows (dtype = "fp8", scale_fmt = "ue8m0"; baseline/indexer.py:14-17) at config 2's shape:
+    q and k rotated, then quantised to e4m3 with one power-of-two scale per row (the cache-write side, timed
+    as ks_fp8_quant_rows), and the indexer call on the codes (dequantisation + statistics pass, bounded scores,
+    exact top-k).  The quantiser is HBM-bound: its roofline is GB/s of bf16 read + codes and scales written."""
+    import torch
+    from kernelswift_amd import _lib, ops, workloads
+    w = workloads.CONFIGS[2]("cuda")
+    t, p = w.tensors, w.params
+    B, S, H, D = t["q"].shape
+    T = t["k"].shape[1]
+    qr, kr = t["q"].clone(), t["k"].clone()
+    ops.rope_inplace(qr, t["freqs"], rope_start=0, pos0=p["start_pos"])
+    ops.rope_inplace(kr, t["freqs"], rope_start=0, pos0=0)
+    qc, qs = ops.fp8_quant(qr, D, True)
+    kc, ks_ = ops.fp8_quant(kr, D, True)
+    qs, ks_ = qs[..., 0].contiguous(), ks_[..., 0].contiguous()
+    tops = _lib.torch_ops()
+
+    def step():
+        return tops.indexer_fp8(qc, qs, kc, ks_, t["w"], p["k_top"], True, p["start_pos"], 1, 0, False, None)
+
+    dev_med, dev_mean = _events_median(step, steps, warmup)
+    wall_med, ms_step = _wall(step, steps, warmup)
+    # the quantiser timed alone (outputs preallocated, launched through the C ABI): q rows, the larger launch
+    lib = _lib.load()
+    qc2, qs2 = torch.empty_like(qc), torch.empty(B * S * H, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def quant_q():
+        _lib.check(lib.ks_fp8_quant_rows(qr.data_ptr(), B * S * H, D, D, 1, qc2.data_ptr(), qs2.data_ptr(), stream),
+                   "fp8 quant")
+
+    quant_us = _events_avg(quant_q, steps, warmup)
+    rows = B * S * H
+    qbytes = rows * D * 3 + rows * 4  # bf16 read, codes and scales written
+    gbs = qbytes / (quant_us * 1e-6) / 1e9
+    res = {"us_per_call": round(dev_med, 3), "us_per_call_mean": round(dev_mean, 3),
+           "wall_us_per_call_sync": round(wall_med, 3), "ms_per_step": ms_step,
+           "workload": f"config-2 shape on e4m3 rows (ue8m0 row scales): B={B} S_q={S} S_kv={T} H={H} D={D} "
+                       f"causal top-{p['k_top']}",
+           "kernels_us": {"fp8_quant_kernel (q rows)": round(quant_us, 3)},
+           "roofline": {"bound": "hbm", "kernel": "fp8_quant_kernel", "achieved": round(gbs, 1),
+                        "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                        "bytes_per_launch": qbytes}}
+    if do_cpu:
+        from oracle import torch_ref
+        torch.set_num_threads(_cpu_threads())
+        qcc, kcc = qc.cpu(), kc.cpu()
+        qsc, ksc, wc = qs.cpu(), ks_.cpu(), t["w"].cpu()
+
+        def cpu_call():
+            qd = (qcc.float() * qsc[..., None]).bfloat16()
+            kd = (kcc.float() * ksc[..., None]).bfloat16()
+            return torch_ref.indexer(qd, kd, wc, None, p["k_top"], True, p["start_pos"], 1, 0, 0, 0, False)
+
+        ms, reps = _cpu_time(cpu_call, cpu_budget)
+        res["cpu_baseline"] = {"value": round(ms * 1e3, 1), "unit": "us/call", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"full call (dequantisation + torch-CPU op sequence of "
+                                                         f"baseline/indexer.py without RoPE), median of {reps}"}
+    return res
+
+
 def run_dropin(steps, warmup):
     """ModelNew at the reference's own example shapes (baseline/*.py get_inputs), timed like the reference
     harness (perf_counter + synchronize per call, median): context beside BASELINE.md's published numbers,
@@ -466,7 +531,7 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.set_device(0)
-    cfgs = [c if c == "mhc" else int(c) for c in args.configs.split(",") if c]
+    cfgs = [c if c in ("mhc", "fp8") else int(c) for c in args.configs.split(",") if c]
     per = {}
     for c in cfgs:
         if c in (2, 4):
@@ -477,6 +542,8 @@ def main():
             per[c] = run_sparse(c, args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
         elif c == "mhc":
             per[c] = run_mhc(args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
+        elif c == "fp8":
+            per[c] = run_fp8(args.steps, args.warmup, not args.no_cpu, args.cpu_seconds)
         print(f"[bench] config {c}: {json.dumps(per[c])}", file=sys.stderr, flush=True)
     dropin = None
     if not args.no_dropin:

@@ -703,10 +703,42 @@ __global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float 
       if (n_unres) atomicAdd(&rc.stats[1], n_unres);
       if (rc.stats_ext && tid == 0) atomicAdd(&rc.stats[2], ncand);
     }
-    // ---- exact selection; hist[0] was cleared by the second pass above
-    if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
-    __syncthreads();
-    select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh, c0, slice_out);
+    // ---- the selection.  Every column of the top k has an exact key >= tau, and every key >= tau is exact (a
+    // bounded score whose upper end reaches tau was recomputed; the others enter below tau).  When at most
+    // Pk (the sort's capacity) keys reach tau they are collected and sorted directly, without the radix
+    // select: the whole row needs at least k_sel of them (it always has them); a slice emits the ones it
+    // has, at most k_sel, and pads its list with absent composites (0), which the merge ranks last.
+    uint32_t nge = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) nge += (key[j] != 0u && key[j] >= tau) ? 1u : 0u;
+    const uint32_t ge_pos = block_inclusive_scan(nge, sh.wsum) - nge;
+    uint32_t n_ge = 0;
+    for (int w = 0; w < kTopkWaves; ++w) n_ge += sh.wsum[w];
+    int Pk = 128;
+    while (Pk < k) Pk <<= 1;
+    const bool direct = n_ge <= static_cast<uint32_t>(Pk) && (slice_out != nullptr || n_ge >= static_cast<uint32_t>(k_sel));
+    if (direct) {  // uniform
+      uint32_t pos = ge_pos;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if (key[j] != 0u && key[j] >= tau) {
+          const uint32_t col = static_cast<uint32_t>(c0 + j * kTopkThreads + tid);
+          cand[pos++] = (static_cast<uint64_t>(key[j]) << 32) | static_cast<uint64_t>(~col);
+        }
+      }
+      __syncthreads();
+      const int n_emit = static_cast<int>(n_ge) < k_sel ? static_cast<int>(n_ge) : k_sel;
+      int P = 128;
+      while (P < static_cast<int>(n_ge)) P <<= 1;
+      sort_merge_store(cand, P, static_cast<int>(n_ge), n_emit, row, k, out, out_i64, causal, limit, offset, slice_out);
+      if (slice_out != nullptr)
+        for (int e = n_emit + tid; e < k_sel; e += kTopkThreads) slice_out[e] = 0ull;
+    } else {
+      // hist[0] was cleared by the second pass above
+      if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
+      __syncthreads();
+      select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh, c0, slice_out);
+    }
   }
 
   // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order); the merge

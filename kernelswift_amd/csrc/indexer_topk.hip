@@ -334,6 +334,147 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
 }
 
+// ---------------------------------------------------------------- short rows: one wave per row
+// Rows of at most 1024 columns with k <= 128 (the drop-in indexer's compressed rows: 650 columns, k = 128):
+// a 1024-lane workgroup per row spends its time in barriers, so here every wave owns a row and no barrier
+// is used.  Lane l holds columns 64 j + l (j < KPT).  The k-th largest key comes from four 8-bit radix
+// passes through the wave's own 256-bin LDS histogram (a wave scan over the bins finds the bucket); keys
+// above it are collected with ballots, keys equal to it in column order (j, then lane) up to the count
+// needed; the k winners are then sorted as composites (key, ~column) by the in-register bitonic network
+// of 128 (two per lane) and stored with the post-processing: the order of topk_rows_kernel.
+constexpr int kWaveRows = kTopkThreads / 64;  // rows per workgroup
+
+__device__ __forceinline__ void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t b) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b), 0u));
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void topk_wave_kernel(const float *__restrict__ scores, int64_t ld,
+                                                                int64_t rows, int64_t S, int T, int k, int causal,
+                                                                int64_t start_pos, int ratio, int64_t offset,
+                                                                void *__restrict__ out, int out_i64) {
+  __shared__ uint32_t hist[kWaveRows][256];
+  __shared__ uint64_t cand[kWaveRows][128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaveRows + wave;
+  if (row >= rows) return;  // uniform per wave; the kernel has no barrier
+  const int64_t s = row % S;
+  int64_t limit = INT64_MAX;
+  int n_valid = T;
+  if (causal) {
+    limit = (start_pos + s + 1) / ratio;
+    n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
+  }
+  const int k_sel = k < n_valid ? k : n_valid;
+  const float *src = scores + row * ld;
+  float f[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {  // every load before the first wait (column 0 stands in past the prefix)
+    const int col = 64 * j + lane;
+    f[j] = src[col < n_valid ? col : 0];
+  }
+  uint32_t key[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) key[j] = 64 * j + lane < n_valid ? score_key(f[j]) : 0u;
+  if (k_sel > 0) {  // uniform
+    uint32_t *h = hist[wave];
+    uint32_t prefix = 0, mask = 0, k_rem = static_cast<uint32_t>(k_sel), eq_total = 0;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) h[64 * i + lane] = 0u;
+      wave_lds_order();
+#pragma unroll
+      for (int j = 0; j < KPT; ++j)
+        if (key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&h[(key[j] >> shift) & 255u], 1u);
+      wave_lds_order();
+      // lane l owns bins 255 - 4l .. 252 - 4l: a lane-order inclusive scan is a suffix sum from the top bin
+      uint32_t c[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) c[i] = h[255 - 4 * lane - i];
+      wave_lds_order();  // the next pass clears the bins after these reads
+      const uint32_t mine = c[0] + c[1] + c[2] + c[3];
+      const uint32_t incl = wave_incl_scan(mine);
+      const uint32_t excl = incl - mine;
+      const bool here = excl < k_rem && incl >= k_rem;
+      uint32_t digit = 0, rem = 0, cnt = 0;
+      if (here) {
+        uint32_t acc = excl;
+        bool found = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (!found && acc + c[i] >= k_rem) {
+            digit = static_cast<uint32_t>(255 - 4 * lane - i);
+            rem = k_rem - acc;
+            cnt = c[i];
+            found = true;
+          }
+          acc += c[i];
+        }
+      }
+      const int src_lane = __builtin_ctzll(__builtin_amdgcn_ballot_w64(here));
+      digit = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(digit), src_lane));
+      rem = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rem), src_lane));
+      cnt = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(cnt), src_lane));
+      prefix |= digit << shift;
+      mask |= 255u << shift;
+      k_rem = rem;
+      eq_total = cnt;
+    }
+    const uint32_t kstar = prefix;  // >= 1: the k_sel-th of nonzero keys
+    const uint32_t take_eq = k_rem, n_gt = static_cast<uint32_t>(k_sel) - take_eq;
+    (void)eq_total;
+    uint64_t *cw = cand[wave];
+    uint32_t base_gt = 0, base_eq = 0;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool gt = key[j] > kstar, eq = key[j] == kstar;
+      const uint64_t bg = __builtin_amdgcn_ballot_w64(gt), be = __builtin_amdgcn_ballot_w64(eq);
+      const uint32_t col = static_cast<uint32_t>(64 * j + lane);
+      if (gt) cw[base_gt + lanes_below(bg)] = (static_cast<uint64_t>(key[j]) << 32) | static_cast<uint64_t>(~col);
+      const uint32_t re = base_eq + lanes_below(be);
+      if (eq && re < take_eq) cw[n_gt + re] = (static_cast<uint64_t>(kstar) << 32) | static_cast<uint64_t>(~col);
+      base_gt += static_cast<uint32_t>(__builtin_popcountll(bg));
+      base_eq += static_cast<uint32_t>(__builtin_popcountll(be));
+    }
+    wave_lds_order();
+    uint64_t v[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int e = r * 64 + lane;
+      v[r] = e < k_sel ? cw[e] : 0ull;
+    }
+    run_sort<2>(v, lane);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int e = r * 64 + lane;
+      if (e < k_sel) {
+        const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[r] & 0xFFFFFFFFull));
+        store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+      }
+    }
+  }
+  // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order)
+  for (int j = k_sel + lane; j < k; j += 64)
+    store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
+}
+
+template <int KPT>
+int launch_topk_wave(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
+                     int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream) {
+  hipLaunchKernelGGL(topk_wave_kernel<KPT>, dim3(static_cast<unsigned>(ceil_div(rows, kWaveRows))),
+                     dim3(kTopkThreads), 0, stream, scores, ld, rows, S, T, k, causal, start_pos, ratio, offset, out,
+                     out_i64);
+  KS_CHECK_LAUNCH("topk_wave_kernel");
+  return KS_OK;
+}
+
 template <int KPT>
 int launch_topk(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal, int64_t start_pos,
                 int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream) {
@@ -909,6 +1050,13 @@ extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
   const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
+  if (T <= 1024 && k <= 128) {  // short rows: one wave per row
+    if (T <= 64) return ks::launch_topk_wave<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+    if (T <= 128) return ks::launch_topk_wave<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+    if (T <= 256) return ks::launch_topk_wave<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+    if (T <= 512) return ks::launch_topk_wave<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+    return ks::launch_topk_wave<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+  }
   if (T <= 1024) return ks::launch_topk<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   if (T <= 2048) return ks::launch_topk<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   if (T <= 4096) return ks::launch_topk<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);

@@ -59,6 +59,22 @@ def test_topk_all_equal_neg_inf_and_zeros(device):
     _check(s, 2999)
 
 
+@pytest.mark.parametrize("T,k", [(1000, 128), (64, 64), (65, 1), (513, 97)])
+def test_topk_short_rows_ties_and_neg_inf(device, T, k):
+    # the one-wave-per-row path (T <= 1024, k <= 128): all -inf rows, +0/-0 ties, a single finite value,
+    # alternating duplicates, rows of few distinct values, and more rows than one workgroup holds
+    s = torch.full((3, 7, T), -float("inf"), device=device)
+    s[0, 1] = 1.0
+    s[0, 2, : T // 3] = 0.0
+    s[0, 2, T // 3: 2 * T // 3] = -0.0
+    s[0, 3, ::2] = 2.0
+    s[1, 4, T - 1] = 5.0
+    g = torch.Generator(device=device).manual_seed(T)
+    s[2] = torch.round(torch.randn(7, T, device=device, generator=g))
+    _check(s.contiguous(), k)
+    _check(s.contiguous(), k, causal=True, start_pos=3, ratio=2, offset=9)
+
+
 def test_topk_causal_limits_and_garbage_padding(device):
     # causal rows with limits below k (outputs -1), garbage beyond the limit must be ignored
     S, T = 40, 650

@@ -46,18 +46,20 @@ static_assert(4 * kEntCap <= 255, "list entries hold the (entry, group) pair in 
 constexpr int kDotCap = 256;  // near-tie dots listed at a time per wave
 
 // Context of one key whose score depends on a near-tie dot: for the four head groups, the relu'd bf16
-// values of the two interval ends (packed pairs; they differ exactly at the near-tie slots).
+// values of the two interval ends (packed pairs, 2 HT per group; they differ exactly at the near-tie slots).
+// Sized by the head count, so that fewer heads leave LDS for a second workgroup per CU.
+template <int HT>
 struct alignas(16) KeyEntry {
-  uint32_t pl[4][8];
-  uint32_t ph[4][8];
+  uint32_t pl[4][2 * HT];
+  uint32_t ph[4][2 * HT];
   int32_t key;
   int32_t pad[3];
 };
 
-template <int KD>
+template <int KD, int HT>
 struct ScoresLds {
   uint4 k[kKR * KD / 8];             // swizzled key block of this workgroup (KD / 8 16-byte chunks per key)
-  KeyEntry ent[kQW][kEntCap];
+  KeyEntry<HT> ent[kQW][kEntCap];
   uint32_t dots[kQW][kDotCap];       // near-tie dots: head << 24 | key row << 16 | pair << 4 | slot,
                                      // pair = 4 entry + group
   int32_t kspan[kKR];                // row statistics of the key block and of each wave's query rows, for
@@ -81,7 +83,7 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
 
 // Near-tie slot bits (16 per head group) of an entry: positions where the two interval ends differ.
 template <int HT>
-__device__ __forceinline__ uint32_t entry_mask(const KeyEntry &en, int gg) {
+__device__ __forceinline__ uint32_t entry_mask(const KeyEntry<HT> &en, int gg) {
   uint32_t m = 0;
 #pragma unroll
   for (int p = 0; p < 2 * HT; ++p) {
@@ -94,10 +96,10 @@ __device__ __forceinline__ uint32_t entry_mask(const KeyEntry &en, int gg) {
 
 // Exact recomputation of the deferred near-tie dots of one wave, then of the affected scores.
 template <int HT, int KD, bool WBF>
-__device__ void flush_entries(ScoresLds<KD> &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
+__device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
                               int64_t qrow0, float *orow, int64_t limit, int T, int kb0, const float (&wv)[HT][4],
                               uint32_t &n_exact, uint32_t &n_unres) {
-  KeyEntry *E = L.ent[wave];
+  KeyEntry<HT> *E = L.ent[wave];
   uint32_t *D = L.dots[wave];
   const int g = lane >> 4, l16 = lane & 15;
   // 1. near-tie masks of the (entry, group) pairs, pair = 4 * entry + group; taken before any patching
@@ -270,7 +272,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
   static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
-  __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD>, ScoresLds<KD>> L;
+  __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD>, ScoresLds<KD, HT>> L;
   // the wave index is uniform per wave; readfirstlane lets the compiler keep the query row, the causal limit
   // and the tile loop in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -293,6 +295,20 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   const bool s_ok = s < S;
   const int64_t kbrow0 = b * kbs;        // first key row of batch b
   const int64_t krow0 = kbrow0 + kb0;    // first key row of this workgroup
+  // A workgroup whose queries all see none of its keys (causal limits at or below the block; the last query
+  // has the largest limit) only writes the mask: no staging, no statistics (uniform over the workgroup, so
+  // every wave leaves before the barrier).  Its key block's norm maximum is then read by no query.
+  if (causal) {
+    const int64_t s_last = static_cast<int64_t>(qgrp) * kQW + kQW - 1 < S - 1 ? static_cast<int64_t>(qgrp) * kQW + kQW - 1
+                                                                             : S - 1;
+    if ((start_pos + s_last + 1) / ratio <= kb0) {
+      if (s_ok) {
+        float *orow_m = scores + (b * S + s) * T;
+        for (int i = lane; i < nk; i += 64) orow_m[kb0 + i] = -INFINITY;
+      }
+      return;
+    }
+  }
 
   // Every prologue load is issued before the first wait (loads complete in order, so each later wait is a
   // partial one): the key statistics and this wave's query statistics and head weights, then the key
@@ -506,7 +522,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
         // defer the keys holding a near-tie dot: save all four groups' interval ends
         if ((km >> l16) & 1u) {
           const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
-          KeyEntry &en = L.ent[wave][e];
+          KeyEntry<HT> &en = L.ent[wave][e];
 #pragma unroll
           for (int p = 0; p < 2 * HT; ++p) {
             en.pl[g][p] = pl[p];

@@ -171,8 +171,6 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
   constexpr int QJ = Sh::QJ, QREG = Sh::QREG, QL = Sh::QL;  // k-steps of the QK MFMA
   constexpr int CT = DV / 16;   // dv column tiles
   constexpr int UPR = Sh::UPR, NJ = Sh::NJ;
-  constexpr int kQB = QJ <= 4 ? QJ : 1;  // QK k-steps whose K fragments are read together (registers allowing)
-  constexpr int kPV = CT <= 8 ? CT : 1;  // dv column tiles whose V fragments are read together
   __shared__ __attribute__((aligned(16))) uint16_t kb[Sh::GROUPS][2][Sh::BUF];
   __shared__ __attribute__((aligned(16))) uint4 qs[Sh::GROUPS][GW][QL > 0 ? QL : 1][64];
 
@@ -285,42 +283,19 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
       nvraw = raw_idx(c2, lane & 31);
     }
     const uint16_t *kbp = kb[grp][buf];
-    // ---- S^T = K Q^T for the chunk's two 16-key tiles.  The K fragments of kQB k-steps of both tiles are
-    // read from LDS together, ahead of their MFMAs (one LDS latency per batch, not one per MFMA)
-    f32x4_t st[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+    // ---- S^T = K Q^T for the chunk's two 16-key tiles
+    f32x4_t st[2];
 #pragma unroll
-    for (int j0 = 0; j0 < QJ; j0 += kQB) {
-      uint4 kf[2][kQB];
+    for (int t = 0; t < 2; ++t) {
+      st[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int jj = 0; jj < kQB; ++jj)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          constexpr int kPat = Sh::SW / 4;  // distinct (4j mod SW) patterns
-          const int j = j0 + jj < QJ ? j0 + jj : QJ - 1;
-          kf[t][jj] = *reinterpret_cast<const uint4 *>(kbp + qk_off[t][j % kPat] + ((4 * j) & ~(Sh::SW - 1)) * 8);
-        }
-#pragma unroll
-      for (int jj = 0; jj < kQB; ++jj) {
-        const int j = j0 + jj;
-        if (j < QJ) {
-          const uint4 qb = j < QREG ? qf[j < QREG ? j : 0] : qs[grp][gw][j < QREG ? 0 : j - QREG][lane];
-#pragma unroll
-          for (int t = 0; t < 2; ++t) st[t] = mfma16(kf[t][jj], qb, st[t]);
-        }
+      for (int j = 0; j < QJ; ++j) {
+        constexpr int kPat = Sh::SW / 4;  // distinct (4j mod SW) patterns
+        const uint16_t *a = kbp + qk_off[t][j % kPat] + ((4 * j) & ~(Sh::SW - 1)) * 8;
+        st[t] = mfma16(*reinterpret_cast<const uint4 *>(a),
+                       j < QREG ? qf[j < QREG ? j : 0] : qs[grp][gw][j < QREG ? 0 : j - QREG][lane], st[t]);
       }
     }
-    // the V fragments of the first kPV dv column tiles are read now, so that their LDS latency passes under
-    // the softmax (they do not depend on it)
-    constexpr int kPat2 = Sh::SW / 2;  // distinct (2cc mod SW) patterns
-    auto v_frag = [&](int cc) {
-      const int hi = ((2 * cc) & ~(Sh::SW - 1)) * 8;
-      const uint2 b0 = lds_read_tr16(kbp + pv_off[0][cc % kPat2] + hi);
-      const uint2 b1 = lds_read_tr16(kbp + pv_off[1][cc % kPat2] + hi);
-      return make_uint4(b0.x, b0.y, b1.x, b1.y);
-    };
-    uint4 vf[kPV];
-#pragma unroll
-    for (int i = 0; i < kPV; ++i) vf[i] = v_frag(i);
     // ---- online softmax (lane: head l16, keys 16t + 4g + r)
     const uint32_t vbits = vm_cur >> (4 * g);  // bit 16t + r: key 16t + 4g + r
     float sc[8];
@@ -359,21 +334,13 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
     // ---- O += P V: V fragment of keys 16h + 4g + (l16 >> 2), dv columns 16cc + 4(l16 & 3) .. +3
     const uint4 pa = make_uint4(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                                 pack_bf16x2(p[6], p[7]));
-    // column tiles in batches of kPV: the next batch's V fragments are read ahead of this batch's MFMAs
 #pragma unroll
-    for (int c0 = 0; c0 < CT; c0 += kPV) {
-      uint4 vn[kPV];
-      if (c0 + kPV < CT) {
-#pragma unroll
-        for (int i = 0; i < kPV; ++i) vn[i] = v_frag(c0 + kPV + i < CT ? c0 + kPV + i : CT - 1);
-      }
-#pragma unroll
-      for (int i = 0; i < kPV; ++i)
-        if (c0 + i < CT) o[c0 + i] = mfma16(pa, vf[i], o[c0 + i]);
-      if (c0 + kPV < CT) {
-#pragma unroll
-        for (int i = 0; i < kPV; ++i) vf[i] = vn[i];
-      }
+    for (int cc = 0; cc < CT; ++cc) {
+      constexpr int kPat = Sh::SW / 2;  // distinct (2cc mod SW) patterns
+      const int hi = ((2 * cc) & ~(Sh::SW - 1)) * 8;
+      const uint2 b0 = lds_read_tr16(kbp + pv_off[0][cc % kPat] + hi);
+      const uint2 b1 = lds_read_tr16(kbp + pv_off[1][cc % kPat] + hi);
+      o[cc] = mfma16(pa, make_uint4(b0.x, b0.y, b1.x, b1.y), o[cc]);
     }
     // this wave's part of chunk c + 1 has landed (the DMA counts as a vector-memory load); with several
     // waves per group, a barrier then publishes everyone's part and releases buffer `buf` for refilling.

@@ -262,7 +262,7 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
                        "topk_rows_kernel (plain, other shapes)": round(topk_us, 3)},
         "roofline": {"bound": "mfma", "kernel": "indexer_scores_kernel (bounded)", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true>@cfg{cfg}")},
+                     "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true>@{cfg}")},
         # the product's bounded top-k reads a score and a bound (8 B) per column; the plain one 4 B
         "topk_bounded_GBps": round(S * T * 8 / (topkb_us * 1e-6) / 1e9, 1),
         "topk_plain_GBps": round(S * T * 4 / (topk_us * 1e-6) / 1e9, 1),
@@ -324,7 +324,7 @@ def run_sinkhorn(steps, warmup, do_cpu, cpu_budget):
            "kernels_us": {"sinkhorn4x4_kernel": round(kus, 3)},
            "roofline": {"bound": "hbm", "kernel": "sinkhorn4x4_kernel", "achieved": round(achieved, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                        "traffic": _traffic("sinkhorn4x4_kernel@cfg1"), "cache": "warm (2 MiB fits in L2)"},
+                        "traffic": _traffic("sinkhorn4x4_kernel@1"), "cache": "warm (2 MiB fits in L2)"},
            "size_sweep_matrices": sweep, "repeat20_kernel_us": round(kus20, 3),
            "ctypes_us_per_call": round(ct_med, 3), "host_issue_us_per_call": host}
     if do_cpu:
@@ -369,7 +369,7 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
                         + " (+ combine)", "achieved": round(achieved, 2),
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                         "traffic": _traffic(("sparse_attn_kernel<128, 128, 1>" if cfg == 3
-                                             else "sparse_attn_mla_kernel<4, 3>") + f"@cfg{cfg}"),
+                                             else "sparse_attn_mla_kernel<4, 3>") + f"@{cfg}"),
                         "cache": ("warm (the 2 MiB kv fits in L2)" if cfg == 3
                                   else "kv 2.25 GiB: gathered rows come from HBM")},
            "gathered_GBps": round(gathered / (op_us * 1e-6) / 1e9, 1)}
@@ -419,7 +419,7 @@ def run_mhc(steps, warmup, do_cpu, cpu_budget, N=4096, C=4096, iters=20):
              "kernels_us": {"mhc_post_kernel (Sinkhorn fused)": round(post_us, 3), "mhc_pre_kernel": round(pre_us, 3)},
              "roofline": {"bound": "hbm", "kernel": "mhc_post_kernel", "achieved": round(gbs, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                          "bytes_per_launch": post_bytes},
+                          "bytes_per_launch": post_bytes, "traffic": _traffic("mhc_post_kernel@mhc")},
              "pre_GBps": round(pre_bytes / (pre_us * 1e-6) / 1e9, 1)}
     if do_cpu:
         from oracle import torch_ref
@@ -481,7 +481,8 @@ def run_fp8(steps, warmup, do_cpu, cpu_budget):
            "kernels_us": {"fp8_quant_kernel (q rows)": round(quant_us, 3)},
            "roofline": {"bound": "hbm", "kernel": "fp8_quant_kernel", "achieved": round(gbs, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                        "bytes_per_launch": qbytes}}
+                        "bytes_per_launch": qbytes,
+                        "traffic": _traffic("fp8_quant_kernel<16>@fp8 (quantiser, q rows)")}}
     if do_cpu:
         from oracle import torch_ref
         torch.set_num_threads(_cpu_threads())

@@ -29,7 +29,7 @@ struct IndexerWs {
   float *scores;
   float *bounds;  // per-score bounds of the bounded path
   float *kmax;    // per key block norm maxima of the bounded path
-  uint64_t *part;  // the split top-k's per-slice lists (rows too few to fill the GPU)
+  uint64_t *part;  // the bounded selection's lists, bucket counts and list lengths
   int64_t part_cap;
   size_t bytes;
 };
@@ -53,7 +53,8 @@ IndexerWs carve(void *base, int64_t B, int64_t S, int64_t H, int64_t D, int64_t 
   w.scores = reinterpret_cast<float *>(take(size_t(B * S * T) * 4));
   w.bounds = reinterpret_cast<float *>(take(size_t(B * S * T) * 4));
   w.kmax = reinterpret_cast<float *>(take(size_t(B * ((T + ks::kScoreKeyBlock - 1) / ks::kScoreKeyBlock)) * 4));
-  w.part_cap = ks::topk_bounded_part_capacity(B * S);
+  // the bounded selection's lists and counts (only shapes that can take the bounded path)
+  w.part_cap = (H == 64 && D == 128) ? ks::topk_bounded_part_capacity(B * S, T) : 0;
   w.part = reinterpret_cast<uint64_t *>(take(size_t(w.part_cap) * 8));
   w.bytes = off;
   return w;

@@ -154,12 +154,13 @@ int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, i
                           int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds = nullptr,
                           float *kmax = nullptr);
 
-// Sorted exact top-k of rows of bounded scores (the bound-emitting score kernel's output): selects with the
-// lower ends, recomputes exactly the scores that may reach the top k (interval test with the score
-// kernel's half-widths, exact double-precision dots for the near ties, canonical head sum), then runs the
-// exact selection.  q / k: the rotated rows and their statistics (64 heads, D = 128), w fp32 [B, S, 64].
+// Sorted exact top-k of rows of bounded scores (the bound-emitting score kernel's output): a threshold from the
+// lower ends, exact recomputation of the scores that may reach the top k (interval test with the score kernel's
+// half-widths, exact double-precision dots for the near ties, canonical head sum; written back with bound 0),
+// then a sort of the exact scores at or above the threshold.  q / k: the rotated rows and their statistics
+// (64 heads, D = 128), w fp32 [B, S, 64].
 struct TopkRecompute {
-  const float *bounds;
+  float *bounds;  // recomputed scores get bound 0
   const float *kmax;
   const uint16_t *q;
   const uint16_t *k;
@@ -172,17 +173,15 @@ struct TopkRecompute {
   float bound_c;
   uint32_t *stats;  // optional: [0] += exact dot recomputations, [1] += dots outside the exact range
   int stats_ext;    // with stats: [2] += recomputed scores
-  // optional: room for rows x slices x (k sorted composites + 2048 32-bit bucket counts).  With it, rows
-  // too few to fill the GPU are split into column slices, each selecting its own exact top k (candidates
-  // for recomputation taken against a threshold from the whole row's bucket counts, computed first); a
-  // merge kernel ranks the slices' lists.
+  // workspace of topk_bounded_part_capacity(rows, T) 64-bit slots: the rows' lists of exact scores at or above
+  // the threshold, the bucket counts of their column slices, the list lengths
   uint64_t *part;
   int64_t part_cap;  // 64-bit slots
 };
-// Slots the split selection needs for `rows` rows (k <= 2048): the workspace reserved for rc.part.
-int64_t topk_bounded_part_capacity(int64_t rows);
-int launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
-                                int causal, int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
+// Slots the bounded selection needs for `rows` rows of T <= 32768 columns (0 outside that range).
+int64_t topk_bounded_part_capacity(int64_t rows, int64_t T);
+int launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k, int causal,
+                                int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
                                 const TopkRecompute &rc, hipStream_t stream);
 
 }  // namespace ks

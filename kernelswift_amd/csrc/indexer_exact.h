@@ -127,44 +127,26 @@ __device__ __forceinline__ int64_t dpp_i64(int64_t v) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Exact dot product of two bf16 rows of length KD, rounded once to bf16 (RNE), for rows of any dynamic
-// range: a fixed-point integer accumulator whose bit i weighs 2^(i - 266).  Every bf16 value is m 2^l with
-// |m| < 2^8 and l >= -133, so every product is an integer multiple of 2^-266 below 2^256, and the sum of
-// 128 products stays below 2^540: 18 limbs of 30 bits, held in int64 so that carries can wait until the
-// end.  The PARTS (2 or 4) adjacent lanes of a group each add the products of KD / PARTS consecutive
-// elements (part = the lane's index in the group); DPP quad permutes sum the limbs.  qword(j) / kword(j)
-// return elements 2j and 2j + 1 of the rows packed in a uint32.  Slow (every product touches the limbs
-// through selects), and used only for dots whose spans exceed the double-precision paths.
-template <int KD, int PARTS, class QW, class KW>
-__device__ __attribute__((noinline)) uint16_t exact_dot_wide_bf16(QW qword, KW kword, int part) {
-  static_assert(PARTS == 2 || PARTS == 4, "pairs or quads of lanes");
-  constexpr int kNL = 18, kW = KD / 2 / PARTS;
-  int64_t L[kNL];
-#pragma unroll
-  for (int i = 0; i < kNL; ++i) L[i] = 0;
-#pragma unroll 1
-  for (int j = part * kW; j < (part + 1) * kW; ++j) {
-    const uint32_t qw = qword(j), kw = kword(j);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t a = h ? (qw >> 16) : (qw & 0xFFFFu), b = h ? (kw >> 16) : (kw & 0xFFFFu);
-      if ((a & 0x7FFFu) == 0u || (b & 0x7FFFu) == 0u) continue;
-      const int ea = static_cast<int>((a >> 7) & 0xFFu), eb = static_cast<int>((b >> 7) & 0xFFu);
-      const int64_t ma = static_cast<int64_t>((a & 0x7Fu) | (ea ? 0x80u : 0u));
-      const int64_t mb = static_cast<int64_t>((b & 0x7Fu) | (eb ? 0x80u : 0u));
-      const int o = (ea ? ea - 134 : -133) + (eb ? eb - 134 : -133) + 266;  // 0 .. 506
-      const int li = o / 30, sh = o - 30 * li;
-      const int64_t v = (((a ^ b) & 0x8000u) ? -(ma * mb) : ma * mb) * (int64_t(1) << sh);  // |v| < 2^46
-      const int64_t lo = v & 0x3FFFFFFF, hi = v >> 30;  // v = hi 2^30 + lo, 0 <= lo < 2^30
-#pragma unroll
-      for (int i = 0; i < kNL; ++i) L[i] += (i == li ? lo : 0) + (i == li + 1 ? hi : 0);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kNL; ++i) {
-    L[i] += dpp_i64<0xB1>(L[i]);                       // quad_perm [1, 0, 3, 2]: the pair
-    if constexpr (PARTS == 4) L[i] += dpp_i64<0x4E>(L[i]);  // quad_perm [2, 3, 0, 1]: the other pair
-  }
+// One product of bf16 values a, b (bit patterns) for the fixed-point accumulator below (bit i weighs
+// 2^(i - 266)): false for a zero product, else v = hi 2^30 + lo (0 <= lo < 2^30) to be added at limbs li, li + 1.
+__device__ __forceinline__ bool wide_product(uint32_t a, uint32_t b, int &li, int64_t &lo, int64_t &hi) {
+  if ((a & 0x7FFFu) == 0u || (b & 0x7FFFu) == 0u) return false;
+  const int ea = static_cast<int>((a >> 7) & 0xFFu), eb = static_cast<int>((b >> 7) & 0xFFu);
+  const int64_t ma = static_cast<int64_t>((a & 0x7Fu) | (ea ? 0x80u : 0u));
+  const int64_t mb = static_cast<int64_t>((b & 0x7Fu) | (eb ? 0x80u : 0u));
+  const int o = (ea ? ea - 134 : -133) + (eb ? eb - 134 : -133) + 266;  // 0 .. 506
+  li = o / 30;
+  const int sh = o - 30 * li;
+  const int64_t v = (((a ^ b) & 0x8000u) ? -(ma * mb) : ma * mb) * (int64_t(1) << sh);  // |v| < 2^46
+  lo = v & 0x3FFFFFFF;
+  hi = v >> 30;
+  return true;
+}
+
+// The fixed-point sum held in 18 limbs of 30 bits (bit i weighs 2^(i - 266); limbs may carry any int64 value)
+// rounded once to bf16 (RNE), +0 for an exact zero.
+__device__ __forceinline__ uint16_t limbs_to_bf16(int64_t (&L)[18]) {
+  constexpr int kNL = 18;
   auto normalize = [&]() {  // limbs 0..16 into [0, 2^30), the signed remainder in limb 17
 #pragma unroll
     for (int i = 0; i + 1 < kNL; ++i) {
@@ -202,6 +184,75 @@ __device__ __attribute__((noinline)) uint16_t exact_dot_wide_bf16(QW qword, KW k
   uint32_t bits = P - 7 >= 133 ? (static_cast<uint32_t>(P - 139) << 7) + kept - 128u : kept;
   if (bits >= 0x7F80u) bits = 0x7F80u;  // beyond the bf16 range: infinity
   return static_cast<uint16_t>((neg ? 0x8000u : 0u) | bits);
+}
+
+// Exact dot product of two bf16 rows of length KD, rounded once to bf16 (RNE), for rows of any dynamic
+// range: a fixed-point integer accumulator whose bit i weighs 2^(i - 266).  Every bf16 value is m 2^l with
+// |m| < 2^8 and l >= -133, so every product is an integer multiple of 2^-266 below 2^256, and the sum of
+// 128 products stays below 2^540: 18 limbs of 30 bits, held in int64 so that carries can wait until the
+// end.  The PARTS (2 or 4) adjacent lanes of a group each add the products of KD / PARTS consecutive
+// elements (part = the lane's index in the group); DPP quad permutes sum the limbs.  qword(j) / kword(j)
+// return elements 2j and 2j + 1 of the rows packed in a uint32.  Slow (every product touches the limbs
+// through selects), and used only for dots whose spans exceed the double-precision paths.
+template <int KD, int PARTS, class QW, class KW>
+__device__ __attribute__((noinline)) uint16_t exact_dot_wide_bf16(QW qword, KW kword, int part) {
+  static_assert(PARTS == 2 || PARTS == 4, "pairs or quads of lanes");
+  constexpr int kNL = 18, kW = KD / 2 / PARTS;
+  int64_t L[kNL];
+#pragma unroll
+  for (int i = 0; i < kNL; ++i) L[i] = 0;
+#pragma unroll 1
+  for (int j = part * kW; j < (part + 1) * kW; ++j) {
+    const uint32_t qw = qword(j), kw = kword(j);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int li;
+      int64_t lo, hi;
+      if (!wide_product(h ? (qw >> 16) : (qw & 0xFFFFu), h ? (kw >> 16) : (kw & 0xFFFFu), li, lo, hi)) continue;
+#pragma unroll
+      for (int i = 0; i < kNL; ++i) L[i] += (i == li ? lo : 0) + (i == li + 1 ? hi : 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kNL; ++i) {
+    L[i] += dpp_i64<0xB1>(L[i]);                       // quad_perm [1, 0, 3, 2]: the pair
+    if constexpr (PARTS == 4) L[i] += dpp_i64<0x4E>(L[i]);  // quad_perm [2, 3, 0, 1]: the other pair
+  }
+  return limbs_to_bf16(L);
+}
+
+
+// exact_dot_wide_bf16 of two rows of 128 elements computed by the whole wave, for kernels whose register budget
+// cannot hold the limbs in every lane: lane l adds the products of elements 2l and 2l + 1 into 18 int64 limbs of
+// wave-private LDS with 64-bit LDS atomics; the limbs are then read into wave-uniform values (scalar registers)
+// and rounded by limbs_to_bf16.  qword(j) / kword(j): elements 2j and 2j + 1 packed in a uint32 (j = lane).
+// Every lane of the wave must call it (the same dot); every lane receives the result.
+template <class QW, class KW>
+__device__ __forceinline__ uint16_t wave_exact_dot_wide_bf16(QW qword, KW kword, int64_t *limb) {
+  const int lane = static_cast<int>(__lane_id());
+  if (lane < 18) limb[lane] = 0;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint32_t qw = qword(lane), kw = kword(lane);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int li;
+    int64_t lo, hi;
+    if (!wide_product(h ? (qw >> 16) : (qw & 0xFFFFu), h ? (kw >> 16) : (kw & 0xFFFFu), li, lo, hi)) continue;
+    atomicAdd(reinterpret_cast<unsigned long long *>(&limb[li]), static_cast<unsigned long long>(lo));
+    atomicAdd(reinterpret_cast<unsigned long long *>(&limb[li + 1]), static_cast<unsigned long long>(hi));
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint64_t mine = lane < 18 ? static_cast<uint64_t>(limb[lane]) : 0ull;
+  int64_t L[18];
+#pragma unroll
+  for (int i = 0; i < 18; ++i) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(mine)), i));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(mine >> 32)), i));
+    L[i] = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+  }
+  return limbs_to_bf16(L);
 }
 
 }  // namespace

@@ -49,17 +49,17 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   return v;
 }
 
-// Inclusive prefix sum over the 1024 lanes of the block (lane order).  `wsum` is kTopkWaves ints of LDS.
+// Inclusive prefix sum over the NW waves of the block (lane order).  `wsum` is NW ints of LDS.
 // TRAIL: end with a barrier so that wsum may be rewritten at once; without it the caller must pass a
 // barrier before the next scan on the same wsum.
-template <bool TRAIL = true>
+template <bool TRAIL = true, int NW = kTopkWaves>
 __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t *wsum) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   v = wave_incl_scan(v);
   if (lane == 63) wsum[wave] = v;
   __syncthreads();
   uint32_t base = 0;
-  for (int w = 0; w < wave; ++w) base += wsum[w];
+  for (int w = 0; w < wave && w < NW; ++w) base += wsum[w];
   if constexpr (TRAIL) __syncthreads();
   return v + base;
 }
@@ -488,15 +488,59 @@ int launch_topk(const float *scores, int64_t ld, int64_t rows, int64_t S, int T,
 }
 
 
-// ---------------------------------------------------------------- rows of bounded scores
-// Inverse of score_key for keys of finite scores.
-__device__ __forceinline__ float key_score(uint32_t key) {
-  return __builtin_bit_cast(float, (key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
+// Histogram slices per row: enough workgroups for the 256 CUs, at most kTopkMaxSlices (the recomputation sums
+// that many bucket counts per row), at least 1024 columns each.
+constexpr int kTopkMaxSlices = 4;
+inline int topk_slices(int64_t rows, int T) {
+  if (rows >= 256) return 1;
+  int p = static_cast<int>((256 + rows - 1) / rows);
+  if (p > kTopkMaxSlices) p = kTopkMaxSlices;
+  while (p > 1 && T / p < kTopkThreads) --p;
+  return p;
 }
 
+// Capacity (composites) of a row's list of exact scores >= tau: the power of two >= T up to 8192 (a longer list
+// takes the whole-row fallback; k <= 2048 on this path, and the 11-bit threshold bucket can hold ~2000 more).
+constexpr int kTopkListCap = 8192;
+inline int topk_list_cap(int T) {
+  int c = 128;
+  while (c < T && c < kTopkListCap) c <<= 1;
+  return c;
+}
+
+// 64-bit workspace slots of the bounded selection: the rows' lists, their slices' bucket counts (2048 x 32 bits
+// each), the rows' states (list length, threshold, largest key: 4 x 32 bits).
+inline int64_t topk_bounded_slots(int64_t rows, int NP, int cap) { return rows * cap + rows * NP * 1024 + rows * 2; }
+
+// Wave-wide minimum and maximum (every lane receives both).
+__device__ __forceinline__ void wave_min_max(uint32_t &mn, uint32_t &mx) {
+#define KS_MM(S)                                             \
+  {                                                          \
+    const uint32_t a = lane_xor<S>(mn), b = lane_xor<S>(mx); \
+    mn = a < mn ? a : mn;                                    \
+    mx = b > mx ? b : mx;                                    \
+  }
+  KS_MM(1) KS_MM(2) KS_MM(4) KS_MM(8) KS_MM(16) KS_MM(32)
+#undef KS_MM
+}
+
+// ---------------------------------------------------------------- rows of bounded scores
+// Bounded scores S with bounds U (the exact score lies in [S - U, S + U]; U = 0 exactly when S is exact) are
+// selected in three launches:
+//  1. topk_slice_hist_kernel, workgroup (row, slice): counts of the first 11-bit digit (2048 buckets) of the lower
+//     ends S - U of the slice's columns.
+//  2. topk_recompute_kernel, workgroup (row, segment): the threshold tau from the row's summed counts (the lower
+//     edge of the bucket holding the row's k-th largest lower end, so no exact score of the top k lies below it);
+//     every score of the segment with U > 0 whose upper end reaches tau is recomputed exactly and written back
+//     (S = exact, U = 0); every exact score >= tau is appended to the row's list as a composite (key, ~column).
+//  3. topk_collected_kernel, one workgroup per row: the list holds every column of the top k, each with its exact
+//     score, so sorting it gives the top k.  A list longer than its capacity falls back to the exact selection over
+//     the whole row, whose keys are exact wherever they reach tau (the others enter as upper ends, below tau).
 constexpr int kRecD = 128;        // head dim of the recomputation
 constexpr int kRecH = 64;         // heads
 constexpr int kRecC = kRecD / 8;  // 16-byte chunks per row
+constexpr int kRecThreads = 512;  // the recomputation's workgroup
+constexpr int kRecWaves = kRecThreads / 64;
 
 // The row's query (64 heads) staged once per workgroup: rows in LDS with a 16-byte XOR swizzle (chunk c of
 // head h at c ^ (h & 15): the 16 lanes reading one chunk of 16 heads hit distinct banks), and the head
@@ -517,22 +561,24 @@ struct RecWave {
   uint4 k[16 * kRecC];
   int32_t ksp[16];         // the tile's key spans
   uint16_t ent[kNearCap];  // lane << 4 | head bit (4 m + r); overwritten by the dot's exact value
+  int64_t limb[18];        // the integer accumulator of the rare dots beyond the double-precision paths
 };
 
 // Exact scores of the keys list[0 .. n) of one row, by the canonical contract, written over the row's
-// scores (srow, the workspace copy the selection reads next).  Each wave takes tiles of 16 keys: four
+// scores (srow, with bound 0 in urow) and over the keys' list slots (bit patterns of the scores).  Each wave takes tiles of 16 keys: four
 // 16-head MFMA rounds (heads 16m + 4g + r, m = 0..3) with the score kernel's interval test (same
 // half-widths: bound_c 2^-23 ||q_h|| times the key block's norm maximum) keep the relu'd lower ends of all
 // 64 heads; the tile's near-tie dots are then recomputed exactly, 16 at a time with a quad of lanes per dot
 // (q_h and the key row from LDS: exact_dot_bf16's arithmetic), and the fp32 fma head sum runs in the
 // canonical order over the corrected values.
-__device__ void recompute_scores(int32_t *list, int n, float *srow, const TopkRecompute &rc,
+template <int NW>
+__device__ void recompute_scores(int32_t *list, int n, float *srow, float *urow, const TopkRecompute &rc,
                                  const RecShared &rs, RecWave &rw, int64_t kbrow0, int64_t kmax_row0,
                                  uint32_t &n_exact, uint32_t &n_unres) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int ntile = (n + 15) / 16;
-  for (int t = wave; t < ntile; t += kTopkWaves) {
+  for (int t = wave; t < ntile; t += NW) {
     const int li = 16 * t + l16;
     const bool kv = li < n;
     const int col = list[kv ? li : n - 1];
@@ -635,13 +681,19 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, const TopkRe
           uint16_t v;
           if (!split && (hi == 0.0 || (fabs(hi) >= 0x1p-126 && fabs(hi) < 0x1p127))) v = round_to_bf16_fast(hi);
           else v = round2_to_bf16(hi, lo);
-          if (span > 84) {
-            // wider still (the whole pair takes this branch): the integer accumulator, any range
-            v = exact_dot_wide_bf16<kRecD, 2>(
-                [&](int j) { return reinterpret_cast<const uint32_t *>(&rs.q[h * kRecC + ((j >> 2) ^ (h & 15))])[j & 3]; },
-                [&](int j) { return reinterpret_cast<const uint32_t *>(&rw.k[kl * kRecC + ((j >> 2) ^ kl)])[j & 3]; },
-                sub);
-            if (sub == 0 && b0 + dq < ns) ++n_unres;  // counted: dots that needed the integer accumulator
+          // wider still (rare): the integer accumulator, any range, one dot at a time by the whole wave (its limbs
+          // in LDS, so the recomputation's register budget does not carry them)
+          uint64_t wide = __builtin_amdgcn_ballot_w64(span > 84 && sub == 0 && b0 + dq < ns);
+          while (wide) {  // uniform
+            const int wl = __builtin_ctzll(wide);
+            wide &= wide - 1;
+            const int wh = __builtin_amdgcn_readlane(h, wl), wk = __builtin_amdgcn_readlane(kl, wl);
+            const uint16_t r = wave_exact_dot_wide_bf16(
+                [&](int j) { return reinterpret_cast<const uint32_t *>(&rs.q[wh * kRecC + ((j >> 2) ^ (wh & 15))])[j & 3]; },
+                [&](int j) { return reinterpret_cast<const uint32_t *>(&rw.k[wk * kRecC + ((j >> 2) ^ wk)])[j & 3]; },
+                rw.limb);
+            if (dq == (wl >> 1)) v = r;  // the pair that owns the dot
+            if (lane == wl) ++n_unres;   // counted: dots that needed the integer accumulator
           }
           const uint16_t rv = (v & 0x8000u) ? 0 : v;  // ReLU (also maps -0 to +0)
           // each pair reads only its own entry before this write (the value replaces the entry)
@@ -681,225 +733,21 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, const TopkRe
     // the tile's lanes read their list slots (and lanes past n read slot n - 1, of this same tile) before
     if (g == 0 && kv) {
       srow[col] = tot;
+      urow[col] = 0.f;
       list[li] = __builtin_bit_cast(int32_t, tot);
     }
   }
 }
 
-// One 1024-lane workgroup per row of bounded scores: lower ends lo = score - U select a threshold tau (the
-// bucket edge, two radix passes deep, of the k-th largest lo: no exact score of the k largest lies below
-// it); every score with U > 0 whose upper end reaches tau is recomputed exactly (in batches of the list
-// capacity); the row's keys then hold exact scores wherever they can matter, and the exact selection runs
-// on them.  A score with U > 0 whose upper end is below tau enters the selection as that upper end: below
-// tau, so below every exact score of the k largest, like the exact score itself.
-// Slice mode (part != null): workgroup (row, p) runs the same on columns [p W, p W + W) of the row and
-// writes its exact top k, sorted, as composites to part[(row P + p) k ..]: the row's top k is the top k of
-// the slices' lists (a column of the row's top k is in the top k of its slice).
-template <int KPT>
-__global__ __launch_bounds__(kTopkThreads) void topk_bounded_kernel(const float *scores, int64_t ld,
-                                                                   int64_t S, int T, int k, int causal,
-                                                                   int64_t start_pos, int ratio, int64_t offset,
-                                                                   void *__restrict__ out, int out_i64,
-                                                                   TopkRecompute rc, int lcap, int W,
-                                                                   uint64_t *__restrict__ part) {
-  extern __shared__ uint64_t cand[];  // the recomputation list first, then the selection's candidates
-  __shared__ SelShared sh;
-  __shared__ RecShared rs;
-  __shared__ RecWave rw[kTopkWaves];
-  const int64_t row = blockIdx.x;
-  const int64_t s = row % S, b = row / S;
-  const int tid = threadIdx.x;
-  int64_t limit = INT64_MAX;
-  int n_valid = T;
-  if (causal) {
-    limit = (start_pos + s + 1) / ratio;
-    n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
-  }
-  // the workgroup's columns: [c0, c0 + nv) of the row's valid prefix
-  const int c0 = static_cast<int>(blockIdx.y) * W;
-  const int nv = n_valid - c0 <= 0 ? 0 : (n_valid - c0 < W ? n_valid - c0 : W);
-  uint64_t *slice_out = part != nullptr ? part + (row * gridDim.y + blockIdx.y) * k : nullptr;
-  const int k_sel = k < nv ? k : nv;
-  const float *src = scores + row * ld + c0;
-  const float *ub = rc.bounds + row * ld + c0;
-
-  // the recomputation's query (64 heads) with its weights and statistics, staged in LDS: issued with the
-  // score loads (one round trip for both) although the candidates are known only after the threshold (one
-  // 16-byte q chunk per thread; every thread writes head entry tid % 64, identical writes)
-  {
-    static_assert(kRecH * kRecC == kTopkThreads, "one q chunk per thread");
-    const int64_t qrow0 = row * kRecH;  // rows of q, w and the q statistics: (b S + s) 64 + head
-    const int h = tid / kRecC, c = tid % kRecC, hh = tid & (kRecH - 1);
-    const uint4 qv = *reinterpret_cast<const uint4 *>(rc.q + (qrow0 + h) * kRecD + 8 * c);
-    const float wv = rc.w[qrow0 + hh], qnv = rc.qn[qrow0 + hh];
-    const int32_t qsv = rc.qsp[qrow0 + hh];
-    rs.q[h * kRecC + (c ^ (h & 15))] = qv;
-    rs.w[hh] = wv;
-    rs.qn[hh] = qnv;
-    rs.qsp[hh] = qsv;
-  }
-  // keys of the lower and upper ends (equal, and exact, where the bound is 0)
-  // every load is issued before the first wait: columns past the slice's valid part read its column 0 (in
-  // bounds: c0 < T) and are masked afterwards, so no load sits behind a branch
-  float sv[KPT], uv[KPT];
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const int col = j * kTopkThreads + tid;  // relative to c0
-    sv[j] = src[col < nv ? col : 0];
-    uv[j] = ub[col < nv ? col : 0];
-  }
-  uint32_t lok[KPT], hik[KPT];
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const bool v = j * kTopkThreads + tid < nv;
-    lok[j] = v ? score_key(uv[j] > 0.f ? sv[j] - uv[j] : sv[j]) : 0u;
-    hik[j] = v ? score_key(uv[j] > 0.f ? sv[j] + uv[j] : sv[j]) : 0u;
-  }
-  if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
-  for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;
-  __syncthreads();
-
-  if (k_sel > 0) {
-    // ---- tau: lower edge of the 22-bit bucket holding the k_sel-th largest lower end; a slice takes the
-    // lower edge of the 11-bit bucket holding its row's k-th largest lower end (from topk_slice_hist_kernel's
-    // counts), which no exact score of the row's top k lies below (hist[0], cleared above, then stays clear
-    // for the selection)
-    uint32_t tau;
-    if (slice_out != nullptr) {
-      // the row's first-digit histogram: the sum of its slices' (stored after the slices' lists); bucket
-      // scan as in radix_pass, for the row's k_sel-th largest lower end
-      const int k_row = k < n_valid ? k : n_valid;
-      const uint32_t *rh = reinterpret_cast<const uint32_t *>(part + static_cast<int64_t>(gridDim.x) * gridDim.y * k) +
-                           row * gridDim.y * 2048;
-      const int hi = 2047 - 2 * tid;  // two buckets per thread, scanned from the top
-      uint32_t c_hi = 0, c_lo = 0;
-      for (int p = 0; p < static_cast<int>(gridDim.y); ++p) {
-        c_hi += rh[p * 2048 + hi];
-        c_lo += rh[p * 2048 + hi - 1];
-      }
-      const uint32_t mine = c_hi + c_lo;
-      const uint32_t incl = block_inclusive_scan<false>(mine, sh.wsum);
-      const uint32_t excl = incl - mine;
-      const uint32_t kr = static_cast<uint32_t>(k_row);
-      if (excl < kr && incl >= kr) sh.digit = static_cast<uint32_t>(excl + c_hi >= kr ? hi : hi - 1);
-      __syncthreads();
-      tau = sh.digit << 21;
-    } else {
-      radix_pass<KPT>(lok, 0u, 0u, 21, 2048, sh, 0);
-      const uint32_t d1 = sh.digit;
-      radix_pass<KPT>(lok, d1 << 21, 0xFFE00000u, 10, 2048, sh, 1);
-      tau = (d1 << 21) | (sh.digit << 10);
-    }
-    // ---- scores to recompute: U > 0 and score + U >= tau; list ranks from a block scan
-    uint32_t cmask = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j)
-      if (lok[j] != hik[j] && hik[j] >= tau) cmask |= 1u << j;
-    const uint32_t cnt = __builtin_popcount(cmask);
-    const uint32_t base = block_inclusive_scan(cnt, sh.wsum) - cnt;
-    uint32_t ncand = 0;
-    for (int w = 0; w < kTopkWaves; ++w) ncand += sh.wsum[w];
-    int32_t *list = reinterpret_cast<int32_t *>(cand);
-    const int64_t kbrow0 = b * rc.kbs;
-    const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
-    float *srow = const_cast<float *>(scores + row * ld);
-    uint32_t n_exact = 0, n_unres = 0;
-    for (uint32_t b0 = 0; b0 < ncand; b0 += static_cast<uint32_t>(lcap)) {
-      const uint32_t nb = ncand - b0 < static_cast<uint32_t>(lcap) ? ncand - b0 : static_cast<uint32_t>(lcap);
-      uint32_t p = base, mm = cmask;
-      while (mm) {
-        const int j = __builtin_ctz(mm);
-        mm &= mm - 1;
-        if (p >= b0 && p < b0 + nb) list[p - b0] = c0 + j * kTopkThreads + tid;
-        ++p;
-      }
-      __syncthreads();
-      recompute_scores(list, static_cast<int>(nb), srow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0, n_exact, n_unres);
-      __syncthreads();  // the list is rewritten by the next batch; the recomputed scores are visible
-    }
-    // the selection's keys: recomputed scores from the row (the workgroup's waves share one L1: the
-    // barrier above orders the rewrites before these loads), exact scores where the bound is 0, and for
-    // the other bounded scores the upper end, which lies below tau like the score itself
-    // (the loads go out together: non-candidates read column c0, a broadcast, and keep their upper end);
-    // with a single batch every recomputed score is still in its list slot in LDS
-    float rsv[KPT];
-    if (ncand <= static_cast<uint32_t>(lcap)) {  // uniform
-      const float *listf = reinterpret_cast<const float *>(list);
-      uint32_t slot = base;
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        const bool cj = (cmask >> j) & 1u;
-        rsv[j] = cj ? listf[slot] : 0.f;
-        slot += cj ? 1u : 0u;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) rsv[j] = srow[c0 + (((cmask >> j) & 1u) ? j * kTopkThreads + tid : 0)];
-    }
-    uint32_t key[KPT];
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) key[j] = ((cmask >> j) & 1u) ? score_key(rsv[j]) : hik[j];
-    if (rc.stats != nullptr) {
-      if (n_exact) atomicAdd(&rc.stats[0], n_exact);
-      if (n_unres) atomicAdd(&rc.stats[1], n_unres);
-      if (rc.stats_ext && tid == 0) atomicAdd(&rc.stats[2], ncand);
-    }
-    // ---- the selection.  Every column of the top k has an exact key >= tau, and every key >= tau is exact (a
-    // bounded score whose upper end reaches tau was recomputed; the others enter below tau).  When at most
-    // Pk (the sort's capacity) keys reach tau they are collected and sorted directly, without the radix
-    // select: the whole row needs at least k_sel of them (it always has them); a slice emits the ones it
-    // has, at most k_sel, and pads its list with absent composites (0), which the merge ranks last.
-    uint32_t nge = 0;
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) nge += (key[j] != 0u && key[j] >= tau) ? 1u : 0u;
-    const uint32_t ge_pos = block_inclusive_scan(nge, sh.wsum) - nge;
-    uint32_t n_ge = 0;
-    for (int w = 0; w < kTopkWaves; ++w) n_ge += sh.wsum[w];
-    int Pk = 128;
-    while (Pk < k) Pk <<= 1;
-    const bool direct = n_ge <= static_cast<uint32_t>(Pk) && (slice_out != nullptr || n_ge >= static_cast<uint32_t>(k_sel));
-    if (direct) {  // uniform
-      uint32_t pos = ge_pos;
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        if (key[j] != 0u && key[j] >= tau) {
-          const uint32_t col = static_cast<uint32_t>(c0 + j * kTopkThreads + tid);
-          cand[pos++] = (static_cast<uint64_t>(key[j]) << 32) | static_cast<uint64_t>(~col);
-        }
-      }
-      __syncthreads();
-      const int n_emit = static_cast<int>(n_ge) < k_sel ? static_cast<int>(n_ge) : k_sel;
-      int P = 128;
-      while (P < static_cast<int>(n_ge)) P <<= 1;
-      sort_merge_store(cand, P, static_cast<int>(n_ge), n_emit, row, k, out, out_i64, causal, limit, offset, slice_out);
-      if (slice_out != nullptr)
-        for (int e = n_emit + tid; e < k_sel; e += kTopkThreads) slice_out[e] = 0ull;
-    } else {
-      // hist[0] was cleared by the second pass above
-      if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
-      __syncthreads();
-      select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh, c0, slice_out);
-    }
-  }
-
-  // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order); the merge
-  // writes it in slice mode
-  if (slice_out == nullptr)
-    for (int j = k_sel + tid; j < k; j += kTopkThreads)
-      store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
-}
-
-// First-digit histograms of a split row, computed before its slices run: workgroup (row, p) counts the top
-// 11 bits (2048 buckets) of the lower ends (score - U; the score itself where U = 0) of slice p's valid
-// columns and stores the counts.  Each slice of the row then sums the row's histograms and takes as its
-// recomputation threshold the lower edge of the bucket holding the row's k_sel-th largest lower end: no
-// exact score of the row's top k lies below it, and it lies far above a slice's own k-th largest (the
-// k-th of a quarter of the columns), so a slice recomputes far fewer candidates.
+// Workgroup (row, slice): counts of the first 11-bit digit (2048 buckets) of the lower ends (score - U; the score
+// itself where U = 0) of slice p's valid columns, stored for the recomputation's threshold.  Workgroup (row, 0)
+// also clears the row's list length and key maximum (the recomputation appends to the list after this launch).
 template <int KPT>
 __global__ __launch_bounds__(kTopkThreads) void topk_slice_hist_kernel(const float *scores, const float *bounds,
                                                                       int64_t ld, int64_t S, int T, int causal,
                                                                       int64_t start_pos, int ratio, int W,
-                                                                      uint32_t *__restrict__ hist_out) {
+                                                                      uint32_t *__restrict__ hist_out,
+                                                                      uint32_t *__restrict__ rstate) {
   __shared__ uint32_t hist[2048];
   const int64_t row = blockIdx.x;
   const int64_t s = row % S;
@@ -920,6 +768,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_slice_hist_kernel(const flo
     sv[j] = src[col < nv ? col : 0];
     uv[j] = ub[col < nv ? col : 0];
   }
+  if (blockIdx.y == 0 && tid == 0) {
+    rstate[4 * row] = 0u;
+    rstate[4 * row + 2] = 0u;
+  }
   for (int i = tid; i < 2048; i += kTopkThreads) hist[i] = 0;
   __syncthreads();
 #pragma unroll
@@ -934,17 +786,270 @@ __global__ __launch_bounds__(kTopkThreads) void topk_slice_hist_kernel(const flo
   for (int i = tid; i < 2048; i += kTopkThreads) dst[i] = hist[i];
 }
 
-// Merge of the (at most 4) slices' sorted lists into the row's top k: slices 0 + 1 and 2 + 3 merge into two
-// lists of at most k, which merge into the output.  One workgroup per row; all lists in LDS.
-__global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(const uint64_t *__restrict__ part, int W, int T,
-                                                                 int k, int64_t S, int causal, int64_t start_pos,
-                                                                 int ratio, int64_t offset, void *__restrict__ out,
-                                                                 int out_i64) {
-  extern __shared__ uint64_t lists[];  // [4][k] slice lists, then [2][k] pair merges
+// Workgroup (row, segment) of kRecThreads lanes over columns [c0, c0 + SW) of the row's valid prefix, SW =
+// kRecThreads KPB (column c0 + j kRecThreads + tid in slot j of thread tid):
+//  - tau: the row's NP bucket counts summed (thread t owns the kBPT buckets below 2048 - kBPT t), a block scan
+//    from the top bucket finds the bucket holding the row's k-th largest lower end; tau is its lower edge;
+//  - recomputation of the scores with U > 0 whose upper end reaches tau (recompute_scores), written back with
+//    U = 0;
+//  - every exact score >= tau of the segment is appended to the row's list (capacity cap composites) at a base
+//    taken from the row's length counter; the row state also receives tau and the largest key appended.
+// Row state (4 x 32 bits per row): list length, tau, largest key, unused.
+template <int KPB>
+__global__ __launch_bounds__(kRecThreads) void topk_recompute_kernel(float *scores, int64_t ld, int64_t S, int T,
+                                                                    int k, int causal, int64_t start_pos, int ratio,
+                                                                    TopkRecompute rc, int segs, int NP,
+                                                                    const uint32_t *__restrict__ hists,
+                                                                    uint64_t *__restrict__ lists, int cap,
+                                                                    uint32_t *__restrict__ rstate) {
+  constexpr int SW = kRecThreads * KPB;
+  __shared__ RecShared rs;
+  __shared__ RecWave rw[kRecWaves];
+  __shared__ int32_t list[SW];
+  __shared__ uint32_t wsum[kRecWaves];
+  __shared__ uint32_t s_tau, s_base;
+  const int64_t row = blockIdx.x / segs;
+  const int seg = static_cast<int>(blockIdx.x % segs);
+  const int64_t s = row % S, b = row / S;
+  const int tid = threadIdx.x;
+  int n_valid = T;
+  if (causal) {
+    const int64_t limit = (start_pos + s + 1) / ratio;
+    n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
+  }
+  const int k_row = k < n_valid ? k : n_valid;
+  const int c0 = seg * SW;
+  const int nv = n_valid - c0 <= 0 ? 0 : (n_valid - c0 < SW ? n_valid - c0 : SW);
+  if (k_row == 0 || nv == 0) return;  // uniform, before any barrier: no valid column here
+  float *srow = scores + row * ld;
+  float *urow = rc.bounds + row * ld;
+
+  // every load goes out before the first wait: the row's query chunks with its head data, the segment's scores
+  // and bounds (column c0 stands in past the valid part), and the row's bucket counts (slice 0 stands in for
+  // the slices past NP)
+  constexpr int kQPT = kRecH * kRecC / kRecThreads;  // q chunks per thread
+  constexpr int kBPT = 2048 / kRecThreads;           // buckets per thread (a multiple of 4)
+  static_assert(kQPT * kRecThreads == kRecH * kRecC && kBPT % 4 == 0, "chunks and buckets per thread");
+  const int64_t qrow0 = row * kRecH;  // rows of q, w and the q statistics: (b S + s) 64 + head
+  uint4 qv[kQPT];
+#pragma unroll
+  for (int i = 0; i < kQPT; ++i) {
+    const int idx = tid + i * kRecThreads, h = idx / kRecC, c = idx % kRecC;
+    qv[i] = *reinterpret_cast<const uint4 *>(rc.q + (qrow0 + h) * kRecD + 8 * c);
+  }
+  const int hh = tid & (kRecH - 1);
+  const float wv = rc.w[qrow0 + hh], qnv = rc.qn[qrow0 + hh];
+  const int32_t qsv = rc.qsp[qrow0 + hh];
+  float sv[KPB], uv[KPB];
+#pragma unroll
+  for (int j = 0; j < KPB; ++j) {
+    const int col = j * kRecThreads + tid;
+    sv[j] = srow[c0 + (col < nv ? col : 0)];
+    uv[j] = urow[c0 + (col < nv ? col : 0)];
+  }
+  uint4 hv[kTopkMaxSlices][kBPT / 4];
+  const uint32_t *hr = hists + row * NP * 2048 + (2048 - kBPT * (tid + 1));
+#pragma unroll
+  for (int p = 0; p < kTopkMaxSlices; ++p)
+#pragma unroll
+    for (int u = 0; u < kBPT / 4; ++u) hv[p][u] = *reinterpret_cast<const uint4 *>(hr + (p < NP ? p : 0) * 2048 + 4 * u);
+#pragma unroll
+  for (int i = 0; i < kQPT; ++i) {
+    const int idx = tid + i * kRecThreads, h = idx / kRecC, c = idx % kRecC;
+    rs.q[h * kRecC + (c ^ (h & 15))] = qv[i];
+  }
+  rs.w[hh] = wv;  // four threads write each head entry, the same values
+  rs.qn[hh] = qnv;
+  rs.qsp[hh] = qsv;
+
+  // ---- tau: bucket e of the thread's kBPT is 2048 - kBPT (tid + 1) + e (the top one is e = kBPT - 1)
+  uint32_t hc[kBPT];
+#pragma unroll
+  for (int e = 0; e < kBPT; ++e) hc[e] = 0u;
+#pragma unroll
+  for (int p = 0; p < kTopkMaxSlices; ++p) {
+    if (p < NP) {
+#pragma unroll
+      for (int u = 0; u < kBPT / 4; ++u) {
+        hc[4 * u] += hv[p][u].x;
+        hc[4 * u + 1] += hv[p][u].y;
+        hc[4 * u + 2] += hv[p][u].z;
+        hc[4 * u + 3] += hv[p][u].w;
+      }
+    }
+  }
+  uint32_t mine = 0;
+#pragma unroll
+  for (int e = 0; e < kBPT; ++e) mine += hc[e];
+  const uint32_t kr = static_cast<uint32_t>(k_row);
+  {
+    const uint32_t incl = block_inclusive_scan<true, kRecWaves>(mine, wsum);
+    const uint32_t excl = incl - mine;
+    if (excl < kr && incl >= kr) {  // exactly one thread: the row holds n_valid >= k_row nonzero lower ends
+      uint32_t acc = excl, bucket = 0;
+      bool found = false;
+#pragma unroll
+      for (int e = kBPT - 1; e >= 0; --e) {
+        acc += hc[e];
+        if (!found && acc >= kr) {
+          bucket = static_cast<uint32_t>(2048 - kBPT * (tid + 1) + e);
+          found = true;
+        }
+      }
+      s_tau = bucket << 21;
+    }
+  }
+  __syncthreads();
+  const uint32_t tau = s_tau;
+  if (seg == 0 && tid == 0) rstate[4 * row + 1] = tau;
+
+  // ---- the segment's candidates (U > 0, upper end >= tau) and its exact keys >= tau
+  uint32_t hik[KPB], cmask = 0;
+#pragma unroll
+  for (int j = 0; j < KPB; ++j) {
+    const bool v = j * kRecThreads + tid < nv;
+    const uint32_t lo = score_key(uv[j] > 0.f ? sv[j] - uv[j] : sv[j]);
+    hik[j] = v ? score_key(uv[j] > 0.f ? sv[j] + uv[j] : sv[j]) : 0u;
+    if (v && lo != hik[j] && hik[j] >= tau) cmask |= 1u << j;
+  }
+  const uint32_t ccnt = __builtin_popcount(cmask);
+  const uint32_t cbase = block_inclusive_scan<true, kRecWaves>(ccnt, wsum) - ccnt;
+  uint32_t ncand = 0;
+#pragma unroll
+  for (int w = 0; w < kRecWaves; ++w) ncand += wsum[w];
+  {
+    uint32_t p = cbase;
+#pragma unroll
+    for (int j = 0; j < KPB; ++j)
+      if ((cmask >> j) & 1u) list[p++] = c0 + j * kRecThreads + tid;
+  }
+  __syncthreads();
+  uint32_t n_exact = 0, n_unres = 0;
+  if (ncand > 0) {
+    const int64_t kbrow0 = b * rc.kbs;
+    const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
+    recompute_scores<kRecWaves>(list, static_cast<int>(ncand), srow, urow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0,
+                                n_exact, n_unres);
+    __syncthreads();  // every recomputed score is in its list slot
+  }
+  if (rc.stats != nullptr) {
+    if (n_exact) atomicAdd(&rc.stats[0], n_exact);
+    if (n_unres) atomicAdd(&rc.stats[1], n_unres);
+    if (rc.stats_ext && tid == 0 && ncand) atomicAdd(&rc.stats[2], ncand);
+  }
+
+  // ---- the exact keys >= tau, appended to the row's list
+  uint32_t key[KPB], nemit = 0;
+  {
+    const float *listf = reinterpret_cast<const float *>(list);
+    uint32_t p = cbase;
+#pragma unroll
+    for (int j = 0; j < KPB; ++j) {
+      const bool cj = (cmask >> j) & 1u;
+      key[j] = cj ? score_key(listf[p]) : hik[j];
+      p += cj ? 1u : 0u;
+      // a non-candidate with hik >= tau is exact (U = 0); below tau its key is dropped
+      if (key[j] < tau) key[j] = 0u;
+      nemit += key[j] != 0u ? 1u : 0u;
+    }
+  }
+  {
+    uint32_t mx = 0, unused = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 0; j < KPB; ++j) mx = key[j] > mx ? key[j] : mx;
+    wave_min_max(unused, mx);
+    if ((tid & 63) == 0 && mx != 0u) atomicMax(&rstate[4 * row + 2], mx);
+  }
+  const uint32_t ebase = block_inclusive_scan<true, kRecWaves>(nemit, wsum) - nemit;
+  if (tid == kRecThreads - 1) s_base = atomicAdd(&rstate[4 * row], ebase + nemit);
+  __syncthreads();
+  uint64_t *dst = lists + row * cap;
+  uint32_t pos = s_base + ebase;
+#pragma unroll
+  for (int j = 0; j < KPB; ++j) {
+    if (key[j] != 0u) {
+      const uint32_t col = static_cast<uint32_t>(c0 + j * kRecThreads + tid);
+      if (pos < static_cast<uint32_t>(cap)) dst[pos] = (static_cast<uint64_t>(key[j]) << 32) | static_cast<uint64_t>(~col);
+      ++pos;
+    }
+  }
+}
+
+// Sorted store of the k_sel largest of n unique composites, entry j * 1024 + tid in v[j] of thread tid, whose keys
+// lie in [kmin, kmax], by ranks from a counting sort: 2048 buckets uniform in the key over [kmin, kmax] (the bucket
+// is a monotone function of the key, so a higher bucket holds only larger composites); bucket starts from a block
+// scan from the top bucket; every entry is scattered into its bucket's range of tmp, and its rank is its bucket's
+// start plus the number of its bucket's entries above it.  Three barriers and O(n) work, against the log2(n)
+// dependent merge rounds of a sort.  Returns false, having stored nothing, when a bucket holds more than
+// kRankBucketMax entries (keys tied or clustered far beyond a smooth distribution); the caller then sorts.  Uses
+// sh.hist (counts, then starts), sh.wsum and tmp[0, n).
+constexpr int kRankBuckets = 2048;
+constexpr int kRankBucketMax = 256;
+template <int PER>
+__device__ bool rank_store(const uint64_t (&v)[PER], int n, uint32_t kmin, uint32_t kmax, int k_sel, int64_t row,
+                           int k, void *out, int out_i64, int causal, int64_t limit, int64_t offset, uint64_t *tmp,
+                           SelShared &sh) {
+  static_assert(kRankBuckets == 2 * kTopkThreads, "two buckets per thread");
+  const int tid = threadIdx.x;
+  uint32_t *cnt = sh.hist[0], *start = sh.hist[1];
+  cnt[tid] = 0u;
+  cnt[tid + kTopkThreads] = 0u;
+  __syncthreads();
+  const float scale = static_cast<float>(kRankBuckets) / (static_cast<float>(kmax - kmin) + 1.0f);
+  uint32_t bk[PER], pos[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    bk[j] = 0u;
+    pos[j] = 0u;
+    if (j * kTopkThreads + tid < n) {
+      const uint32_t d = static_cast<uint32_t>(static_cast<float>(static_cast<uint32_t>(v[j] >> 32) - kmin) * scale);
+      bk[j] = d < kRankBuckets - 1 ? d : kRankBuckets - 1;
+      pos[j] = atomicAdd(&cnt[bk[j]], 1u);  // the entry's place in its bucket (arrival order)
+    }
+  }
+  __syncthreads();
+  const int hi = kRankBuckets - 1 - 2 * tid;  // buckets hi and hi - 1, scanned from the top
+  const uint32_t c_hi = cnt[hi], c_lo = cnt[hi - 1];
+  const uint32_t excl = block_inclusive_scan<false>(c_hi + c_lo, sh.wsum) - (c_hi + c_lo);
+  start[hi] = excl;
+  start[hi - 1] = excl + c_hi;
+  if (__syncthreads_or(c_hi > kRankBucketMax || c_lo > kRankBucketMax)) return false;  // uniform
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (j * kTopkThreads + tid < n) tmp[start[bk[j]] + pos[j]] = v[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    if (j * kTopkThreads + tid < n) {
+      const uint32_t s0 = start[bk[j]], c = cnt[bk[j]];
+      uint32_t r = s0;
+#pragma unroll 4
+      for (uint32_t e = 0; e < c; ++e) r += tmp[s0 + e] > v[j] ? 1u : 0u;
+      if (r < static_cast<uint32_t>(k_sel)) {
+        const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[j] & 0xFFFFFFFFull));
+        store_index(out, out_i64, row * k + r, col, causal, limit, offset);
+      }
+    }
+  }
+  return true;
+}
+
+// One workgroup per row: the row's list (every column of its top k, each with its exact score; at least k_sel
+// entries) sorted, and the first k_sel stored with the post-processing.  A list past its capacity (its length
+// counter still counts every entry) falls back to the exact selection over the row's keys: the score where
+// U = 0 (exact, recomputed ones included), the upper end elsewhere (below tau, so below every score of the top k).
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void topk_collected_kernel(const float *scores, const float *bounds,
+                                                                     int64_t ld, int64_t S, int T, int k, int causal,
+                                                                     int64_t start_pos, int ratio, int64_t offset,
+                                                                     void *__restrict__ out, int out_i64,
+                                                                     const uint64_t *__restrict__ lists, int cap,
+                                                                     const uint32_t *__restrict__ rstate) {
+  extern __shared__ uint64_t cand[];  // 2 cap composites: the list, then the sort's exchange buffers
+  __shared__ SelShared sh;
   const int64_t row = blockIdx.x;
   const int64_t s = row % S;
   const int tid = threadIdx.x;
-  const int NP = (T + W - 1) / W;
   int64_t limit = INT64_MAX;
   int n_valid = T;
   if (causal) {
@@ -952,82 +1057,57 @@ __global__ __launch_bounds__(kTopkThreads) void topk_merge_kernel(const uint64_t
     n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
   }
   const int k_sel = k < n_valid ? k : n_valid;
-  int len[4];
+  if (k_sel > 0) {
+    // the length and the list go out together: the list up to its capacity (the rows' typical length is a
+    // fraction of it; the loads past the length are discarded)
+    const uint4 st = *reinterpret_cast<const uint4 *>(rstate + 4 * row);  // length, tau, largest key
+    const uint32_t n = st.x;
+    const uint64_t *src = lists + row * cap;
+    constexpr int kMaxPer = kTopkListCap / kTopkThreads;
+    uint64_t v[kMaxPer];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int nv = p < NP ? (n_valid - p * W <= 0 ? 0 : (n_valid - p * W < W ? n_valid - p * W : W)) : 0;
-    len[p] = k < nv ? k : nv;
+    for (int j = 0; j < kMaxPer; ++j) {
+      const int i = j * kTopkThreads + tid;
+      v[j] = src[i < cap ? i : 0];
+    }
+    if (n >= static_cast<uint32_t>(k_sel) && n <= static_cast<uint32_t>(cap)) {  // uniform
+      if (!rank_store<kMaxPer>(v, static_cast<int>(n), st.y, st.z, k_sel, row, k, out, out_i64, causal, limit, offset,
+                               cand, sh)) {
+#pragma unroll
+        for (int j = 0; j < kMaxPer; ++j) {
+          const uint32_t i = static_cast<uint32_t>(j * kTopkThreads + tid);
+          if (i < n) cand[i] = v[j];
+        }
+        __syncthreads();
+        int P = 128;
+        while (P < static_cast<int>(n)) P <<= 1;
+        sort_merge_store(cand, P, static_cast<int>(n), k_sel, row, k, out, out_i64, causal, limit, offset, nullptr);
+      }
+    } else {
+      const float *src = scores + row * ld;
+      const float *ub = bounds + row * ld;
+      float sv[KPT], uv[KPT];
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int col = j * kTopkThreads + tid;
+        sv[j] = src[col < n_valid ? col : 0];
+        uv[j] = ub[col < n_valid ? col : 0];
+      }
+      uint32_t key[KPT];
+#pragma unroll
+      for (int j = 0; j < KPT; ++j)
+        key[j] = j * kTopkThreads + tid < n_valid ? score_key(uv[j] > 0.f ? sv[j] + uv[j] : sv[j]) : 0u;
+      if (tid == 0) sh.k_rem = static_cast<uint32_t>(k_sel);
+      for (int i = tid; i < 2048; i += kTopkThreads) sh.hist[0][i] = 0;
+      __syncthreads();
+      select_sort_store<KPT>(key, k_sel, row, k, out, out_i64, causal, limit, offset, cand, sh);
+    }
   }
-  // the (at most 4 x 2048) composites go out in one round trip: two per list and thread (k <= 2048 on the
-  // split path), absent entries reading composite 0 of the row
-  const uint64_t *src = part + row * NP * k;
-  constexpr int kPer = 2048 / kTopkThreads;
-  uint64_t v[4][kPer];
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = tid + j * kTopkThreads;
-      v[p][j] = src[p < NP && i < len[p] ? p * k + i : 0];
-    }
-#pragma unroll
-  for (int p = 0; p < 4; ++p)
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = tid + j * kTopkThreads;
-      if (p < NP && i < len[p]) lists[p * k + i] = v[p][j];
-    }
-  __syncthreads();
-  uint64_t *pair = lists + 4 * k;
-  const int na = len[0] + len[1] < k ? len[0] + len[1] : k, nb = len[2] + len[3] < k ? len[2] + len[3] : k;
-  merge_first(lists, len[0], lists + k, len[1], na, [&](int e, uint64_t v) { pair[e] = v; });
-  merge_first(lists + 2 * k, len[2], lists + 3 * k, len[3], nb, [&](int e, uint64_t v) { pair[k + e] = v; });
-  __syncthreads();
-  merge_first(pair, na, pair + k, nb, k_sel, [&](int e, uint64_t v) {
-    const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v & 0xFFFFFFFFull));
-    store_index(out, out_i64, row * k + e, col, causal, limit, offset);
-  });
+  // ---- masked tail: fewer valid columns than k (the -inf ties, in ascending column order)
   for (int j = k_sel + tid; j < k; j += kTopkThreads)
     store_index(out, out_i64, row * k + j, static_cast<int64_t>(n_valid) + (j - k_sel), causal, limit, offset);
 }
 
-// W: columns per workgroup (T for whole rows), NP = ceil(T / W) slices (part != null when NP > 1)
-template <int KPT>
-int launch_topk_bounded(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
-                        int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, const TopkRecompute &rc,
-                        int W, int NP, uint64_t *part, hipStream_t stream) {
-  int P = 128;  // the sort's runs of 128
-  while (P < k) P <<= 1;
-  // dynamic LDS: the selection's 2P composites, or the recomputation list (4P columns)
-  const int lcap = 4 * P;
-  const size_t shmem = static_cast<size_t>(2 * P) * sizeof(uint64_t);
-  hipLaunchKernelGGL(topk_bounded_kernel<KPT>, dim3(static_cast<unsigned>(rows), static_cast<unsigned>(NP)),
-                     dim3(kTopkThreads), shmem, stream, scores, ld, S, T, k, causal, start_pos, ratio, offset, out,
-                     out_i64, rc, lcap, W, part);
-  KS_CHECK_LAUNCH("topk_bounded_kernel");
-  return KS_OK;
-}
-
-template <int KPT>
-int launch_topk_bounded_rows(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
-                             int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
-                             const TopkRecompute &rc, hipStream_t stream) {
-  return launch_topk_bounded<KPT>(scores, ld, rows, S, T, k, causal, start_pos, ratio, offset, out, out_i64, rc, T, 1,
-                                  nullptr, stream);
-}
-
-// Slices per row of the split selection: rows much longer than k (T > 8k: the load and the threshold
-// passes, which a slice shares out, dominate; shorter rows are bound by the sort of k and the candidates
-// near the threshold, which every slice repeats), enough workgroups for the 256 CUs, at most 4 (the merge
-// takes 4 lists), and at least 2k columns per slice.
-constexpr int kTopkMaxSlices = 4;
-inline int topk_slices(int64_t rows, int T, int k) {
-  if (rows >= 256 || T <= 4 * k) return 1;
-  int p = static_cast<int>((256 + rows - 1) / rows);
-  if (p > kTopkMaxSlices) p = kTopkMaxSlices;
-  while (p > 1 && T / p < 2 * k) --p;
-  return p;
-}
 }  // namespace
 }  // namespace ks
 
@@ -1066,86 +1146,95 @@ extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64
   return ks::launch_topk<64>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
 }
 
-int ks::launch_indexer_topk_bounded(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
+int ks::launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
                                     int causal, int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
                                     const TopkRecompute &rc, hipStream_t st) {
-  KS_CHECK_ARG(B >= 0 && S >= 0 && T >= 1 && T <= 65536 && k >= 1 && k <= T && k <= kTopkMaxK && ld >= T &&
-                   ratio >= 1 && start_pos >= 0,
+  KS_CHECK_ARG(B >= 0 && S >= 0 && T >= 1 && T <= 32768 && k >= 1 && k <= T && k <= 2048 && ld >= T && ratio >= 1 &&
+                   start_pos >= 0,
                "indexer top-k (bounded): bad arguments");
   const int64_t rows = B * S;
   if (rows == 0) return KS_OK;
-  KS_CHECK_ARG(rows < (int64_t(1) << 31), "indexer top-k (bounded): too many rows");
   const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
   const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
-  const int np = topk_slices(rows, Ti, ki);
-  if (np > 1 && k <= 2048 && rc.part != nullptr && rows * np * (k + 1024) <= rc.part_cap) {
-    // slices of W columns: 1024 times a power of two (W / 1024 keys per thread cover a slice)
-    int W = kTopkThreads;
-    while (W * np < Ti) W <<= 1;
-    const int NP = (Ti + W - 1) / W;
-    // the slices' first-digit histograms first, into the slots after the slices' lists
-    uint32_t *hist = reinterpret_cast<uint32_t *>(rc.part + rows * NP * k);
-    const float *bnd = rc.bounds;
-    const int sc = c;
-    const dim3 hgrid(static_cast<unsigned>(rows), static_cast<unsigned>(NP));
-#define KS_HIST(KPT_)                                                                                            \
-  hipLaunchKernelGGL(topk_slice_hist_kernel<KPT_>, hgrid, dim3(kTopkThreads), 0, st, scores, bnd, ld, S, Ti, sc, \
-                     start_pos, ratio, W, hist)
-    switch (W / kTopkThreads) {
-      case 1: KS_HIST(1); break;
-      case 2: KS_HIST(2); break;
-      case 4: KS_HIST(4); break;
-      case 8: KS_HIST(8); break;
-      case 16: KS_HIST(16); break;
-      default: KS_HIST(32); break;
-    }
-#undef KS_HIST
-    KS_CHECK_LAUNCH("topk_slice_hist_kernel");
-    int rcode;
-    switch (W / kTopkThreads) {
-      case 1: rcode = launch_topk_bounded<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
-      case 2: rcode = launch_topk_bounded<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
-      case 4: rcode = launch_topk_bounded<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
-      case 8: rcode = launch_topk_bounded<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
-      case 16: rcode = launch_topk_bounded<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
-      default: rcode = launch_topk_bounded<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, W, NP, rc.part, st); break;
-    }
-    if (rcode != KS_OK) return rcode;
-    const size_t shmem = static_cast<size_t>(6) * k * sizeof(uint64_t);  // 4 slice lists + 2 pair merges
-    hipLaunchKernelGGL(topk_merge_kernel, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, st, rc.part, W,
-                       Ti, ki, S, c, start_pos, ratio, offset, out, o);
-    KS_CHECK_LAUNCH("topk_merge_kernel");
-    return KS_OK;
+  const int np = topk_slices(rows, Ti);
+  int W = kTopkThreads;  // columns per histogram slice: 1024 times a power of two
+  while (W * np < Ti) W <<= 1;
+  const int NP = (Ti + W - 1) / W;
+  const int cap = topk_list_cap(Ti);
+  // columns per recomputation thread: 8, 4 or 2, the largest that still gives ~512 workgroups (two per CU; each
+  // wave should own about one tile of candidates: the tile's chain of dependent steps, not the arithmetic, sets
+  // its time, while every workgroup stages the row's query once)
+  int kpb = 8;
+  while (kpb > 2 && rows * ((Ti + kRecThreads * kpb - 1) / (kRecThreads * kpb)) < 512) kpb >>= 1;
+  const int segs = (Ti + kRecThreads * kpb - 1) / (kRecThreads * kpb);
+  KS_CHECK_ARG(rows * segs < (int64_t(1) << 31), "indexer top-k (bounded): too many rows");
+  const int64_t need = topk_bounded_slots(rows, NP, cap);
+  KS_CHECK_ARG(rc.part != nullptr && rc.part_cap >= need,
+               "indexer top-k (bounded): %lld 64-bit workspace slots required, %lld given", (long long)need,
+               (long long)rc.part_cap);
+  uint64_t *lists = rc.part;
+  uint32_t *hists = reinterpret_cast<uint32_t *>(rc.part + rows * cap);
+  uint32_t *rstate = hists + rows * NP * 2048;
+  const float *bnd = rc.bounds;
+  const dim3 hgrid(static_cast<unsigned>(rows), static_cast<unsigned>(NP));
+#define KS_HIST(KPT_)                                                                                          \
+  hipLaunchKernelGGL(topk_slice_hist_kernel<KPT_>, hgrid, dim3(kTopkThreads), 0, st, scores, bnd, ld, S, Ti, c, \
+                     start_pos, ratio, W, hists, rstate)
+  switch (W / kTopkThreads) {
+    case 1: KS_HIST(1); break;
+    case 2: KS_HIST(2); break;
+    case 4: KS_HIST(4); break;
+    case 8: KS_HIST(8); break;
+    case 16: KS_HIST(16); break;
+    default: KS_HIST(32); break;
   }
-  if (T <= 1024) return launch_topk_bounded_rows<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  if (T <= 2048) return launch_topk_bounded_rows<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  if (T <= 4096) return launch_topk_bounded_rows<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  if (T <= 8192) return launch_topk_bounded_rows<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  if (T <= 16384)
-    return launch_topk_bounded_rows<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
-  return launch_topk_bounded_rows<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, rc, st);
+#undef KS_HIST
+  KS_CHECK_LAUNCH("topk_slice_hist_kernel");
+  const dim3 rgrid(static_cast<unsigned>(rows * segs));
+#define KS_REC(KPB_)                                                                                             \
+  hipLaunchKernelGGL(topk_recompute_kernel<KPB_>, rgrid, dim3(kRecThreads), 0, st, scores, ld, S, Ti, ki, c, start_pos, \
+                     ratio, rc, segs, NP, hists, lists, cap, rstate)
+  if (kpb == 2) KS_REC(2);
+  else if (kpb == 4) KS_REC(4);
+  else KS_REC(8);
+#undef KS_REC
+  KS_CHECK_LAUNCH("topk_recompute_kernel");
+  const size_t shmem = static_cast<size_t>(2 * cap) * sizeof(uint64_t);
+#define KS_COLL(KPT_)                                                                                                \
+  hipLaunchKernelGGL(topk_collected_kernel<KPT_>, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, st, \
+                     scores, bnd, ld, S, Ti, ki, c, start_pos, ratio, offset, out, o, lists, cap, rstate)
+  if (Ti <= 1024) KS_COLL(1);
+  else if (Ti <= 2048) KS_COLL(2);
+  else if (Ti <= 4096) KS_COLL(4);
+  else if (Ti <= 8192) KS_COLL(8);
+  else if (Ti <= 16384) KS_COLL(16);
+  else KS_COLL(32);
+#undef KS_COLL
+  KS_CHECK_LAUNCH("topk_collected_kernel");
+  return KS_OK;
 }
 
-int64_t ks::topk_bounded_part_capacity(int64_t rows) {
-  if (rows <= 0 || rows >= 256) return 0;
-  int64_t p = (256 + rows - 1) / rows;
-  if (p > kTopkMaxSlices) p = kTopkMaxSlices;
-  return rows * p * (2048 + 1024);  // the slices' lists (k <= 2048), then their 2048-bucket histograms
+int64_t ks::topk_bounded_part_capacity(int64_t rows, int64_t T) {
+  if (rows <= 0 || T < 1 || T > 32768) return 0;
+  const int Ti = static_cast<int>(T);
+  const int np = topk_slices(rows, Ti);
+  int W = kTopkThreads;
+  while (W * np < Ti) W <<= 1;
+  return topk_bounded_slots(rows, (Ti + W - 1) / W, topk_list_cap(Ti));
 }
 
 // Diagnostic entry (not part of the public header) of the bounded top-k, for timing it alone: scores and
-// bounds from ks_dbg_indexer_scores_bounded over rotated q / k (with their row statistics); the scores
-// that are recomputed are rewritten in place.  ratio 1, int32 output.  part (optional, part_cap 64-bit slots,
-// topk_bounded_part_capacity(B S) of them: the slices' lists, then their bucket counts) enables the split
-// selection.
-extern "C" int ks_dbg_indexer_topk_bounded(float *scores, const float *bounds, const float *kmax, const uint16_t *q,
+// bounds from ks_dbg_indexer_scores_bounded over rotated q / k (with their row statistics); the scores that
+// are recomputed are rewritten in place (bound 0).  ratio 1, int32 output.  part: part_cap 64-bit slots, at
+// least ks_dbg_topk_bounded_slots(B S, T) of them.
+extern "C" int ks_dbg_indexer_topk_bounded(float *scores, float *bounds, const float *kmax, const uint16_t *q,
                                            const uint16_t *k, const float *w, const float *q_norm,
                                            const int32_t *q_span, const float *k_norm, const int32_t *k_span,
                                            int64_t B, int64_t S, int64_t T, int64_t k_top, int32_t causal,
                                            int64_t start_pos, void *out, void *stream, uint64_t *part,
                                            int64_t part_cap) {
   ks::last_error().clear();
-  KS_CHECK_ARG(scores && bounds && kmax && q && k && w && q_norm && q_span && k_norm && k_span && out,
+  KS_CHECK_ARG(scores && bounds && kmax && q && k && w && q_norm && q_span && k_norm && k_span && out && part,
                "ks_dbg_indexer_topk_bounded: null pointer");
   KS_CHECK_ARG(T <= 32768 && k_top <= 2048, "ks_dbg_indexer_topk_bounded: T <= 32768 and k <= 2048");
   const ks::TopkRecompute rc{bounds, kmax, q, k, w, q_norm, q_span, k_norm, k_span, T, ks::kScoreBoundC, nullptr, 0,
@@ -1153,3 +1242,5 @@ extern "C" int ks_dbg_indexer_topk_bounded(float *scores, const float *bounds, c
   return ks::launch_indexer_topk_bounded(scores, T, B, S, T, k_top, causal ? 1 : 0, start_pos, 1, 0, out, 0, rc,
                                          static_cast<hipStream_t>(stream));
 }
+
+extern "C" int64_t ks_dbg_topk_bounded_slots(int64_t rows, int64_t T) { return ks::topk_bounded_part_capacity(rows, T); }

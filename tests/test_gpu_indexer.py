@@ -475,14 +475,17 @@ def test_indexer_bounded_equals_exact_path(device, dist):
     print(f"[info] bounded path: {int(st[0])} exact dot recomputations", flush=True)
 
 
-# Rows too few to fill the GPU and much longer than k split into column slices (each selects its own exact
-# top k; a merge combines the sorted lists): causal rows whose valid prefix ends inside the first slice (later slices empty, masked tail), a
-# prefix ending inside the second slice, slices of unequal width (T = 5000), and all-equal scores, whose
-# order across slices is decided by the column alone.
+# Rows too few to fill the GPU: column slices for the threshold's bucket counts and several recomputation
+# segments per row, appending to one list per row: causal rows whose valid prefix ends inside the first slice
+# (later slices and segments empty, masked tail), a prefix ending inside the second slice, slices of unequal
+# width (T = 5000), and all-equal scores, whose order is decided by the column alone: every key lands in one
+# bucket of the rank store (the merge sort takes over at T = 8192, the list's capacity), and past the capacity
+# (T = 9000) the whole-row selection does.
 @pytest.mark.parametrize("S,T,k_top,start_pos,causal,zero_q", [(8, 4096, 256, 0, True, False),
                                                               (6, 4096, 256, 1490, True, False),
                                                               (5, 5000, 300, 0, False, False),
-                                                              (4, 8192, 512, 0, False, True)])
+                                                              (4, 8192, 512, 0, False, True),
+                                                              (3, 9000, 512, 0, False, True)])
 def test_indexer_split_topk(device, S, T, k_top, start_pos, causal, zero_q):
     g = torch.Generator().manual_seed(S * T + k_top)
     q = torch.randn(1, S, 64, 128, generator=g)

@@ -808,8 +808,12 @@ __global__ __launch_bounds__(kRecThreads) void topk_recompute_kernel(float *scor
   __shared__ int32_t list[SW];
   __shared__ uint32_t wsum[kRecWaves];
   __shared__ uint32_t s_tau, s_base;
-  const int64_t row = blockIdx.x / segs;
-  const int seg = static_cast<int>(blockIdx.x % segs);
+  // workgroups are dealt to the 8 XCDs round-robin (block id mod 8): the segments of one row are placed on one
+  // XCD, so its L2 serves the row's query rows and bucket counts to all of them
+  const int64_t nblk = gridDim.x;
+  const int64_t lb = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int64_t row = lb / segs;
+  const int seg = static_cast<int>(lb % segs);
   const int64_t s = row % S, b = row / S;
   const int tid = threadIdx.x;
   int n_valid = T;

@@ -1,0 +1,57 @@
+"""No kernel of the library reads the AQL dispatch packet (CPU: hipcc cross-compiles every source).
+
+The dispatch packet lives in the HSA queue's ring buffer in host memory, so a kernel that needs it (for the
+workgroup size: the compiler asks for it when it moves a per-thread array into LDS and must compute the flat
+thread id) makes each workgroup's first scalar load a round trip to the host: one such array in the bounded
+top-k's recomputation delayed every workgroup's first loads by 5-10 us.  The kernel descriptors record the
+request as .amdhsa_user_sgpr_dispatch_ptr; this compiles each source with the library's flags and checks that
+no kernel sets it."""
+import concurrent.futures
+import glob
+import os
+import re
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def dispatch_ptr_kernels(asm: str):
+    """Names of the kernels whose descriptor requests the dispatch pointer."""
+    out = []
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", asm, re.S):
+        d = re.search(r"\.amdhsa_user_sgpr_dispatch_ptr\s+(\d+)", m.group(2))
+        if d is not None and d.group(1) != "0":
+            out.append(m.group(1))
+    return out
+
+
+def test_checker_pins():
+    desc = ("\t.amdhsa_kernel _Za\n\t\t.amdhsa_user_sgpr_dispatch_ptr 1\n\t\t.amdhsa_user_sgpr_queue_ptr 0\n"
+            "\t.end_amdhsa_kernel\n\t.amdhsa_kernel _Zb\n\t\t.amdhsa_user_sgpr_dispatch_ptr 0\n"
+            "\t.end_amdhsa_kernel\n")
+    assert dispatch_ptr_kernels(desc) == ["_Za"]
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc is not installed")
+def test_no_kernel_reads_the_dispatch_packet(tmp_path):
+    sys.path.insert(0, REPO)
+    from kernelswift_amd import build as ksbuild
+    srcs = sorted(glob.glob(os.path.join(REPO, "kernelswift_amd", "csrc", "*.hip")))
+    assert srcs
+
+    def compile_one(src):
+        out = tmp_path / (os.path.basename(src) + ".s")
+        r = subprocess.run([ksbuild.HIPCC, *ksbuild.COMMON, "--cuda-device-only", "-S", src, "-o", str(out)],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-2000:]
+        return src, dispatch_ptr_kernels(out.read_text())
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=4) as ex:
+        results = list(ex.map(compile_one, srcs))
+    bad = [f"{os.path.basename(src)}: {k}" for src, ks in results for k in ks]
+    assert bad == [], "\n".join(bad)

@@ -220,16 +220,17 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
     kmax = torch.empty(B, (T + 255) // 256, dtype=torch.float32, device="cuda")
     idx = torch.empty(B, S, min(p["k_top"], T), dtype=torch.int32, device="cuda")
     lib = _lib.load()
-    # the bounded selection's workspace: lists, bucket counts, list lengths
-    part = torch.empty(lib.ks_dbg_topk_bounded_slots(B * S, T), dtype=torch.int64, device="cuda")
+    # the bounded selection's workspace: lists, bucket counts, list lengths; where the fused call counts the
+    # rows in the score kernel (a one-round score grid), so does the diagnostic one, into this zeroed region
+    part = torch.zeros(lib.ks_dbg_topk_bounded_slots(B * S, T), dtype=torch.int64, device="cuda")
     (qn, qs), (kn, ks_) = stats
     stream = torch.cuda.current_stream().cuda_stream
 
     def scores_bounded():
         _lib.check(lib.ks_dbg_indexer_scores_bounded(qr.data_ptr(), kr.data_ptr(), t["w"].data_ptr(), qn.data_ptr(),
                                                      qs.data_ptr(), kn.data_ptr(), ks_.data_ptr(), out.data_ptr(),
-                                                     bnd.data_ptr(), kmax.data_ptr(), B, S, T, 1, p["start_pos"],
-                                                     stream), "scores (bounded)")
+                                                     bnd.data_ptr(), kmax.data_ptr(), part.data_ptr(), B, S, T, 1,
+                                                     p["start_pos"], stream), "scores (bounded)")
 
     def topk_bounded():
         _lib.check(lib.ks_dbg_indexer_topk_bounded(out.data_ptr(), bnd.data_ptr(), kmax.data_ptr(), qr.data_ptr(),
@@ -244,13 +245,17 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
                                          T, 1, p["start_pos"], 1, stream), "scores")
 
     score_us = _events_avg(scores_bounded, steps, warmup)
-    # the bounded top-k writes its recomputed scores back (bound 0), so every timed call starts from a fresh
-    # copy of the score kernel's output; the copies are timed alone and subtracted
-    out0, bnd0 = out.clone(), bnd.clone()
+    # the bounded top-k writes its recomputed scores back (bound 0) and appends to its lists, so every timed
+    # call starts from a fresh copy of one score kernel call's output (scores, bounds, counts on a zeroed
+    # workspace); the copies are timed alone and subtracted
+    part.zero_()
+    scores_bounded()
+    out0, bnd0, part0 = out.clone(), bnd.clone(), part.clone()
 
     def restore():
         out.copy_(out0)
         bnd.copy_(bnd0)
+        part.copy_(part0)
 
     def restore_topk():
         restore()
@@ -270,12 +275,13 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
         "us_per_call": round(dev_med, 3), "us_per_call_mean": round(dev_mean, 3),
         "wall_us_per_call_sync": round(wall_med, 3), "ms_per_step": ms_step,
         "kernels_us": {"indexer_scores_kernel (bounded)": round(score_us, 3),
-                       "bounded top-k (histograms, recomputation, sort)": round(topkb_us, 3),
+                       "bounded top-k": round(topkb_us, 3),
                        "indexer_scores_kernel (exact, other shapes)": round(exact_us, 3),
                        "topk_rows_kernel (plain, other shapes)": round(topk_us, 3)},
         "roofline": {"bound": "mfma", "kernel": "indexer_scores_kernel (bounded)", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true>@{cfg}")},
+                     "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true, true>@{cfg}")
+                     or _traffic(f"indexer_scores_kernel<4, 128, false, true, false>@{cfg}")},
         # the product's bounded top-k reads a score and a bound (8 B) per column; the plain one 4 B
         "topk_bounded_GBps": round(S * T * 8 / (topkb_us * 1e-6) / 1e9, 1),
         "topk_plain_GBps": round(S * T * 4 / (topk_us * 1e-6) / 1e9, 1),

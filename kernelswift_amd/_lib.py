@@ -53,7 +53,7 @@ SIGNATURES = {
 # diagnostic exports (not in include/kswift.h)
 DEBUG_SIGNATURES = {
     "ks_dbg_indexer_scores_bounded": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
-                                                     _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_p]),
+                                                     _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_p]),
     "ks_dbg_indexer_topk_bounded": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_p, _c_p,
                                                    _c_p, _c_i64]),

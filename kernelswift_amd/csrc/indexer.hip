@@ -84,25 +84,38 @@ int check_indexer_args(const char *fn, int64_t k_top, int64_t start_pos, int32_t
   return KS_OK;
 }
 
-// Scores of the prepared rows (ws.q_rot / ws.k_rot with their statistics) -> exact top-k.
-// path: 0 = bounded when the shape allows it, 1 = exact, 2 = bounded (error when the shape does not allow
-// it), 3 = bounded with the extended counters.
+// Whether the scores take the bounded path (path: 0 = bounded when the shape allows it, 1 = exact, 2 = bounded,
+// 3 = bounded with the extended counters).
+bool takes_bounded(int64_t k_top, int32_t w_bf16, int64_t H, int64_t D, int64_t T, int path) {
+  const int64_t kk = k_top < T ? k_top : T;
+  return H == 64 && D == 128 && !w_bf16 && T <= 32768 && kk <= 2048 && path != 1;
+}
+
+// The bounded path's count region in the workspace, which the row preparation launch clears when the score
+// kernel counts the rows: 16-byte words.
+int64_t count_words16(const IndexerWs &ws, int64_t B, int64_t S, int64_t T) {
+  return ws.part_cap > 0 && ks::scores_count_rows(B, S, T) ? B * S * ks::kTopkCountWords / 4 : 0;
+}
+
+// Scores of the prepared rows (ws.q_rot / ws.k_rot with their statistics) -> exact top-k.  Where the score
+// kernel counts the rows, the bounded path needs the count region cleared by the row preparation launch.
 int indexer_select(const char *fn, const IndexerWs &ws, const void *w, int32_t w_bf16, int64_t k_top, int32_t causal,
                    int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
                    int64_t H, int64_t D, int64_t T, hipStream_t st, float bound_c, uint32_t *stats, int path) {
   const int64_t kk = k_top < T ? k_top : T;
-  const bool can_bound = H == 64 && D == 128 && !w_bf16 && T <= 32768 && kk <= 2048;
+  const bool can_bound = takes_bounded(k_top, w_bf16, H, D, T, 0);
   KS_CHECK_ARG(path < 2 || can_bound,
                "%s: the bounded path needs H = 64, D = 128, fp32 weights, T <= 32768 and k <= 2048", fn);
   int rc;
   if (can_bound && path != 1) {
+    const bool counted = ks::scores_count_rows(B, S, T);
     rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span, ws.scores, B,
                                    S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, bound_c, nullptr, st, ws.bounds,
-                                   ws.kmax);
+                                   ws.kmax, counted ? ks::topk_bounded_counts(ws.part, B * S, T) : nullptr);
     if (rc != KS_OK) return rc;
     const ks::TopkRecompute trc{ws.bounds, ws.kmax, ws.q_rot, ws.k_rot, static_cast<const float *>(w), ws.q_norm,
                                 ws.q_span, ws.k_norm, ws.k_span, T, bound_c, stats, path == 3 ? 1 : 0, ws.part,
-                                ws.part_cap};
+                                ws.part_cap, counted ? 1 : 0};
     return ks::launch_indexer_topk_bounded(ws.scores, T, B, S, T, kk, causal ? 1 : 0, start_pos, ratio, offset, out,
                                            out_i64 ? 1 : 0, trc, st);
   }
@@ -140,7 +153,10 @@ int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_
   // q rows at positions start_pos + s; k rows of every batch (stride k_batch_stride) at positions t
   const ks::RowJob qjob{q, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H, H, S, start_pos, rd};
   const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
-  rc = ks::launch_rope_rows(qjob, kjob, freqs, static_cast<int>(D), static_cast<int>(rope_start), st);
+  const bool bounded = takes_bounded(k_top, w_bf16, H, D, T, path);
+  rc = ks::launch_rope_rows(qjob, kjob, freqs, static_cast<int>(D), static_cast<int>(rope_start), st,
+                            bounded ? ks::topk_bounded_counts(ws.part, B * S, T) : nullptr,
+                            bounded ? count_words16(ws, B, S, T) : 0);
   if (rc != KS_OK) return rc;
   return indexer_select("ks_indexer", ws, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B, S, H,
                         D, T, st, bound_c, stats, path);
@@ -166,7 +182,10 @@ int indexer_fp8_impl(const uint8_t *q, const float *q_scale, const uint8_t *k, c
   // q rows (scale per row) and k rows of every batch (stride k_batch_stride, scale per row, same stride)
   const ks::Fp8RowJob qjob{q, q_scale, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H};
   const ks::Fp8RowJob kjob{k, k_scale, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride};
-  rc = ks::launch_fp8_rows(qjob, kjob, static_cast<int>(D), st);
+  const bool bounded = takes_bounded(k_top, w_bf16, H, D, T, path);
+  rc = ks::launch_fp8_rows(qjob, kjob, static_cast<int>(D), st,
+                           bounded ? ks::topk_bounded_counts(ws.part, B * S, T) : nullptr,
+                           bounded ? count_words16(ws, B, S, T) : 0);
   if (rc != KS_OK) return rc;
   return indexer_select("ks_indexer_fp8", ws, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B, S,
                         H, D, T, st, bound_c, stats, path);

@@ -5,6 +5,13 @@
 
 namespace ks {
 
+// Order-preserving 32-bit key of an fp32 score (larger score, larger key; -0 and +0 share a key).
+__device__ __forceinline__ uint32_t score_key(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) == 0) u = 0;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // Exponent of the least significant bit of a nonzero bf16 value: value = m * 2^lsb, m integer.
 __host__ __device__ inline int bf16_lsb_exponent(uint16_t b) {
   const int e = (b >> 7) & 0xFF;
@@ -123,9 +130,11 @@ struct RowJob {
 };
 
 // Both jobs in one launch (job1.rows may be 0); rows of D in {64, 128} for statistics, any multiple of 8
-// otherwise.  Rotated dims [rope_start, rope_start + job.rope_dim), freqs = (cos, sin) per position.
+// otherwise.  Rotated dims [rope_start, rope_start + job.rope_dim), freqs = (cos, sin) per position.  The
+// launch also clears zero16 16-byte words at zero (the bounded selection's counts, which the score kernel
+// that follows accumulates into).
 int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
-                     hipStream_t stream);
+                     hipStream_t stream, void *zero = nullptr, int64_t zero16 = 0);
 
 // One set of e4m3 rows for the dequantisation / row-statistics launch: row r is source row
 // (r / rows_per_batch) * src_batch_rows + r % rows_per_batch of src (D code bytes) with fp32 scale
@@ -139,20 +148,30 @@ struct Fp8RowJob {
   int64_t rows, rows_per_batch, src_batch_rows;
 };
 
-// Both jobs in one launch (job1.rows may be 0); D in {64, 128}.
-int launch_fp8_rows(const Fp8RowJob &job0, const Fp8RowJob &job1, int D, hipStream_t stream);
+// Both jobs in one launch (job1.rows may be 0); D in {64, 128}.  Clears zero16 16-byte words at zero, as
+// launch_rope_rows does.
+int launch_fp8_rows(const Fp8RowJob &job0, const Fp8RowJob &job1, int D, hipStream_t stream, void *zero = nullptr,
+                    int64_t zero16 = 0);
 
 // Exact scores (bounds == nullptr), or, with bounds (H = 64, D = 128, fp32 weights), the canonical score from
 // the lower interval end of every dot plus a per-score bound U: the exact score lies in [score - U,
 // score + U], both ends also after rounding to nearest, and U = 0 exactly when the score is exact.  kmax
 // [B][ceil(T / kScoreKeyBlock)] then receives each key block's key-norm maximum (the interval half-width
-// of a dot is bound_c 2^-23 ||q_h|| kmax), for an exact recomputation with the same intervals.
+// of a dot is bound_c 2^-23 ||q_h|| kmax), for an exact recomputation with the same intervals, and
+// row_counts [B S][2048] (zero on entry; may be null) is incremented by each row's counts of the first 11-bit
+// digit of score_key(lower end) over its valid columns (the bounded selection's threshold histogram).
 constexpr int kScoreKeyBlock = 256;
+// Whether the fused entry counts the rows in the score kernel: its grid of (key block, 8 queries) workgroups
+// fits the 256 CUs in one round.  The counts' LDS leaves no room for a second workgroup per CU, which a grid
+// of several rounds needs to start its next workgroups in the tails of the running ones; such grids are counted
+// by the selection's own histogram launch instead.
+constexpr int64_t kScoreCountGrid = 256;
+bool scores_count_rows(int64_t B, int64_t S, int64_t T);
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
                           int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds = nullptr,
-                          float *kmax = nullptr);
+                          float *kmax = nullptr, uint32_t *row_counts = nullptr);
 
 // Sorted exact top-k of rows of bounded scores (the bound-emitting score kernel's output): a threshold from the
 // lower ends, exact recomputation of the scores that may reach the top k (interval test with the score kernel's
@@ -177,9 +196,16 @@ struct TopkRecompute {
   // the threshold, the bucket counts of their column slices, the list lengths
   uint64_t *part;
   int64_t part_cap;  // 64-bit slots
+  // nonzero: the score kernel has already counted the rows (one slice per row, at topk_bounded_counts) and the
+  // row states there are clear, so the selection starts with the threshold
+  int counted;
 };
 // Slots the bounded selection needs for `rows` rows of T <= 32768 columns (0 outside that range).
 int64_t topk_bounded_part_capacity(int64_t rows, int64_t T);
+// The counted form's region in part: the rows' bucket counts ([rows][2048] 32-bit) followed by their states
+// ([rows][4] 32-bit), kTopkCountWords 32-bit words per row in all, to be cleared before the score kernel.
+constexpr int64_t kTopkCountWords = 2048 + 4;
+uint32_t *topk_bounded_counts(uint64_t *part, int64_t rows, int64_t T);
 int launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k, int causal,
                                 int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
                                 const TopkRecompute &rc, hipStream_t stream);

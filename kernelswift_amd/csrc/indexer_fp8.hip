@@ -125,9 +125,11 @@ Fp8RowJobK kernel_job(const Fp8RowJob &j) {
 }
 
 // One lane per 8 elements (8 code bytes in, 16 bf16 bytes out); the CPR = D / 8 lanes of a row reduce its
-// statistics.  Blocks [0, blocks0) take job 0, the rest job 1 (fields selected one by one, uniformly).
+// statistics.  Blocks [0, blocks0) take job 0, the rest job 1 (fields selected one by one, uniformly).  The
+// grid's threads also clear zero16 16-byte words at zero (grid-strided).
 template <int CPR>
-__global__ __launch_bounds__(256) void fp8_rows_kernel(Fp8RowJobK j0, Fp8RowJobK j1, uint32_t blocks0) {
+__global__ __launch_bounds__(256) void fp8_rows_kernel(Fp8RowJobK j0, Fp8RowJobK j1, uint32_t blocks0,
+                                                      uint4 *__restrict__ zero, uint32_t zero16) {
   constexpr int D = 8 * CPR;
   const bool second = blockIdx.x >= blocks0;
 #define KS_PICK(f) (second ? j1.f : j0.f)
@@ -169,12 +171,17 @@ __global__ __launch_bounds__(256) void fp8_rows_kernel(Fp8RowJobK j0, Fp8RowJobK
     int32_t *span = second ? j1.span : j0.span;
     row_norm_span(ss, lsb, norm[row], span[row]);
   }
+  // after the row's own stores, so that its loads do not wait behind these
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < zero16; i += gridDim.x * 256u) zero[i] = make_uint4(0, 0, 0, 0);
 }
 
 }  // namespace
 
-int launch_fp8_rows(const Fp8RowJob &job0, const Fp8RowJob &job1, int D, hipStream_t stream) {
+int launch_fp8_rows(const Fp8RowJob &job0, const Fp8RowJob &job1, int D, hipStream_t stream, void *zero,
+                    int64_t zero16) {
   KS_CHECK_ARG(D == 64 || D == 128, "fp8 rows: D=%d, supported: 64 and 128", D);
+  KS_CHECK_ARG(zero16 >= 0 && zero16 < (int64_t(1) << 31) && (zero16 == 0 || aligned(zero, 16)),
+               "fp8 rows: clear range of %lld words", (long long)zero16);
   const int64_t c0 = job0.rows * (D / 8), c1 = job1.rows * (D / 8);
   KS_CHECK_ARG(c0 + c1 + 512 < (int64_t(1) << 31), "fp8 rows: %lld + %lld chunks exceed the 32-bit grid",
                (long long)c0, (long long)c1);
@@ -182,14 +189,17 @@ int launch_fp8_rows(const Fp8RowJob &job0, const Fp8RowJob &job1, int D, hipStre
                    job1.rows_per_batch < (int64_t(1) << 31),
                "fp8 rows: rows per batch out of range");
   const int64_t b0 = ceil_div(c0, 256), b1 = ceil_div(c1, 256);
+  KS_CHECK_ARG(b0 + b1 > 0 || zero16 == 0, "fp8 rows: a clear range needs rows");
   if (b0 + b1 == 0) return KS_OK;
   const dim3 grid(static_cast<unsigned>(b0 + b1));
   const Fp8RowJobK k0 = kernel_job(job0), k1 = kernel_job(job1);
   const uint32_t n0 = static_cast<uint32_t>(b0);
+  uint4 *zp = static_cast<uint4 *>(zero);
+  const uint32_t zn = static_cast<uint32_t>(zero16);
   if (D == 128) {
-    hipLaunchKernelGGL(fp8_rows_kernel<16>, grid, dim3(256), 0, stream, k0, k1, n0);
+    hipLaunchKernelGGL(fp8_rows_kernel<16>, grid, dim3(256), 0, stream, k0, k1, n0, zp, zn);
   } else {
-    hipLaunchKernelGGL(fp8_rows_kernel<8>, grid, dim3(256), 0, stream, k0, k1, n0);
+    hipLaunchKernelGGL(fp8_rows_kernel<8>, grid, dim3(256), 0, stream, k0, k1, n0, zp, zn);
   }
   KS_CHECK_LAUNCH("fp8_rows_kernel");
   return KS_OK;

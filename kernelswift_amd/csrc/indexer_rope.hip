@@ -48,11 +48,12 @@ RowJobK kernel_job(const RowJob &j) {
 
 // One thread per 16-byte chunk; blocks [0, blocks0) take job 0 and the rest job 1 (a uniform choice, so
 // each field is selected separately from the kernel arguments, never through a pointer to them).
-// CPR: chunks per row, 8 or 16 with statistics (0: any D, no statistics).
+// CPR: chunks per row, 8 or 16 with statistics (0: any D, no statistics).  The grid's threads also clear
+// zero16 16-byte words at zero (grid-strided).
 template <int CPR>
 __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, uint32_t blocks0,
                                                        const float *__restrict__ freqs, int D, FastDiv cpr,
-                                                       int rope_start) {
+                                                       int rope_start, uint4 *__restrict__ zero, uint32_t zero16) {
   const bool second = blockIdx.x >= blocks0;
 #define KS_PICK(f) (second ? j1.f : j0.f)
   const uint16_t *__restrict__ src = KS_PICK(src);
@@ -98,12 +99,16 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, 
       row_norm_span(ss, lsb, norm[row], span[row]);
     }
   }
+  // after the row's own stores, so that its loads do not wait behind these
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < zero16; i += gridDim.x * 256u) zero[i] = make_uint4(0, 0, 0, 0);
 }
 
 }  // namespace
 
 int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
-                     hipStream_t stream) {
+                     hipStream_t stream, void *zero, int64_t zero16) {
+  KS_CHECK_ARG(zero16 >= 0 && zero16 < (int64_t(1) << 31) && (zero16 == 0 || aligned(zero, 16)),
+               "rope rows: clear range of %lld words", (long long)zero16);
   const int64_t c0 = job0.rows * (D / 8), c1 = job1.rows * (D / 8);
   KS_CHECK_ARG(c0 + c1 + 512 < (int64_t(1) << 31), "rope rows: %lld + %lld chunks exceed the 32-bit grid",
                (long long)c0, (long long)c1);
@@ -113,6 +118,7 @@ int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs,
                    job1.H < (int64_t(1) << 31) && job0.S < (int64_t(1) << 31) && job1.S < (int64_t(1) << 31),
                "rope rows: batch, head or position extent out of range");
   const int64_t b0 = ceil_div(c0, 256), b1 = ceil_div(c1, 256);
+  KS_CHECK_ARG(b0 + b1 > 0 || zero16 == 0, "rope rows: a clear range needs rows");
   if (b0 + b1 == 0) return KS_OK;
   const bool stats = job0.norm != nullptr;
   KS_CHECK_ARG((job1.rows == 0 || (job1.norm != nullptr) == stats) && (!stats || D == 64 || D == 128),
@@ -121,12 +127,14 @@ int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs,
   const RowJobK k0 = kernel_job(job0), k1 = kernel_job(job1);
   const FastDiv cpr(static_cast<uint32_t>(D / 8));
   const uint32_t n0 = static_cast<uint32_t>(b0);
+  uint4 *zp = static_cast<uint4 *>(zero);
+  const uint32_t zn = static_cast<uint32_t>(zero16);
   if (stats && D == 128) {
-    hipLaunchKernelGGL(rope_rows_kernel<16>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start);
+    hipLaunchKernelGGL(rope_rows_kernel<16>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn);
   } else if (stats) {
-    hipLaunchKernelGGL(rope_rows_kernel<8>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start);
+    hipLaunchKernelGGL(rope_rows_kernel<8>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn);
   } else {
-    hipLaunchKernelGGL(rope_rows_kernel<0>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start);
+    hipLaunchKernelGGL(rope_rows_kernel<0>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn);
   }
   KS_CHECK_LAUNCH("rope_rows_kernel");
   return KS_OK;

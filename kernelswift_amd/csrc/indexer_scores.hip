@@ -27,6 +27,11 @@
 // (span_q + span_k <= 52); up to 84 a hi/lo split keeps both halves exact; beyond that an integer
 // accumulator (exact_dot_wide_bf16) computes the dot.  A wave whose norms could overflow inside the MFMA
 // ((||q|| ||k|| >= 2^126) treats every dot as a near tie.
+//
+// Bound mode (BOUND) keeps the interval test but writes, instead of recomputing near ties, the canonical score
+// of the lower interval ends and a bound U on its distance from the exact score; its counting form (COUNT) also
+// builds each row's histogram of the first 11-bit digit of the lower ends' keys for the bounded top-k's
+// threshold (per-wave LDS counts, flushed with one global atomic per nonzero bucket).
 #include "common.h"
 #include "indexer_common.h"
 #include "indexer_exact.h"
@@ -250,10 +255,13 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
 }
 
 // Shared memory of the bound-emitting variant: the key block and the per-wave norm maxima only (no
-// deferred-key entries, no dot lists, no row statistics).
-template <int KD>
+// deferred-key entries, no dot lists, no row statistics), and in the counting form each wave's counts of its
+// row's lower ends (2048 buckets as 16-bit halves: a wave counts at most kKR keys).  The counts take the LDS
+// of a second workgroup per CU, so the counting form is for grids of one round.
+template <int KD, bool COUNT>
 struct ScoresLdsBound {
   uint4 k[kKR * KD / 8];
+  uint32_t cnt[COUNT ? kQW : 0][1024];
   float knorm[kKR];
   int32_t kspan[kKR];
   int32_t qspan[kQW][64];
@@ -262,17 +270,18 @@ struct ScoresLdsBound {
   float red[kQW];
 };
 
-template <int HT, int KD, bool WBF, bool BOUND>
+template <int HT, int KD, bool WBF, bool BOUND, bool COUNT = false>
 __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
     const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
     int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats, int xcd_pk,
-    float *__restrict__ bounds, float *__restrict__ kmax) {
+    float *__restrict__ bounds, float *__restrict__ kmax, uint32_t *__restrict__ row_counts) {
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
   static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
-  __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD>, ScoresLds<KD, HT>> L;
+  static_assert(BOUND || !COUNT, "counts of lower ends need the bounds");
+  __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD, COUNT>, ScoresLds<KD, HT>> L;
   // the wave index is uniform per wave; readfirstlane lets the compiler keep the query row, the causal limit
   // and the tile loop in scalar registers
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -360,6 +369,10 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const int lin = it * kThreads + tid;
     const int kr = lin / kC, ch = lin % kC;
     L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = kr < nk ? kv[it] : make_uint4(0, 0, 0, 0);
+  }
+  if constexpr (COUNT) {  // this wave's lower-end counts start at zero
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<uint4 *>(L.cnt[wave])[lane + 64 * i] = make_uint4(0, 0, 0, 0);
   }
   // the only barrier (from here on every wave runs independently): LDS writes done, no wait for the q loads
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -490,7 +503,15 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
       }
       float u = (dph[0] - dpl[0]) + 0x1p-16f * (dph[0] + dpl[0]) + 0x1p-21f * fabsf(tot) + 0x1p-100f;
       if (forced) u = __builtin_inff();  // score 0 with an infinite bound: always recomputed
-      if (g == 0 && kvalid) urow[key] = (key < limit && ((km >> l16) & 1u)) ? u : 0.f;
+      const bool live_key = kvalid && key < limit;
+      const float us = (live_key && ((km >> l16) & 1u)) ? u : 0.f;
+      if (g == 0 && kvalid) urow[key] = us;
+      // the row's threshold histogram: first 11-bit digit of the lower end's key, counted for the valid columns
+      // (the same arithmetic as the stored score and bound give)
+      if (COUNT && g == 0 && live_key) {
+        const uint32_t kk = score_key(us > 0.f ? outv - us : outv);
+        if (kk != 0u) atomicAdd(&L.cnt[wave][kk >> 22], 1u << ((kk >> 17) & 16u));
+      }
     }
     return km;
   };
@@ -499,8 +520,21 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   // deferred keys are flushed at one place: before a tile's deferred keys would overflow the list, and in
   // one extra round after the last tile.
   f32x4_t acc[HT], nxt[HT];
-  if (nlive > 0) tile_mfma(0, acc);
-  for (int t = 0; t <= nlive; ++t) {
+  if constexpr (BOUND) {
+    // no deferred keys: two tiles per iteration, alternating the accumulator sets (no copy between them)
+    if (nlive > 0) tile_mfma(0, acc);
+    for (int t = 0; t < nlive; t += 2) {
+      uint32_t pl[2 * HT], ph[2 * HT];
+      if (t + 1 < nlive) tile_mfma(t + 1, nxt);
+      (void)tile_epilogue(t, acc, pl, ph);
+      if (t + 1 < nlive) {
+        if (t + 2 < nlive) tile_mfma(t + 2, acc);
+        (void)tile_epilogue(t + 1, nxt, pl, ph);
+      }
+    }
+  }
+  if (!BOUND && nlive > 0) tile_mfma(0, acc);
+  for (int t = 0; t <= (BOUND ? -1 : nlive); ++t) {
     const bool live_t = t < nlive;
     uint32_t pl[2 * HT], ph[2 * HT];
     uint32_t km = 0;
@@ -543,6 +577,20 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     const int key_l = 16 * t + l16;
     if (g == 0 && key_l < nk) orow[kb0 + key_l] = -INFINITY;
   }
+  if constexpr (COUNT) {
+    // the wave's counts into its row's histogram (only the nonzero buckets: a block of 256 keys fills a few
+    // dozen of the 2048)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t *hrow = row_counts + (b * S + s) * 2048;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int wd = lane + 64 * i;
+      const uint32_t v = L.cnt[wave][wd];
+      if (v & 0xFFFFu) atomicAdd(&hrow[2 * wd], v & 0xFFFFu);
+      if (v >> 16) atomicAdd(&hrow[2 * wd + 1], v >> 16);
+    }
+  }
   if (stats != nullptr) {
     if (lane == 0 && n_exact) atomicAdd(&stats[0], n_exact);
     if (n_unres) atomicAdd(&stats[1], n_unres);
@@ -553,7 +601,7 @@ template <int HT, int KD>
 int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                      const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                      int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c, uint32_t *stats,
-                     float *bounds, float *kmax, hipStream_t stream) {
+                     float *bounds, float *kmax, uint32_t *row_counts, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
   // XCD tiling (Pq x Pk = 8) that minimises the L2 fills: each query group's rows are read by Pk XCDs,
@@ -575,20 +623,27 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
   if (bounds != nullptr) {
     if constexpr (HT == 4) {
       if (w_bf16) return fail(KS_ERR_INVALID, "indexer scores: score bounds need fp32 weights");
-      hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true>), grid, dim3(kThreads), 0, stream, q, k, w, qn,
-                         qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats,
-                         xcd_pk, bounds, kmax);
+      if (kmax == nullptr) return fail(KS_ERR_INVALID, "indexer scores: score bounds need the kmax buffer");
+      if (row_counts != nullptr) {
+        hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, true>), grid, dim3(kThreads), 0, stream, q, k, w,
+                           qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
+                           stats, xcd_pk, bounds, kmax, row_counts);
+      } else {
+        hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, false>), grid, dim3(kThreads), 0, stream, q, k,
+                           w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
+                           stats, xcd_pk, bounds, kmax, nullptr);
+      }
     } else {
       return fail(KS_ERR_INVALID, "indexer scores: score bounds need H = 64");
     }
   } else if (w_bf16) {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp,
                        kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk,
-                       nullptr, nullptr);
+                       nullptr, nullptr, nullptr);
   } else {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn,
                        qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats,
-                       xcd_pk, nullptr, nullptr);
+                       xcd_pk, nullptr, nullptr, nullptr);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;
@@ -598,17 +653,17 @@ template <int KD>
 int launch_scores_d(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                     const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                     int64_t H, int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c,
-                    uint32_t *stats, float *bounds, float *kmax, hipStream_t stream) {
+                    uint32_t *stats, float *bounds, float *kmax, uint32_t *row_counts, hipStream_t stream) {
   switch (H) {
     case 16:
       return launch_scores_ht<1, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, stream);
     case 32:
       return launch_scores_ht<2, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, stream);
     case 64:
       return launch_scores_ht<4, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, stream);
     default:
       return fail(KS_ERR_INVALID, "indexer scores: H=%lld, supported: 16, 32, 64", (long long)H);
   }
@@ -616,17 +671,21 @@ int launch_scores_d(const uint16_t *q, const uint16_t *k, const void *w, int w_b
 
 }  // namespace
 
+bool scores_count_rows(int64_t B, int64_t S, int64_t T) {
+  return ceil_div(T, kKR) * ceil_div(S, kQW) * B <= kScoreCountGrid;
+}
+
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
                           int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds,
-                          float *kmax) {
+                          float *kmax, uint32_t *row_counts) {
   if (D == 128)
     return launch_scores_d<128>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                                bound_c, stats, bounds, kmax, stream);
+                                bound_c, stats, bounds, kmax, row_counts, stream);
   if (D == 64)
     return launch_scores_d<64>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                               bound_c, stats, bounds, kmax, stream);
+                               bound_c, stats, bounds, kmax, row_counts, stream);
   return fail(KS_ERR_INVALID, "indexer scores: D=%lld, supported: 64, 128", (long long)D);
 }
 
@@ -687,19 +746,23 @@ extern "C" int ks_dbg_indexer_scores(const uint16_t *q, const uint16_t *k, const
 }
 
 // Diagnostic variant of the bounded score kernel (not part of the public header), for timing it alone:
-// as ks_dbg_indexer_scores with fp32 weights, 64 heads and D = 128, plus the per-score bounds [B, S, T]
-// and the key-block norm maxima [B, ceil(T / 256)].
+// as ks_dbg_indexer_scores with fp32 weights, 64 heads and D = 128, plus the per-score bounds [B, S, T],
+// the key-block norm maxima [B, ceil(T / 256)] and the bounded selection's workspace part
+// (ks_dbg_topk_bounded_slots(B S, T) 64-bit slots).  Where the fused entry counts the rows in the score
+// kernel (ks::scores_count_rows), so does this one, into part's count region, which must then be zero.
 extern "C" int ks_dbg_indexer_scores_bounded(const uint16_t *q, const uint16_t *k, const float *w,
                                              const float *q_norm, const int32_t *q_span, const float *k_norm,
                                              const int32_t *k_span, float *scores, float *bounds, float *kmax,
-                                             int64_t B, int64_t S, int64_t T, int32_t causal, int64_t start_pos,
-                                             void *stream) {
+                                             uint64_t *part, int64_t B, int64_t S, int64_t T, int32_t causal,
+                                             int64_t start_pos, void *stream) {
   ks::last_error().clear();
   int rc = check_scores_args(q, k, w, q_norm, q_span, k_norm, k_span, scores, B, S, 64, 128, T, T, 1, start_pos);
   if (rc != KS_OK) return rc;
-  KS_CHECK_ARG(bounds && kmax, "ks_dbg_indexer_scores_bounded: null pointer");
+  KS_CHECK_ARG(bounds && kmax && part, "ks_dbg_indexer_scores_bounded: null pointer");
+  KS_CHECK_ARG(T <= 32768, "ks_dbg_indexer_scores_bounded: T <= 32768");
   if (B * S == 0) return KS_OK;
   return ks::launch_indexer_scores(q, k, w, 0, q_norm, q_span, k_norm, k_span, scores, B, S, 64, 128, T, T,
                                    causal ? 1 : 0, start_pos, 1, ks::kScoreBoundC, nullptr,
-                                   static_cast<hipStream_t>(stream), bounds, kmax);
+                                   static_cast<hipStream_t>(stream), bounds, kmax,
+                                   ks::scores_count_rows(B, S, T) ? ks::topk_bounded_counts(part, B * S, T) : nullptr);
 }

@@ -28,13 +28,8 @@ constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / 64;
 constexpr int kTopkMaxK = 4096;
 
-// fp32 -> uint32 whose unsigned order equals the float order; -0 is canonicalised to +0.
-// Key 0 is reserved for "absent" (it would be a negative NaN, which is outside the contract).
-__device__ __forceinline__ uint32_t score_key(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) == 0) u = 0;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
+// score_key (indexer_common.h): key 0 is reserved for "absent" (it would be a negative NaN, which is outside the
+// contract).
 
 // Inclusive prefix sum over the 64 lanes of a wave with DPP: row shifts by 1, 2, 4, 8 within each 16-lane
 // row, then the last lane of row 0 / row 2 broadcast into rows 1 / 3 and lane 31 into rows 2-3.  Lanes
@@ -526,7 +521,7 @@ __device__ __forceinline__ void wave_min_max(uint32_t &mn, uint32_t &mx) {
 
 // ---------------------------------------------------------------- rows of bounded scores
 // Bounded scores S with bounds U (the exact score lies in [S - U, S + U]; U = 0 exactly when S is exact) are
-// selected in three launches:
+// selected in three launches (two where the score kernel has counted the rows, TopkRecompute::counted):
 //  1. topk_slice_hist_kernel, workgroup (row, slice): counts of the first 11-bit digit (2048 buckets) of the lower
 //     ends S - U of the slice's columns.
 //  2. topk_recompute_kernel, workgroup (row, segment): the threshold tau from the row's summed counts (the lower
@@ -1160,7 +1155,8 @@ int ks::launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_
   if (rows == 0) return KS_OK;
   const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
   const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
-  const int np = topk_slices(rows, Ti);
+  // counted: the score kernel has counted each row whole (one slice); otherwise the histogram launch counts slices
+  const int np = rc.counted ? 1 : topk_slices(rows, Ti);
   int W = kTopkThreads;  // columns per histogram slice: 1024 times a power of two
   while (W * np < Ti) W <<= 1;
   const int NP = (Ti + W - 1) / W;
@@ -1180,20 +1176,22 @@ int ks::launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_
   uint32_t *hists = reinterpret_cast<uint32_t *>(rc.part + rows * cap);
   uint32_t *rstate = hists + rows * NP * 2048;
   const float *bnd = rc.bounds;
-  const dim3 hgrid(static_cast<unsigned>(rows), static_cast<unsigned>(NP));
+  if (!rc.counted) {
+    const dim3 hgrid(static_cast<unsigned>(rows), static_cast<unsigned>(NP));
 #define KS_HIST(KPT_)                                                                                          \
   hipLaunchKernelGGL(topk_slice_hist_kernel<KPT_>, hgrid, dim3(kTopkThreads), 0, st, scores, bnd, ld, S, Ti, c, \
                      start_pos, ratio, W, hists, rstate)
-  switch (W / kTopkThreads) {
-    case 1: KS_HIST(1); break;
-    case 2: KS_HIST(2); break;
-    case 4: KS_HIST(4); break;
-    case 8: KS_HIST(8); break;
-    case 16: KS_HIST(16); break;
-    default: KS_HIST(32); break;
-  }
+    switch (W / kTopkThreads) {
+      case 1: KS_HIST(1); break;
+      case 2: KS_HIST(2); break;
+      case 4: KS_HIST(4); break;
+      case 8: KS_HIST(8); break;
+      case 16: KS_HIST(16); break;
+      default: KS_HIST(32); break;
+    }
 #undef KS_HIST
-  KS_CHECK_LAUNCH("topk_slice_hist_kernel");
+    KS_CHECK_LAUNCH("topk_slice_hist_kernel");
+  }
   const dim3 rgrid(static_cast<unsigned>(rows * segs));
 #define KS_REC(KPB_)                                                                                             \
   hipLaunchKernelGGL(topk_recompute_kernel<KPB_>, rgrid, dim3(kRecThreads), 0, st, scores, ld, S, Ti, ki, c, start_pos, \
@@ -1218,6 +1216,12 @@ int ks::launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_
   return KS_OK;
 }
 
+uint32_t *ks::topk_bounded_counts(uint64_t *part, int64_t rows, int64_t T) {
+  // the lists first (rows x cap composites), then one slice of counts per row and the row states, as the
+  // launcher lays them out for NP = 1
+  return reinterpret_cast<uint32_t *>(part + rows * topk_list_cap(static_cast<int>(T)));
+}
+
 int64_t ks::topk_bounded_part_capacity(int64_t rows, int64_t T) {
   if (rows <= 0 || T < 1 || T > 32768) return 0;
   const int Ti = static_cast<int>(T);
@@ -1230,7 +1234,9 @@ int64_t ks::topk_bounded_part_capacity(int64_t rows, int64_t T) {
 // Diagnostic entry (not part of the public header) of the bounded top-k, for timing it alone: scores and
 // bounds from ks_dbg_indexer_scores_bounded over rotated q / k (with their row statistics); the scores that
 // are recomputed are rewritten in place (bound 0).  ratio 1, int32 output.  part: part_cap 64-bit slots, at
-// least ks_dbg_topk_bounded_slots(B S, T) of them.
+// least ks_dbg_topk_bounded_slots(B S, T) of them, holding, where the fused entry counts the rows in the score
+// kernel (ks::scores_count_rows), the counts that ks_dbg_indexer_scores_bounded accumulated into its zeroed
+// count region; otherwise the selection counts the rows itself (its histogram launch).
 extern "C" int ks_dbg_indexer_topk_bounded(float *scores, float *bounds, const float *kmax, const uint16_t *q,
                                            const uint16_t *k, const float *w, const float *q_norm,
                                            const int32_t *q_span, const float *k_norm, const int32_t *k_span,
@@ -1242,7 +1248,7 @@ extern "C" int ks_dbg_indexer_topk_bounded(float *scores, float *bounds, const f
                "ks_dbg_indexer_topk_bounded: null pointer");
   KS_CHECK_ARG(T <= 32768 && k_top <= 2048, "ks_dbg_indexer_topk_bounded: T <= 32768 and k <= 2048");
   const ks::TopkRecompute rc{bounds, kmax, q, k, w, q_norm, q_span, k_norm, k_span, T, ks::kScoreBoundC, nullptr, 0,
-                             part, part_cap};
+                             part, part_cap, ks::scores_count_rows(B, S, T) ? 1 : 0};
   return ks::launch_indexer_topk_bounded(scores, T, B, S, T, k_top, causal ? 1 : 0, start_pos, 1, 0, out, 0, rc,
                                          static_cast<hipStream_t>(stream));
 }

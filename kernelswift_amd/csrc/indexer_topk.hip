@@ -21,6 +21,8 @@
 #include "indexer_common.h"
 #include "indexer_exact.h"
 
+#include <type_traits>
+
 namespace ks {
 namespace {
 
@@ -544,6 +546,7 @@ struct RecShared {
   uint4 q[kRecH * kRecC];
   float w[kRecH];
   float qn[kRecH];
+  float qd[kRecH];  // bound_c 2^-23 (qn + 2^-122): the per-head factor of the interval half-widths
   int32_t qsp[kRecH];
 };
 
@@ -568,7 +571,7 @@ struct RecWave {
 // canonical order over the corrected values.
 template <int NW>
 __device__ void recompute_scores(int32_t *list, int n, float *srow, float *urow, const TopkRecompute &rc,
-                                 const RecShared &rs, RecWave &rw, int64_t kbrow0, int64_t kmax_row0,
+                                 const RecShared &rs, RecWave &rw, int64_t kbrow0, int64_t kmax_row0, float qpmax,
                                  uint32_t &n_exact, uint32_t &n_unres) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
@@ -589,6 +592,13 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, float *urow,
     rw.ksp[l16] = ksv;  // the four lanes of a key write the same span; read by the near-tie dots below
     uint32_t pl[8];     // relu'd lower ends, heads 16m + 4g + (0, 1) | (2, 3): pl[2m], pl[2m + 1]
     uint32_t ntm = 0;   // bit 4m + r: head 16m + 4g + r is a near tie
+    // Interval half-widths: one fma per dot from the per-head factor qd (two roundings, within the three that
+    // the bound constant allows for evaluating the width, so the width still bounds the MFMA error; it need not
+    // equal the score kernel's, since any valid width certifies the same exact values).  When the query's
+    // largest padded norm times a key block's reaches 2^126 (uniform over the wave, and rare), the MFMA may
+    // overflow: every dot of the tile is then taken as a near tie and computed exactly.
+    const float kp = knm + 0x1p-122f;
+    const bool overflow = __builtin_amdgcn_ballot_w64(!(qpmax * kp < 0x1p126f)) != 0ull;
 #pragma unroll
     for (int m = 0; m < kRecH / 16; ++m) {
       f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -597,17 +607,16 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, float *urow,
 #pragma unroll
       for (int rp = 0; rp < 2; ++rp) {
         const int h0 = 16 * m + 4 * g + 2 * rp;
-        const float d0 = dot_halfwidth(rs.qn[h0], knm, rc.bound_c), d1 = dot_halfwidth(rs.qn[h0 + 1], knm, rc.bound_c);
+        const float d0 = __builtin_fmaf(rs.qd[h0], kp, 0x1p-144f), d1 = __builtin_fmaf(rs.qd[h0 + 1], kp, 0x1p-144f);
         const uint32_t lo = cvt_relu_pk(acc[2 * rp] - d0, acc[2 * rp + 1] - d1);
         const uint32_t hi = cvt_relu_pk(acc[2 * rp] + d0, acc[2 * rp + 1] + d1);
         pl[2 * m + rp] = lo;
         const uint32_t x = lo ^ hi;
-        // an infinite half-width (norms that could overflow inside the MFMA) makes the dot a near tie even
-        // when A itself is not finite
-        ntm |= (((x & 0xFFFFu) != 0u || d0 == __builtin_inff()) && kv ? 1u : 0u) << (4 * m + 2 * rp);
-        ntm |= (((x >> 16) != 0u || d1 == __builtin_inff()) && kv ? 1u : 0u) << (4 * m + 2 * rp + 1);
+        ntm |= ((x & 0xFFFFu) != 0u && kv ? 1u : 0u) << (4 * m + 2 * rp);
+        ntm |= ((x >> 16) != 0u && kv ? 1u : 0u) << (4 * m + 2 * rp + 1);
       }
     }
+    if (overflow) ntm = kv ? 0xFFFFu : 0u;
     if (__builtin_amdgcn_ballot_w64(ntm != 0u) != 0ull) {
       const uint32_t cnt = __builtin_popcount(ntm);
       const uint32_t incl = wave_incl_scan(cnt);
@@ -859,7 +868,14 @@ __global__ __launch_bounds__(kRecThreads) void topk_recompute_kernel(float *scor
   }
   rs.w[hh] = wv;  // four threads write each head entry, the same values
   rs.qn[hh] = qnv;
+  rs.qd[hh] = rc.bound_c * 0x1p-23f * (qnv + 0x1p-122f);
   rs.qsp[hh] = qsv;
+  // the query's largest padded head norm (lane h of every wave holds head h): decides per tile whether the
+  // one-fma half-widths apply
+  float qpmax = qnv + 0x1p-122f;
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) qpmax = fmaxf(qpmax, __shfl_xor(qpmax, d, 64));
+  qpmax = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int32_t, qpmax)));
 
   // ---- tau: bucket e of the thread's kBPT is 2048 - kBPT (tid + 1) + e (the top one is e = kBPT - 1)
   uint32_t hc[kBPT];
@@ -927,7 +943,7 @@ __global__ __launch_bounds__(kRecThreads) void topk_recompute_kernel(float *scor
   if (ncand > 0) {
     const int64_t kbrow0 = b * rc.kbs;
     const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
-    recompute_scores<kRecWaves>(list, static_cast<int>(ncand), srow, urow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0,
+    recompute_scores<kRecWaves>(list, static_cast<int>(ncand), srow, urow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0, qpmax,
                                 n_exact, n_unres);
     __syncthreads();  // every recomputed score is in its list slot
   }

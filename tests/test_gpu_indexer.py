@@ -451,6 +451,29 @@ def test_indexer_bounded_recompute_everything(device, S, T, k_top, start_pos):
     assert st[0] > 0 and st[1] == 0
 
 
+def test_indexer_bounded_norms_beyond_overflow_guard(device):
+    # the bounded path on rows whose norm products reach 2^126 (the MFMA could overflow): the score kernel gives
+    # such waves infinite bounds, and the recomputation takes every dot of a tile whose key block reaches the
+    # guard as a near tie and computes it exactly
+    g = torch.Generator().manual_seed(19)
+    S, T = 4, 160
+    q = torch.zeros(1, S, 64, 128)
+    idx = torch.randint(0, 128, (S, 64, 3), generator=g)
+    for s in range(S):
+        for h in range(64):
+            q[0, s, h, idx[s, h]] = torch.randn(3, generator=g) * 2.0 ** 62
+    k = torch.randn(1, T, 128, generator=g)
+    k[0, ::7] = k[0, ::7] * 2.0 ** 62
+    q, k = q.bfloat16(), k.bfloat16()
+    w = (torch.rand(1, S, 64, generator=g) + 0.5) * 2.0 ** -30
+    tab = workloads.freqs_table(64, T + 1)
+    print("[case] bounded path beyond the overflow guard", flush=True)
+    got, st = _dbg_indexer(q, k, w, tab, 32, False, 0, 2)
+    want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), 32, False, 0, 1, 0, 0, 64, True)
+    np.testing.assert_array_equal(got, want)
+    assert st[0] > 0
+
+
 @pytest.mark.parametrize("dist", ["normal", "scaled", "midpoints"])
 def test_indexer_bounded_equals_exact_path(device, dist):
     # the two score paths select identical indices (and both equal the oracle's)

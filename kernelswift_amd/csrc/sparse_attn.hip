@@ -67,13 +67,17 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t *p) {
 }
 
 // A wave-uniform pointer moved to SGPRs (the compiler cannot prove uniformity of values derived from the
-// wave index).
+// wave index).  The result is typed as a global-memory pointer: rebuilt from an integer, a generic pointer
+// would make its loads flat loads, which also count in lgkmcnt, so every wait for an LDS read would then
+// wait for them too.
 template <typename T>
-__device__ __forceinline__ T *uniform_ptr(T *p) {
+using global_ptr = __attribute__((address_space(1))) T *;
+template <typename T>
+__device__ __forceinline__ global_ptr<T> uniform_ptr(T *p) {
   const uint64_t v = reinterpret_cast<uint64_t>(p);
   const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
   const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<T *>((static_cast<uint64_t>(hi) << 32) | lo);
+  return reinterpret_cast<global_ptr<T>>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // Reductions over the four 16-lane rows of the wave (lanes l, l^16, l^32, l^48), result in every lane:
@@ -191,8 +195,8 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
   const bool head_ok = item_ok && head < H;
   const int k_begin = split * KR;  // K < 2^31 (host-checked): key positions fit int32
   const int k_end = item_ok ? (k_begin + KR < K ? k_begin + KR : static_cast<int>(K)) : k_begin;
-  const int32_t *irow = uniform_ptr(idx + qm * K);
-  const uint16_t *kvb = uniform_ptr(kv + b * N * DQK);
+  const global_ptr<const int32_t> irow = uniform_ptr(idx + qm * K);
+  const global_ptr<const uint16_t> kvb = uniform_ptr(kv + b * N * DQK);
   const int nch = (KR + kKC - 1) / kKC;  // the same for every group of the workgroup
 
   // DMA slot 64 (gw + GW i) + lane of a chunk holds unit u_i of key key_i (fixed per lane).
@@ -224,12 +228,17 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
       if (jj < Sh::TI) {
         const bool ok = (vm >> key_i[i]) & 1u;
         const uint32_t voff = static_cast<uint32_t>(ok ? raw[i] : 0) * (DQK * 2) + uoff_i[i];
-        dma16(kvb, voff, kb_lds + (buf * Sh::BUF + 64 * jj * 8) * 2);
+        dma16((const void *)kvb, voff, kb_lds + (buf * Sh::BUF + 64 * jj * 8) * 2);
       }
     }
   };
 
-  // q B-fragments: Q[head][32j + 8g .. +7]
+  // chunk 0's indices first, then the q B-fragments (Q[head][32j + 8g .. +7]): the first gather waits for the
+  // indices alone and is in flight with the q loads
+  int32_t nraw[NJ];
+#pragma unroll
+  for (int i = 0; i < NJ; ++i) nraw[i] = raw_idx(0, key_i[i]);
+  int32_t nvraw = raw_idx(0, lane & 31);
   uint4 qf[QREG];
 #pragma unroll
   for (int j = 0; j < QJ; ++j) {
@@ -238,11 +247,6 @@ __global__ __launch_bounds__((SaShape<DQK, DV, GW>::THREADS)) void sparse_attn_k
     if (j < QREG) qf[j < QREG ? j : 0] = v;
     else qs[grp][gw][j - QREG][lane] = v;
   }
-
-  int32_t nraw[NJ];
-#pragma unroll
-  for (int i = 0; i < NJ; ++i) nraw[i] = raw_idx(0, key_i[i]);
-  int32_t nvraw = raw_idx(0, lane & 31);
   uint32_t vm_cur = valid_mask(0, nvraw);
   gather(nraw, vm_cur, 0);
   const int c1 = nch > 1 ? 1 : 0;
@@ -617,19 +621,24 @@ __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
   const int k_begin = split * KR;
   const int k_end = k_begin + KR < K ? k_begin + KR : static_cast<int>(K);
   const int nch = (k_end - k_begin + kKC - 1) / kKC;  // >= 1: every range of the plan is non-empty
-  const uint16_t *kvb = uniform_ptr(kv + b * N * Sh::DQK);
+  const global_ptr<const uint16_t> kvb = uniform_ptr(kv + b * N * Sh::DQK);
 
-  // ---- stage the item's row indices (validated: -1 = outside the range or not in [0, N))
+  // ---- the item's row indices and the q B-fragments are loaded together (one round trip): the indices
+  // first, unrolled (wave-uniform guards, positions clamped into the range), so that staging them waits for
+  // them alone; q: Q[head][32j + 8g .. +7] with head = 32 wave + 16 ht + l16 for both head tiles, all in VGPRs
+  // (the k-steps past QREG, if any, in LDS)
+  constexpr int kIPT = (Sh::KR_MAX + Sh::THREADS - 1) / Sh::THREADS;
+  const int ntot = nch * kKC;  // <= KR_MAX (host-checked range length, rounded up to whole chunks)
+  int32_t iraw[kIPT];
   {
     const int32_t *irow = idx + qm * K;
-    for (int t = tid; t < nch * kKC; t += Sh::THREADS) {
-      const int pos = k_begin + t;
-      const int32_t v = pos < k_end ? irow[pos] : -1;
-      sidx[t] = (v >= 0 && v < N) ? v : -1;
+#pragma unroll
+    for (int i = 0; i < kIPT; ++i) {
+      const int pos = k_begin + tid + i * Sh::THREADS;
+      iraw[i] = -1;
+      if (i * Sh::THREADS < ntot) iraw[i] = irow[pos < k_end ? pos : k_end - 1];
     }
   }
-  // ---- q B-fragments of both head tiles, Q[head][32j + 8g .. +7] with head = 32 wave + 16 ht + l16, all in
-  // VGPRs (the k-steps past QREG, if any, in LDS)
   uint4 qf[2][QREG];
 #pragma unroll
   for (int ht = 0; ht < 2; ++ht) {
@@ -640,6 +649,12 @@ __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
       if (j < QREG) qf[ht][j < QREG ? j : 0] = v;
       else qs[((wave * QL + (j < QREG ? 0 : j - QREG)) * 2 + ht) * 64 + lane] = v;
     }
+  }
+  // staged validated (-1 = outside the range or not in [0, N))
+#pragma unroll
+  for (int i = 0; i < kIPT; ++i) {
+    const int t = tid + i * Sh::THREADS;
+    if (t < ntot) sidx[t] = (k_begin + t < k_end && iraw[i] >= 0 && iraw[i] < N) ? iraw[i] : -1;
   }
   // the q loads complete here, not at their first use inside the loop (where the wait would also drain
   // the gathers in flight on every iteration)
@@ -673,7 +688,7 @@ __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
         const int key = sl / UPR;
         const uint32_t voff =
             static_cast<uint32_t>(r[i] < 0 ? 0 : r[i]) * (Sh::DQK * 2) + ((sl % UPR) ^ (key & 7)) * 16;
-        dma16(kvb, voff, kb_lds + (buf * Sh::BUF + 64 * jj * 8) * 2);
+        dma16((const void *)kvb, voff, kb_lds + (buf * Sh::BUF + 64 * jj * 8) * 2);
       }
     }
   };

@@ -1,11 +1,17 @@
-"""No kernel of the library reads the AQL dispatch packet (CPU: hipcc cross-compiles every source).
+"""No kernel of the library reads the AQL dispatch packet or uses flat memory instructions (CPU: hipcc
+cross-compiles every source).
 
 The dispatch packet lives in the HSA queue's ring buffer in host memory, so a kernel that needs it (for the
 workgroup size: the compiler asks for it when it moves a per-thread array into LDS and must compute the flat
 thread id) makes each workgroup's first scalar load a round trip to the host: one such array in the bounded
 top-k's recomputation delayed every workgroup's first loads by 5-10 us.  The kernel descriptors record the
 request as .amdhsa_user_sgpr_dispatch_ptr; this compiles each source with the library's flags and checks that
-no kernel sets it."""
+no kernel sets it.
+
+Flat loads and stores count in lgkmcnt as well as vmcnt, so every wait for an LDS read (lgkmcnt(0) before an
+LDS-fed MFMA) also waits for them: one pointer rebuilt from an integer, which the compiler treats as generic,
+turned a sparse-attention kernel's index prefetch into flat loads that stalled each chunk's LDS reads.  The
+same compile checks that no kernel contains a flat memory instruction."""
 import concurrent.futures
 import glob
 import os
@@ -29,16 +35,29 @@ def dispatch_ptr_kernels(asm: str):
     return out
 
 
+def flat_memory_kernels(asm: str):
+    """Names of the kernels whose code contains a flat load, store or atomic."""
+    out = []
+    for m in re.finditer(r"^(\w+):\s*$(.*?)^\.Lfunc_end", asm, re.S | re.M):
+        if re.search(r"^\s+flat_(load|store|atomic)", m.group(2), re.M):
+            out.append(m.group(1))
+    return out
+
+
 def test_checker_pins():
     desc = ("\t.amdhsa_kernel _Za\n\t\t.amdhsa_user_sgpr_dispatch_ptr 1\n\t\t.amdhsa_user_sgpr_queue_ptr 0\n"
             "\t.end_amdhsa_kernel\n\t.amdhsa_kernel _Zb\n\t\t.amdhsa_user_sgpr_dispatch_ptr 0\n"
             "\t.end_amdhsa_kernel\n")
     assert dispatch_ptr_kernels(desc) == ["_Za"]
+    code = ("_Za:\n\tglobal_load_dword v1, v[2:3], off\n.Lfunc_end0:\n"
+            "_Zb:\n\tflat_load_dword v1, v[2:3]\n.Lfunc_end1:\n"
+            "_Zc:\n\tds_read_b32 v1, v2\n\tflat_store_dword v[2:3], v1\n.Lfunc_end2:\n")
+    assert flat_memory_kernels(code) == ["_Zb", "_Zc"]
 
 
 @pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
                     reason="hipcc is not installed")
-def test_no_kernel_reads_the_dispatch_packet(tmp_path):
+def test_no_dispatch_packet_reads_or_flat_memory(tmp_path):
     sys.path.insert(0, REPO)
     from kernelswift_amd import build as ksbuild
     srcs = sorted(glob.glob(os.path.join(REPO, "kernelswift_amd", "csrc", "*.hip")))
@@ -49,9 +68,11 @@ def test_no_kernel_reads_the_dispatch_packet(tmp_path):
         r = subprocess.run([ksbuild.HIPCC, *ksbuild.COMMON, "--cuda-device-only", "-S", src, "-o", str(out)],
                            capture_output=True, text=True)
         assert r.returncode == 0, r.stderr[-2000:]
-        return src, dispatch_ptr_kernels(out.read_text())
+        asm = out.read_text()
+        return src, dispatch_ptr_kernels(asm), flat_memory_kernels(asm)
 
     with concurrent.futures.ThreadPoolExecutor(max_workers=4) as ex:
         results = list(ex.map(compile_one, srcs))
-    bad = [f"{os.path.basename(src)}: {k}" for src, ks in results for k in ks]
+    bad = [f"{os.path.basename(src)}: {k} (dispatch pointer)" for src, ks, _ in results for k in ks]
+    bad += [f"{os.path.basename(src)}: {k} (flat memory instruction)" for src, _, fl in results for k in fl]
     assert bad == [], "\n".join(bad)

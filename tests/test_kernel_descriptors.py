@@ -36,10 +36,13 @@ def dispatch_ptr_kernels(asm: str):
 
 
 def flat_memory_kernels(asm: str):
-    """Names of the kernels whose code contains a flat load, store or atomic."""
+    """Names of the kernels (entry points with a kernel descriptor) whose own code contains a flat load, store
+    or atomic.  Non-inlined device functions are not checked: their pointer parameters are generic by nature,
+    and the library calls them only on rare paths (the integer-accumulator exact dot, the merge-sort fallback)."""
+    kernels = set(re.findall(r"\.amdhsa_kernel (\S+)", asm))
     out = []
-    for m in re.finditer(r"^(\w+):\s*$(.*?)^\.Lfunc_end", asm, re.S | re.M):
-        if re.search(r"^\s+flat_(load|store|atomic)", m.group(2), re.M):
+    for m in re.finditer(r"^(\w+):[^\n]*\n(.*?)^\.Lfunc_end", asm, re.S | re.M):
+        if m.group(1) in kernels and re.search(r"^\s+flat_(load|store|atomic)", m.group(2), re.M):
             out.append(m.group(1))
     return out
 
@@ -49,9 +52,12 @@ def test_checker_pins():
             "\t.end_amdhsa_kernel\n\t.amdhsa_kernel _Zb\n\t\t.amdhsa_user_sgpr_dispatch_ptr 0\n"
             "\t.end_amdhsa_kernel\n")
     assert dispatch_ptr_kernels(desc) == ["_Za"]
-    code = ("_Za:\n\tglobal_load_dword v1, v[2:3], off\n.Lfunc_end0:\n"
-            "_Zb:\n\tflat_load_dword v1, v[2:3]\n.Lfunc_end1:\n"
-            "_Zc:\n\tds_read_b32 v1, v2\n\tflat_store_dword v[2:3], v1\n.Lfunc_end2:\n")
+    code = ("_Za:                  ; @_Za\n\tglobal_load_dword v1, v[2:3], off\n.Lfunc_end0:\n"
+            "_Zb:                  ; @_Zb\n\tflat_load_dword v1, v[2:3]\n.Lfunc_end1:\n"
+            "_Zc:\n\tds_read_b32 v1, v2\n\tflat_store_dword v[2:3], v1\n.Lfunc_end2:\n"
+            "_Zf:\n\tflat_load_dword v1, v[2:3]\n.Lfunc_end3:\n"
+            "\t.amdhsa_kernel _Za\n\t.end_amdhsa_kernel\n\t.amdhsa_kernel _Zb\n\t.end_amdhsa_kernel\n"
+            "\t.amdhsa_kernel _Zc\n\t.end_amdhsa_kernel\n")
     assert flat_memory_kernels(code) == ["_Zb", "_Zc"]
 
 

@@ -800,7 +800,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_slice_hist_kernel(const flo
 //    taken from the row's length counter; the row state also receives tau and the largest key appended.
 // Row state (4 x 32 bits per row): list length, tau, largest key, unused.
 template <int KPB>
-__global__ __launch_bounds__(kRecThreads) void topk_recompute_kernel(float *scores, int64_t ld, int64_t S, int T,
+__global__ __launch_bounds__(kRecThreads, 4) void topk_recompute_kernel(float *scores, int64_t ld, int64_t S, int T,
                                                                     int k, int causal, int64_t start_pos, int ratio,
                                                                     TopkRecompute rc, int segs, int NP,
                                                                     const uint32_t *__restrict__ hists,
@@ -918,25 +918,36 @@ __global__ __launch_bounds__(kRecThreads) void topk_recompute_kernel(float *scor
   const uint32_t tau = s_tau;
   if (seg == 0 && tid == 0) rstate[4 * row + 1] = tau;
 
-  // ---- the segment's candidates (U > 0, upper end >= tau) and its exact keys >= tau
-  uint32_t hik[KPB], cmask = 0;
+  // ---- the segment's candidates (U > 0, upper end >= tau) and its list slots: every column whose upper end
+  // reaches tau (the candidates, and the exact scores >= tau) gets a slot, counted before the recomputation so
+  // that one block scan counts both (candidates in the low 16 bits, slots in the high 16: at most SW <= 4096 of
+  // each per workgroup) and the reservation is made as soon as a wave's own recomputation ends; a candidate whose
+  // exact score falls below tau leaves its slot empty (key 0, which the rank store skips).
+  // (few registers stay live across the recomputation: the masks share one word, the bases another, and the
+  // largest upper end is taken from hik afterwards)
+  uint32_t hik[KPB], masks = 0;  // bit j: column j is a candidate; bit 8 + j: it has a slot
+  static_assert(KPB <= 8, "masks of up to 8 columns per thread");
 #pragma unroll
   for (int j = 0; j < KPB; ++j) {
     const bool v = j * kRecThreads + tid < nv;
     const uint32_t lo = score_key(uv[j] > 0.f ? sv[j] - uv[j] : sv[j]);
     hik[j] = v ? score_key(uv[j] > 0.f ? sv[j] + uv[j] : sv[j]) : 0u;
-    if (v && lo != hik[j] && hik[j] >= tau) cmask |= 1u << j;
+    if (v && hik[j] >= tau) masks |= (lo != hik[j] ? 0x101u : 0x100u) << j;
   }
-  const uint32_t ccnt = __builtin_popcount(cmask);
-  const uint32_t cbase = block_inclusive_scan<true, kRecWaves>(ccnt, wsum) - ccnt;
-  uint32_t ncand = 0;
+  static_assert(SW < 65536, "candidate and slot counts share a 32-bit scan");
+  const uint32_t both = __builtin_popcount(masks & 0xFFu) | (__builtin_popcount(masks >> 8) << 16);
+  const uint32_t bexcl = block_inclusive_scan<true, kRecWaves>(both, wsum) - both;  // slots << 16 | candidates
+  uint32_t ncand = 0, nres = 0;
 #pragma unroll
-  for (int w = 0; w < kRecWaves; ++w) ncand += wsum[w];
+  for (int w = 0; w < kRecWaves; ++w) {
+    ncand += wsum[w] & 0xFFFFu;
+    nres += wsum[w] >> 16;
+  }
   {
-    uint32_t p = cbase;
+    uint32_t p = bexcl & 0xFFFFu;
 #pragma unroll
     for (int j = 0; j < KPB; ++j)
-      if ((cmask >> j) & 1u) list[p++] = c0 + j * kRecThreads + tid;
+      if ((masks >> j) & 1u) list[p++] = c0 + j * kRecThreads + tid;
   }
   __syncthreads();
   uint32_t n_exact = 0, n_unres = 0;
@@ -945,46 +956,38 @@ __global__ __launch_bounds__(kRecThreads) void topk_recompute_kernel(float *scor
     const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
     recompute_scores<kRecWaves>(list, static_cast<int>(ncand), srow, urow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0, qpmax,
                                 n_exact, n_unres);
-    __syncthreads();  // every recomputed score is in its list slot
   }
+  // each wave, its own recomputation done (the atomics wait behind no tile load, and the last wave, which holds
+  // the fewest tiles, makes the reservation while the others finish theirs): the row's largest key, bounded by
+  // the largest upper end, and the workgroup's slots
+  {
+    uint32_t umax = 0, unused = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 0; j < KPB; ++j) umax = ((masks >> (8 + j)) & 1u) && hik[j] > umax ? hik[j] : umax;
+    wave_min_max(unused, umax);
+    if ((tid & 63) == 0 && umax != 0u) atomicMax(&rstate[4 * row + 2], umax);
+  }
+  if (tid == kRecThreads - 1) s_base = nres > 0 ? atomicAdd(&rstate[4 * row], nres) : 0u;
+  __syncthreads();  // every recomputed score is in its list slot, and the reservation's base is known
   if (rc.stats != nullptr) {
     if (n_exact) atomicAdd(&rc.stats[0], n_exact);
     if (n_unres) atomicAdd(&rc.stats[1], n_unres);
     if (rc.stats_ext && tid == 0 && ncand) atomicAdd(&rc.stats[2], ncand);
   }
 
-  // ---- the exact keys >= tau, appended to the row's list
-  uint32_t key[KPB], nemit = 0;
-  {
-    const float *listf = reinterpret_cast<const float *>(list);
-    uint32_t p = cbase;
-#pragma unroll
-    for (int j = 0; j < KPB; ++j) {
-      const bool cj = (cmask >> j) & 1u;
-      key[j] = cj ? score_key(listf[p]) : hik[j];
-      p += cj ? 1u : 0u;
-      // a non-candidate with hik >= tau is exact (U = 0); below tau its key is dropped
-      if (key[j] < tau) key[j] = 0u;
-      nemit += key[j] != 0u ? 1u : 0u;
-    }
-  }
-  {
-    uint32_t mx = 0, unused = 0xFFFFFFFFu;
-#pragma unroll
-    for (int j = 0; j < KPB; ++j) mx = key[j] > mx ? key[j] : mx;
-    wave_min_max(unused, mx);
-    if ((tid & 63) == 0 && mx != 0u) atomicMax(&rstate[4 * row + 2], mx);
-  }
-  const uint32_t ebase = block_inclusive_scan<true, kRecWaves>(nemit, wsum) - nemit;
-  if (tid == kRecThreads - 1) s_base = atomicAdd(&rstate[4 * row], ebase + nemit);
-  __syncthreads();
+  // ---- the reserved slots: the exact key, or 0 where a recomputed score fell below tau
+  const float *listf = reinterpret_cast<const float *>(list);
   uint64_t *dst = lists + row * cap;
-  uint32_t pos = s_base + ebase;
+  uint32_t pos = s_base + (bexcl >> 16), p = bexcl & 0xFFFFu;
 #pragma unroll
   for (int j = 0; j < KPB; ++j) {
-    if (key[j] != 0u) {
+    if ((masks >> (8 + j)) & 1u) {
+      const bool cj = (masks >> j) & 1u;
+      uint32_t key = cj ? score_key(listf[p]) : hik[j];
+      p += cj ? 1u : 0u;
+      if (key < tau) key = 0u;
       const uint32_t col = static_cast<uint32_t>(c0 + j * kRecThreads + tid);
-      if (pos < static_cast<uint32_t>(cap)) dst[pos] = (static_cast<uint64_t>(key[j]) << 32) | static_cast<uint64_t>(~col);
+      if (pos < static_cast<uint32_t>(cap)) dst[pos] = (static_cast<uint64_t>(key) << 32) | static_cast<uint64_t>(~col);
       ++pos;
     }
   }
@@ -1016,7 +1019,7 @@ __device__ bool rank_store(const uint64_t (&v)[PER], int n, uint32_t kmin, uint3
   for (int j = 0; j < PER; ++j) {
     bk[j] = 0u;
     pos[j] = 0u;
-    if (j * kTopkThreads + tid < n) {
+    if (j * kTopkThreads + tid < n && (v[j] >> 32) != 0u) {  // key 0: an empty slot, not ranked
       const uint32_t d = static_cast<uint32_t>(static_cast<float>(static_cast<uint32_t>(v[j] >> 32) - kmin) * scale);
       bk[j] = d < kRankBuckets - 1 ? d : kRankBuckets - 1;
       pos[j] = atomicAdd(&cnt[bk[j]], 1u);  // the entry's place in its bucket (arrival order)
@@ -1031,11 +1034,11 @@ __device__ bool rank_store(const uint64_t (&v)[PER], int n, uint32_t kmin, uint3
   if (__syncthreads_or(c_hi > kRankBucketMax || c_lo > kRankBucketMax)) return false;  // uniform
 #pragma unroll
   for (int j = 0; j < PER; ++j)
-    if (j * kTopkThreads + tid < n) tmp[start[bk[j]] + pos[j]] = v[j];
+    if (j * kTopkThreads + tid < n && (v[j] >> 32) != 0u) tmp[start[bk[j]] + pos[j]] = v[j];
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    if (j * kTopkThreads + tid < n) {
+    if (j * kTopkThreads + tid < n && (v[j] >> 32) != 0u) {
       const uint32_t s0 = start[bk[j]], c = cnt[bk[j]];
       uint32_t r = s0;
 #pragma unroll 4

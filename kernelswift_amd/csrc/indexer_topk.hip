@@ -529,9 +529,10 @@ __device__ __forceinline__ void wave_min_max(uint32_t &mn, uint32_t &mx) {
 //  2. topk_recompute_kernel, workgroup (row, segment): the threshold tau from the row's summed counts (the lower
 //     edge of the bucket holding the row's k-th largest lower end, so no exact score of the top k lies below it);
 //     every score of the segment with U > 0 whose upper end reaches tau is recomputed exactly and written back
-//     (S = exact, U = 0); every exact score >= tau is appended to the row's list as a composite (key, ~column).
+//     (S = exact, U = 0); every column whose upper end reaches tau has a slot in the row's list, which receives
+//     the composite (key, ~column) of its exact score, or key 0 (an empty slot) where that score fell below tau.
 //  3. topk_collected_kernel, one workgroup per row: the list holds every column of the top k, each with its exact
-//     score, so sorting it gives the top k.  A list longer than its capacity falls back to the exact selection over
+//     score, so sorting its nonempty slots gives the top k.  A list longer than its capacity falls back to the exact selection over
 //     the whole row, whose keys are exact wherever they reach tau (the others enter as upper ends, below tau).
 constexpr int kRecD = 128;        // head dim of the recomputation
 constexpr int kRecH = 64;         // heads
@@ -796,9 +797,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_slice_hist_kernel(const flo
 //    from the top bucket finds the bucket holding the row's k-th largest lower end; tau is its lower edge;
 //  - recomputation of the scores with U > 0 whose upper end reaches tau (recompute_scores), written back with
 //    U = 0;
-//  - every exact score >= tau of the segment is appended to the row's list (capacity cap composites) at a base
-//    taken from the row's length counter; the row state also receives tau and the largest key appended.
-// Row state (4 x 32 bits per row): list length, tau, largest key, unused.
+//  - the segment's columns whose upper end reaches tau fill a range of the row's list (capacity cap composites)
+//    reserved on the row's length counter: the exact key of each, or 0 where the exact score fell below tau; the
+//    row state also receives tau and an upper bound of its largest key (the largest upper end).
+// Row state (4 x 32 bits per row): list length (slots reserved), tau, largest key bound, unused.
 template <int KPB>
 __global__ __launch_bounds__(kRecThreads, 4) void topk_recompute_kernel(float *scores, int64_t ld, int64_t S, int T,
                                                                     int k, int causal, int64_t start_pos, int ratio,

@@ -1064,7 +1064,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_collected_kernel(const floa
                                                                      int64_t start_pos, int ratio, int64_t offset,
                                                                      void *__restrict__ out, int out_i64,
                                                                      const uint64_t *__restrict__ lists, int cap,
-                                                                     const uint32_t *__restrict__ rstate) {
+                                                                     int spec, const uint32_t *__restrict__ rstate) {
   extern __shared__ uint64_t cand[];  // 2 cap composites: the list, then the sort's exchange buffers
   __shared__ SelShared sh;
   const int64_t row = blockIdx.x;
@@ -1078,8 +1078,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_collected_kernel(const floa
   }
   const int k_sel = k < n_valid ? k : n_valid;
   if (k_sel > 0) {
-    // the length and the list go out together: the list up to its capacity (the rows' typical length is a
-    // fraction of it; the loads past the length are discarded)
+    // the length and the list's first spec entries go out together (a list rarely runs much past k; the loads
+    // past the length are discarded), the rest of the list once the length asks for it
     const uint4 st = *reinterpret_cast<const uint4 *>(rstate + 4 * row);  // length, tau, largest key
     const uint32_t n = st.x;
     const uint64_t *src = lists + row * cap;
@@ -1088,7 +1088,14 @@ __global__ __launch_bounds__(kTopkThreads) void topk_collected_kernel(const floa
 #pragma unroll
     for (int j = 0; j < kMaxPer; ++j) {
       const int i = j * kTopkThreads + tid;
-      v[j] = src[i < cap ? i : 0];
+      v[j] = 0;
+      if (j * kTopkThreads < spec) v[j] = src[i < cap ? i : 0];  // uniform
+    }
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j) {
+      const int i = j * kTopkThreads + tid;
+      if (j * kTopkThreads >= spec && j * kTopkThreads < static_cast<int>(n < static_cast<uint32_t>(cap) ? n : cap))
+        v[j] = src[i < cap ? i : 0];  // uniform
     }
     if (n >= static_cast<uint32_t>(k_sel) && n <= static_cast<uint32_t>(cap)) {  // uniform
       if (!rank_store<kMaxPer>(v, static_cast<int>(n), st.y, st.z, k_sel, row, k, out, out_i64, causal, limit, offset,
@@ -1223,9 +1230,11 @@ int ks::launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_
 #undef KS_REC
   KS_CHECK_LAUNCH("topk_recompute_kernel");
   const size_t shmem = static_cast<size_t>(2 * cap) * sizeof(uint64_t);
+  // list entries loaded with the length (a multiple of the workgroup): ~1.25 k, which the lists rarely exceed
+  const int spec = static_cast<int>(ceil_div(ki + ki / 4, kTopkThreads) * kTopkThreads);
 #define KS_COLL(KPT_)                                                                                                \
   hipLaunchKernelGGL(topk_collected_kernel<KPT_>, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), shmem, st, \
-                     scores, bnd, ld, S, Ti, ki, c, start_pos, ratio, offset, out, o, lists, cap, rstate)
+                     scores, bnd, ld, S, Ti, ki, c, start_pos, ratio, offset, out, o, lists, cap, spec, rstate)
   if (Ti <= 1024) KS_COLL(1);
   else if (Ti <= 2048) KS_COLL(2);
   else if (Ti <= 4096) KS_COLL(4);

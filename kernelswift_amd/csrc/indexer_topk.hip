@@ -55,8 +55,13 @@ __device__ __forceinline__ uint32_t block_inclusive_scan(uint32_t v, uint32_t *w
   v = wave_incl_scan(v);
   if (lane == 63) wsum[wave] = v;
   __syncthreads();
+  // the preceding waves' totals: every one read at once (a loop to the wave's index would wait for each read)
   uint32_t base = 0;
-  for (int w = 0; w < wave && w < NW; ++w) base += wsum[w];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const uint32_t x = wsum[w];
+    base += w < wave ? x : 0u;
+  }
   if constexpr (TRAIL) __syncthreads();
   return v + base;
 }
@@ -1042,9 +1047,13 @@ __device__ bool rank_store(const uint64_t (&v)[PER], int n, uint32_t kmin, uint3
   for (int j = 0; j < PER; ++j) {
     if (j * kTopkThreads + tid < n && (v[j] >> 32) != 0u) {
       const uint32_t s0 = start[bk[j]], c = cnt[bk[j]];
-      uint32_t r = s0;
-#pragma unroll 4
-      for (uint32_t e = 0; e < c; ++e) r += tmp[s0 + e] > v[j] ? 1u : 0u;
+      uint32_t r = s0, e = 0;
+      // four members per step, read together (one LDS round trip per step, not per member)
+      for (; e + 4 <= c; e += 4) {
+        const uint64_t a0 = tmp[s0 + e], a1 = tmp[s0 + e + 1], a2 = tmp[s0 + e + 2], a3 = tmp[s0 + e + 3];
+        r += (a0 > v[j] ? 1u : 0u) + (a1 > v[j] ? 1u : 0u) + (a2 > v[j] ? 1u : 0u) + (a3 > v[j] ? 1u : 0u);
+      }
+      for (; e < c; ++e) r += tmp[s0 + e] > v[j] ? 1u : 0u;
       if (r < static_cast<uint32_t>(k_sel)) {
         const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[j] & 0xFFFFFFFFull));
         store_index(out, out_i64, row * k + r, col, causal, limit, offset);

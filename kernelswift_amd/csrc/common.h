@@ -58,6 +58,14 @@ __host__ __device__ inline uint16_t f32_to_bf16_rne(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Two fp32 values to a packed bf16 pair (lo in bits 0-15) with the hardware conversion (v_cvt_pk_bf16_f32):
+// RNE, subnormals kept, overflow to infinity; the same results as f32_to_bf16_rne for every non-NaN input.
+typedef float cvt_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 cvt_bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((cvt_f32x2_t{lo, hi}), cvt_bf16x2_t));
+}
+
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 

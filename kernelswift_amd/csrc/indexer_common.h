@@ -54,7 +54,7 @@ __device__ __forceinline__ uint4 rope_chunk(uint4 v, const float2 *__restrict__ 
     const float2 t = tc[p];
     const float y0 = x0 * t.x - x1 * t.y;
     const float y1 = x0 * t.y + x1 * t.x;
-    w[p] = static_cast<uint32_t>(f32_to_bf16_rne(y0)) | (static_cast<uint32_t>(f32_to_bf16_rne(y1)) << 16);
+    w[p] = cvt_pk_bf16(y0, y1);  // one v_cvt_pk_bf16_f32: RNE, subnormals kept, overflow to infinity
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
@@ -69,7 +69,7 @@ __device__ __forceinline__ void chunk_stats(uint4 v, float &ss, int &lsb) {
     for (int h = 0; h < 2; ++h) {
       const uint16_t b = static_cast<uint16_t>(h ? (w[p] >> 16) : (w[p] & 0xFFFFu));
       const float f = bf16_to_f32(b);
-      ss += f * f;
+      ss = __builtin_fmaf(f, f, ss);  // a bound (the norm is rounded up by 2^-12 at the end): any order
       if ((b & 0x7FFFu) != 0) lsb = min(lsb, bf16_lsb_exponent(b));
     }
   }

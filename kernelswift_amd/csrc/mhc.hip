@@ -47,7 +47,7 @@ __device__ __forceinline__ uint4 pack8(const float (&v)[8]) {
   uint32_t w[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p)
-    w[p] = static_cast<uint32_t>(f32_to_bf16_rne(v[2 * p])) | (static_cast<uint32_t>(f32_to_bf16_rne(v[2 * p + 1])) << 16);
+    w[p] = cvt_pk_bf16(v[2 * p], v[2 * p + 1]);
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 

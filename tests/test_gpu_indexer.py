@@ -38,6 +38,21 @@ def test_rope_bit_exact_first_and_last_segments(device):
         np.testing.assert_array_equal(_u16(x), want)
 
 
+@pytest.mark.parametrize("scale", [2.0 ** -128, 2.0 ** -120, 2.0 ** 126])
+def test_rope_bit_exact_extreme_magnitudes(device, scale):
+    # rotated values in the subnormal range (the fp32 products and sums, and the bf16 results) and at the top
+    # of the range (sums that overflow to infinity): the RNE conversion must match the oracle's bit for bit
+    g = torch.Generator().manual_seed(3)
+    q = (torch.randn(2, 17, 4, 128, generator=g) * scale).bfloat16()
+    tab = workloads.freqs_table(64, 4096)
+    print(f"[case] rope scale=2^{np.log2(scale):.0f}", flush=True)
+    x = q.to(device)
+    ops.rope_inplace(x, tab.to(device), rope_start=0, pos0=5)
+    torch.cuda.synchronize()
+    want = oracle.rope_bf16(_u16(q), tab.numpy(), 0, 64, 5)
+    np.testing.assert_array_equal(_u16(x), want)
+
+
 def test_row_stats(device):
     g = torch.Generator().manual_seed(2)
     x = torch.randn(300, 128, generator=g).bfloat16()

@@ -270,8 +270,11 @@ struct ScoresLdsBound {
   float red[kQW];
 };
 
+// The non-counting bound kernel runs grids of several workgroups per CU: at most 168 VGPRs (three waves per SIMD)
+// let the next workgroup start as soon as one wave per SIMD of the current one has finished.
 template <int HT, int KD, bool WBF, bool BOUND, bool COUNT = false>
-__global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu((BOUND && !COUNT) ? 3 : 1))) void
+indexer_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
     const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
@@ -441,10 +444,26 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
       for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv, acc[m]);
     }
   };
+  // the same in two halves (BOUND): the B fragments of a tile are read one tile ahead of its MFMAs
+  auto tile_b = [&](int t, uint4(&bv)[KD / 32]) {
+    const int key_l = 16 * t + l16;
+#pragma unroll
+    for (int kk = 0; kk < KD / 32; ++kk) bv[kk] = L.k[key_l * kC + ((4 * kk + g) ^ (key_l & (kC - 1)))];
+  };
+  auto tile_mfma_b = [&](const uint4(&bv)[KD / 32], f32x4_t(&acc)[HT]) {
+#pragma unroll
+    for (int m = 0; m < HT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KD / 32; ++kk)
+#pragma unroll
+      for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv[kk], acc[m]);
+  };
 
   // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot; pl / ph keep the
-  // interval ends for them
-  auto tile_epilogue = [&](int t, const f32x4_t(&acc)[HT], uint32_t(&pl)[2 * HT], uint32_t(&ph)[2 * HT]) {
+  // interval ends for them.  FC (std::true_type / std::false_type) is the wave's `forced` flag as a constant in
+  // the bound kernels, whose tile loop is compiled once per value, so that no branch splits the epilogue.
+  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], uint32_t(&pl)[2 * HT], uint32_t(&ph)[2 * HT]) {
+    const bool fcd = BOUND ? decltype(FC)::value : forced;
     const int key_l = 16 * t + l16;
     const int key = kb0 + key_l;
     const bool kvalid = key_l < nk;
@@ -461,7 +480,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
         ph[2 * m + rp] = cvt_relu_pk(A0 + d0, A1 + d1);
         anyr |= __builtin_amdgcn_ballot_w64(pl[2 * m + rp] != ph[2 * m + rp]);
       }
-    if (forced) {  // wave-uniform and rare: A may not even be finite; the exact values replace everything
+    if (fcd) {  // wave-uniform and rare: A may not even be finite; the exact values replace everything
 #pragma unroll
       for (int p = 0; p < 2 * HT; ++p) {
         pl[p] = 0u;
@@ -483,6 +502,17 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
           G = __builtin_fmaf(rv, wv[m][r], G);
         }
       }
+    if constexpr (BOUND) {
+      // the next tile's 16 MFMAs (issued before this epilogue, in the same basic block) spread over the interval
+      // test and the head sum, one per 7 VALU instructions: the wave keeps issuing VALU work while the matrix
+      // core runs, instead of stalling on 16 back-to-back MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
+      }
+    }
     const float tot = combine_groups(G);
     const float outv = WBF ? round_bf16_f(tot) : tot;
     if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
@@ -502,7 +532,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
         dpl = mfma16(wa[hh], make_uint4(pl[4 * hh], pl[4 * hh + 1], pl[4 * hh + 2], pl[4 * hh + 3]), dpl);
       }
       float u = (dph[0] - dpl[0]) + 0x1p-16f * (dph[0] + dpl[0]) + 0x1p-21f * fabsf(tot) + 0x1p-100f;
-      if (forced) u = __builtin_inff();  // score 0 with an infinite bound: always recomputed
+      if (fcd) u = __builtin_inff();  // score 0 with an infinite bound: always recomputed
       const bool live_key = kvalid && key < limit;
       const float us = (live_key && ((km >> l16) & 1u)) ? u : 0.f;
       if (g == 0 && kvalid) urow[key] = us;
@@ -521,16 +551,31 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
   // one extra round after the last tile.
   f32x4_t acc[HT], nxt[HT];
   if constexpr (BOUND) {
-    // no deferred keys: two tiles per iteration, alternating the accumulator sets (no copy between them)
-    if (nlive > 0) tile_mfma(0, acc);
-    for (int t = 0; t < nlive; t += 2) {
-      uint32_t pl[2 * HT], ph[2 * HT];
-      if (t + 1 < nlive) tile_mfma(t + 1, nxt);
-      (void)tile_epilogue(t, acc, pl, ph);
-      if (t + 1 < nlive) {
-        if (t + 2 < nlive) tile_mfma(t + 2, acc);
-        (void)tile_epilogue(t + 1, nxt, pl, ph);
+    // no deferred keys: two tiles per iteration, alternating the accumulator sets (no copy between them) and
+    // the B-fragment sets (read one tile ahead).  The MFMAs and reads past the last live tile repeat that tile
+    // (results unused), so that no branch separates them from the epilogue they are interleaved with.
+    auto run = [&](auto FC) {
+      uint4 ba[KD / 32], bb[KD / 32];
+      const int last = nlive - 1;
+      tile_b(0, ba);
+      tile_mfma_b(ba, acc);
+      tile_b(1 < nlive ? 1 : last, bb);
+      for (int t = 0; t < nlive; t += 2) {
+        uint32_t pl[2 * HT], ph[2 * HT];
+        tile_mfma_b(bb, nxt);
+        tile_b(t + 2 < nlive ? t + 2 : last, ba);
+        (void)tile_epilogue(FC, t, acc, pl, ph);
+        if (t + 1 >= nlive) break;
+        tile_mfma_b(ba, acc);
+        tile_b(t + 3 < nlive ? t + 3 : last, bb);
+        (void)tile_epilogue(FC, t + 1, nxt, pl, ph);
       }
+    };
+    if (nlive > 0) {
+      if (forced)
+        run(std::true_type{});
+      else
+        run(std::false_type{});
     }
   }
   if (!BOUND && nlive > 0) tile_mfma(0, acc);
@@ -540,7 +585,7 @@ __global__ __launch_bounds__(kThreads, 1) void indexer_scores_kernel(
     uint32_t km = 0;
     if (live_t) {
       if (t + 1 < nlive) tile_mfma(t + 1, nxt);
-      km = tile_epilogue(t, acc, pl, ph);
+      km = tile_epilogue(std::false_type{}, t, acc, pl, ph);
     }
     if constexpr (BOUND) km = 0u;  // the bound replaces the exact recomputation
     const int cnt = __builtin_popcount(km);

@@ -406,6 +406,23 @@ indexer_scores_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) any_inf = any_inf || dl[m][r] == __builtin_inff();
   const bool forced = __builtin_amdgcn_ballot_w64(any_inf) != 0ull;
+  // BOUND: the tile MFMAs start from -delta instead of 0, so that they return the lower interval end A - delta
+  // without a subtraction, and the upper end is fl((A - delta) + 2 delta).  The accumulation model above applies
+  // to any initial value: the running values now carry -delta, which adds at most 16 (2^-31 + 2^-24) delta
+  // (< 2^-19 delta) to its loss; the lower end needs no fp32 rounding of its own, and the upper end's single
+  // rounding loses at most 2^-24 (|A - delta| + 2 delta), as forming A + delta did.  The constant 13 still
+  // covers the sum (12.07 + 0.5 + 2^-19 + the constant's 3 ulps).
+  // (each -delta passes through an empty asm, so that the compiler cannot rewrite the upper end's fma in terms of
+  // +delta and keep both sets of 16 registers live)
+  f32x4_t negd[HT];
+#pragma unroll
+  for (int m = 0; m < HT; ++m)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = -dl[m][r];
+      asm("" : "+v"(x));
+      negd[m][r] = x;
+    }
 
   // BOUND: A-fragments holding bf16 upper bounds of |w| for the two 32-head halves.  With the relu'd
   // interval ends of a tile as B-fragments (lane (l16, g) holds heads 4g + 0..3 and 16 + 4g + 0..3 of
@@ -444,7 +461,7 @@ indexer_scores_kernel(
       for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv, acc[m]);
     }
   };
-  // the same in two halves (BOUND): the B fragments of a tile are read one tile ahead of its MFMAs
+  // the same in two halves (BOUND, from -delta): the B fragments of a tile are read one tile ahead of its MFMAs
   auto tile_b = [&](int t, uint4(&bv)[KD / 32]) {
     const int key_l = 16 * t + l16;
 #pragma unroll
@@ -452,7 +469,7 @@ indexer_scores_kernel(
   };
   auto tile_mfma_b = [&](const uint4(&bv)[KD / 32], f32x4_t(&acc)[HT]) {
 #pragma unroll
-    for (int m = 0; m < HT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < HT; ++m) acc[m] = negd[m];  // lower ends A - delta
 #pragma unroll
     for (int kk = 0; kk < KD / 32; ++kk)
 #pragma unroll
@@ -475,9 +492,15 @@ indexer_scores_kernel(
 #pragma unroll
       for (int rp = 0; rp < 2; ++rp) {
         const float A0 = acc[m][2 * rp], A1 = acc[m][2 * rp + 1];
-        const float d0 = dl[m][2 * rp], d1 = dl[m][2 * rp + 1];
-        pl[2 * m + rp] = cvt_relu_pk(A0 - d0, A1 - d1);
-        ph[2 * m + rp] = cvt_relu_pk(A0 + d0, A1 + d1);
+        if constexpr (BOUND) {  // A0, A1 are already the lower ends A - delta
+          const float n0 = negd[m][2 * rp], n1 = negd[m][2 * rp + 1];
+          pl[2 * m + rp] = cvt_relu_pk(A0, A1);
+          ph[2 * m + rp] = cvt_relu_pk(__builtin_fmaf(-2.f, n0, A0), __builtin_fmaf(-2.f, n1, A1));
+        } else {
+          const float d0 = dl[m][2 * rp], d1 = dl[m][2 * rp + 1];
+          pl[2 * m + rp] = cvt_relu_pk(A0 - d0, A1 - d1);
+          ph[2 * m + rp] = cvt_relu_pk(A0 + d0, A1 + d1);
+        }
         anyr |= __builtin_amdgcn_ballot_w64(pl[2 * m + rp] != ph[2 * m + rp]);
       }
     if (fcd) {  // wave-uniform and rare: A may not even be finite; the exact values replace everything

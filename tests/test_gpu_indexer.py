@@ -489,6 +489,68 @@ def test_indexer_bounded_norms_beyond_overflow_guard(device):
     assert st[0] > 0
 
 
+def _bounded_scores_gpu(q, k, w, start_pos):
+    """Bound-mode score kernel through the diagnostic export (causal): returns (scores, bounds)."""
+    qd, kd, wd = q.to("cuda"), k.to("cuda"), w.to("cuda")
+    (qn, qs), (kn, ks_) = ops.indexer_row_stats(qd), ops.indexer_row_stats(kd)
+    B, S, H, D = q.shape
+    T = k.shape[1]
+    lib = _lib.load()
+    out = torch.empty(B, S, T, dtype=torch.float32, device="cuda")
+    bnd = torch.empty(B, S, T, dtype=torch.float32, device="cuda")
+    kmax = torch.empty(B, (T + 255) // 256, dtype=torch.float32, device="cuda")
+    part = torch.zeros(lib.ks_dbg_topk_bounded_slots(B * S, T), dtype=torch.int64, device="cuda")
+    rc = lib.ks_dbg_indexer_scores_bounded(qd.data_ptr(), kd.data_ptr(), wd.data_ptr(), qn.data_ptr(), qs.data_ptr(),
+                                           kn.data_ptr(), ks_.data_ptr(), out.data_ptr(), bnd.data_ptr(),
+                                           kmax.data_ptr(), part.data_ptr(), B, S, T, 1, start_pos,
+                                           torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "ks_dbg_indexer_scores_bounded")
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), bnd.cpu().numpy()
+
+
+@pytest.mark.parametrize("dist,S,T", [("normal", 16, 768), ("scaled", 16, 768), ("midpoints", 16, 768),
+                                      ("heavy", 16, 768), ("adversarial", 16, 768), ("normal", 136, 4096)])
+def test_bounded_scores_contain_exact(device, dist, S, T):
+    # the bound-mode score kernel's contract, checked score by score against the oracle's exact scores on the
+    # valid (unmasked) columns: U >= 0, the stored score exact (bit for bit) where U = 0, |exact - S| <= U elsewhere.  The last
+    # shape's grid (17 query groups x 16 key blocks) exceeds one round of the GPU, so it runs the non-counting
+    # form of the kernel; the others run the counting form.
+    g = torch.Generator().manual_seed(41 + S)
+    q = torch.randn(1, S, 64, 128, generator=g)
+    k = torch.randn(1, T, 128, generator=g)
+    if dist == "scaled":
+        q = q * torch.exp2(torch.randint(-8, 9, (1, S, 64, 1), generator=g).float())
+        k = k * torch.exp2(torch.randint(-8, 9, (1, T, 1), generator=g).float())
+    elif dist == "midpoints":
+        q = torch.randint(-3, 4, q.shape, generator=g).float()
+        k = torch.randint(-3, 4, k.shape, generator=g).float()
+    elif dist == "heavy":
+        q, k = q ** 3, k ** 3
+        q = torch.where(q.abs() < 1e-3, torch.zeros_like(q), q)
+        k = torch.where(k.abs() < 1e-3, torch.zeros_like(k), k)
+    q, k = q.bfloat16(), k.bfloat16()
+    w = torch.randn(1, S, 64, generator=g) / 8
+    if dist == "adversarial":  # the MFMA-accumulation pair of test_scores_adversarial_accumulation in query 0
+        q1, k0, k1 = _adversarial_key_pair()
+        q[0, 0, :] = q1
+        k[0, T - 40], k[0, T - 39] = k0, k1
+        w[0, 0] = w[0, 0].abs() + 0.0625
+    start_pos = T - S
+    print(f"[case] bounded scores contain exact {dist} S={S} T={T}", flush=True)
+    got, u = _bounded_scores_gpu(q, k, w, start_pos)
+    want = _oracle_scores(q, k, w, True, start_pos)
+    valid = np.isfinite(want)  # the causal mask; masked columns hold -inf and no bound (never read)
+    assert np.array_equal(np.isfinite(got), valid) and (got[~valid] == -np.inf).all()
+    assert (u[valid] >= 0).all()
+    tight = valid & (u == 0)
+    np.testing.assert_array_equal(got[tight].view(np.uint32), want[tight].view(np.uint32))
+    loose = valid & (u > 0) & np.isfinite(u)
+    err = np.abs(want[loose].astype(np.float64) - got[loose].astype(np.float64))
+    assert (err <= u[loose].astype(np.float64)).all()
+    print(f"[info] {int(loose.sum())} of {int(valid.sum())} scores bounded (U > 0)", flush=True)
+
+
 @pytest.mark.parametrize("dist", ["normal", "scaled", "midpoints"])
 def test_indexer_bounded_equals_exact_path(device, dist):
     # the two score paths select identical indices (and both equal the oracle's)

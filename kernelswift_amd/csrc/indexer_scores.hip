@@ -527,13 +527,13 @@ indexer_scores_kernel(
       }
     if constexpr (BOUND) {
       // the next tile's 16 MFMAs (issued before this epilogue, in the same basic block) spread over the interval
-      // test and the head sum, one per 7 VALU instructions: the wave keeps issuing VALU work while the matrix
+      // test and the head sum, one per 6 VALU instructions: the wave keeps issuing VALU work while the matrix
       // core runs, instead of stalling on 16 back-to-back MFMAs
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
       }
     }
     const float tot = combine_groups(G);

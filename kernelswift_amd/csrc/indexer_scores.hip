@@ -335,6 +335,14 @@ indexer_scores_kernel(
   const int kst = kin ? kt : nk - 1;  // nk >= 1: the grid covers T with key blocks
   const float kn_v = kn[krow0 + kst];
   const int32_t ks_v = ksp[krow0 + kst];
+  // every wave reads the whole block's key norms (keys lane + 64 j), so that it forms the block's norm maximum,
+  // and with it the interval half-widths, without waiting for the other waves
+  float kn4[kKR / 64];
+#pragma unroll
+  for (int j = 0; j < kKR / 64; ++j) {
+    const int kj = lane + 64 * j;
+    kn4[j] = kn[krow0 + (kj < nk ? kj : nk - 1)];
+  }
   const int hl = lane & (H - 1);
   const int64_t hrow = qrow0 + hl;
   const float qn_v = qn[hrow];
@@ -348,6 +356,13 @@ indexer_scores_kernel(
     const int kr = lin / kC, ch = lin % kC;
     kv[it] = *reinterpret_cast<const uint4 *>(k + (krow0 + (kr < nk ? kr : nk - 1)) * KD + ch * 8);
   }
+  // Every wave's key-block loads are queued ahead of every q load: the memory pipeline serves a CU's loads in
+  // issue order, and the waves that issued last would otherwise wait behind the others' q rows (8 x 16 KiB)
+  // for their share of the key block, which the barrier below waits for.  (The scheduling barriers keep every
+  // load on its side of the barrier.)
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   // query rows as MFMA A-fragments (rows of query 0 for a wave past S, which leaves after the barrier); the
   // barrier below waits for the key block only, so these arrive under it and the first tile's MFMAs
   uint4 qa[HT][KD / 32];
@@ -357,12 +372,13 @@ indexer_scores_kernel(
     for (int kk = 0; kk < KD / 32; ++kk)
       qa[m][kk] = *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g);
   // max key norm over this workgroup's range (the error bound uses it for every key)
-  float knm = kin ? kn_v : 0.f;
-  L.knorm[kt] = knm;
+  L.knorm[kt] = kin ? kn_v : 0.f;
   L.kspan[kt] = kin ? ks_v : 0;
+  float knm = 0.f;
+#pragma unroll
+  for (int j = 0; j < kKR / 64; ++j) knm = fmaxf(knm, lane + 64 * j < nk ? kn4[j] : 0.f);
 #pragma unroll
   for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
-  if (lane == 0) L.red[wave] = knm;
   L.qspan[wave][hl] = qs_v;
   L.qnorm[wave][hl] = qn_v;
   L.w[wave][hl] = w_v;
@@ -371,7 +387,10 @@ indexer_scores_kernel(
   for (int it = 0; it < kKL; ++it) {
     const int lin = it * kThreads + tid;
     const int kr = lin / kC, ch = lin % kC;
-    L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = kr < nk ? kv[it] : make_uint4(0, 0, 0, 0);
+    // zero rows past T by a mask, not a select: a select lets the compiler move the load behind a branch and
+    // below the barrier that orders the key-block loads before the q loads
+    const uint32_t msk = kr < nk ? 0xFFFFFFFFu : 0u;
+    L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = make_uint4(kv[it].x & msk, kv[it].y & msk, kv[it].z & msk, kv[it].w & msk);
   }
   if constexpr (COUNT) {  // this wave's lower-end counts start at zero
 #pragma unroll
@@ -381,9 +400,6 @@ indexer_scores_kernel(
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  knm = L.red[0];
-#pragma unroll
-  for (int i = 1; i < kQW; ++i) knm = fmaxf(knm, L.red[i]);
   // BOUND: the block's key-norm maximum for the exact recomputation of candidate scores, which must use
   // the same interval width (every query group writes the same value)
   if constexpr (BOUND) {

@@ -72,7 +72,6 @@ struct ScoresLds {
   int32_t qspan[kQW][64];
   float qnorm[kQW][64];
   float w[kQW][64];                  // each wave's head weights (fp32)
-  float red[kQW];
 };
 
 // Inclusive prefix sum over the 64 lanes of a wave.
@@ -267,7 +266,6 @@ struct ScoresLdsBound {
   int32_t qspan[kQW][64];
   float qnorm[kQW][64];
   float w[kQW][64];
-  float red[kQW];
 };
 
 // The non-counting bound kernel runs grids of several workgroups per CU: at most 168 VGPRs (three waves per SIMD)
@@ -365,11 +363,13 @@ indexer_scores_kernel(
   __builtin_amdgcn_sched_barrier(0);
   // query rows as MFMA A-fragments (rows of query 0 for a wave past S, which leaves after the barrier); the
   // barrier below waits for the key block only, so these arrive under it and the first tile's MFMAs
+  // (issued in the order the first tile's MFMAs use them, k-step by k-step, so that they can start on the first
+  // k-step's fragments while the rest arrive)
   uint4 qa[HT][KD / 32];
 #pragma unroll
-  for (int m = 0; m < HT; ++m)
+  for (int kk = 0; kk < KD / 32; ++kk)
 #pragma unroll
-    for (int kk = 0; kk < KD / 32; ++kk)
+    for (int m = 0; m < HT; ++m)
       qa[m][kk] = *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g);
   // max key norm over this workgroup's range (the error bound uses it for every key)
   L.knorm[kt] = kin ? kn_v : 0.f;

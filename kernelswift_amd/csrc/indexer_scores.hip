@@ -71,6 +71,7 @@ struct ScoresLds {
   float knorm[kKR];                  // the exact recomputation (no global loads there)
   int32_t qspan[kQW][64];
   float qnorm[kQW][64];
+  float dl[kQW][64];                 // each wave's interval half-widths, one per head
   float w[kQW][64];                  // each wave's head weights (fp32)
 };
 
@@ -265,7 +266,9 @@ struct ScoresLdsBound {
   int32_t kspan[kKR];
   int32_t qspan[kQW][64];
   float qnorm[kQW][64];
+  float dl[kQW][64];
   float w[kQW][64];
+  uint16_t wup[kQW][64];  // |w| rounded up to bf16, for the bound MFMAs
 };
 
 // The non-counting bound kernel runs grids of several workgroups per CU: at most 168 VGPRs (three waves per SIMD)
@@ -381,6 +384,9 @@ indexer_scores_kernel(
   for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
   L.qspan[wave][hl] = qs_v;
   L.qnorm[wave][hl] = qn_v;
+  // per-head data formed once per head (lane h), not by each of the 16 lanes that use it
+  L.dl[wave][hl] = dot_halfwidth(qn_v, knm, bound_c);
+  if constexpr (BOUND) L.wup[wave][hl] = bf16_abs_round_up(w_v);
   L.w[wave][hl] = w_v;
   // the workgroup's whole key block into LDS (zero rows past T)
 #pragma unroll
@@ -413,7 +419,7 @@ indexer_scores_kernel(
     for (int r = 0; r < 4; ++r) {
       const int h = 16 * m + 4 * g + r;
       wv[m][r] = L.w[wave][h];
-      dl[m][r] = dot_halfwidth(L.qnorm[wave][h], knm, bound_c);
+      dl[m][r] = L.dl[wave][h];
     }
   // a half-width of +inf (norms that could overflow inside the MFMA): every dot of the wave is a near tie
   bool any_inf = false;
@@ -448,12 +454,10 @@ indexer_scores_kernel(
   if constexpr (BOUND) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-      const float *wr = wv[2 * hh];
-      const float *wr1 = wv[2 * hh + 1];
-      auto pk = [](float a, float c) {
-        return static_cast<uint32_t>(bf16_abs_round_up(a)) | (static_cast<uint32_t>(bf16_abs_round_up(c)) << 16);
-      };
-      wa[hh] = make_uint4(pk(wr[0], wr[1]), pk(wr[2], wr[3]), pk(wr1[0], wr1[1]), pk(wr1[2], wr1[3]));
+      // heads 16 m + 4 g + (0, 1) and (2, 3) of m = 2 hh and 2 hh + 1, as packed pairs
+      const uint32_t *up = reinterpret_cast<const uint32_t *>(L.wup[wave]);
+      const int h0 = 16 * (2 * hh) + 4 * g, h1 = h0 + 16;
+      wa[hh] = make_uint4(up[h0 / 2], up[h0 / 2 + 1], up[h1 / 2], up[h1 / 2 + 1]);
     }
   }
   const int64_t limit = causal ? (start_pos + s + 1) / ratio : INT64_MAX;

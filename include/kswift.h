@@ -270,18 +270,21 @@ int ks_mhc_post(const uint16_t *x, const uint16_t *f, const float *res_logits,
 /* ------------------------------------------------------------------------
  * ks_sparse_attn without a workspace: allocates nothing.
  *
- * No counterpart in the reference (whose torch op allocates its tiling tensors,
- * optimized/sparse_attention/op_extension/sparse_attn_torch.cpp:80-94).  For callers
- * that cannot allocate device memory: code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc.  Same arguments and results as
- * ks_sparse_attn, minus the workspace: the split partials live in a static device
- * array of ks_sparse_attn_noalloc_max_scratch() bytes (64 MiB) that each GPU holds
- * for the life of the process; its address on the stream's device is resolved on
- * that device's first call.  Shapes whose ks_sparse_attn_workspace_size exceeds the
- * maximum return KS_ERR_INVALID without launching.  Calls that overlap on one GPU
- * (two streams, two threads) share the array and race: serialise them.  The array
- * keeps the last call's contents; no call relies on them (every partial is written
- * before it is read within the call).
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments and results as ks_sparse_attn, minus the workspace:
+ * the split partials live in a static device array of
+ * ks_sparse_attn_noalloc_max_scratch() bytes (64 MiB).  The array is part of the
+ * library's code object, so every GPU on which the library is loaded holds its own
+ * 64 MiB copy for the life of the process, whether or not this entry point is ever
+ * called.  Its address on the stream's device is resolved (hipGetSymbolAddress) on
+ * that device's first call: make one call on each device before capturing this
+ * entry point into a HIP graph, so that the capture records kernel launches only.
+ * Shapes whose ks_sparse_attn_workspace_size exceeds the maximum return
+ * KS_ERR_INVALID without launching.  Calls that overlap on one GPU (two streams,
+ * two threads) share the array and race: serialise them.  The array keeps the last
+ * call's contents; no call relies on them (every partial is written before it is
+ * read within the call).
  * ---------------------------------------------------------------------- */
 size_t ks_sparse_attn_noalloc_max_scratch(void);
 int ks_sparse_attn_noalloc(const uint16_t *q, const uint16_t *kv, const float *sink,

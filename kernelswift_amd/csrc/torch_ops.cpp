@@ -101,6 +101,8 @@ at::Tensor indexer_topk(const at::Tensor& scores, bool causal, int64_t ratio, in
   TORCH_CHECK(scores.scalar_type() == at::kFloat, "scores must be float32");
   TORCH_CHECK(scores.dim() == 3 && scores.stride(2) == 1 && scores.stride(0) == scores.size(1) * scores.stride(1),
               "scores must be [b, s, ld] with contiguous rows");
+  TORCH_CHECK(actual_t >= 1 && actual_t <= scores.size(2), "actual_t=", actual_t,
+              " must be in [1, scores.size(2)=", scores.size(2), "]");
   const int64_t kk = std::min(k, actual_t);
   at::Tensor out = at::empty({scores.size(0), scores.size(1), kk}, scores.options().dtype(out_i64 ? at::kLong : at::kInt));
   check_rc(ks_indexer_topk(scores.data_ptr<float>(), scores.stride(1), scores.size(0), scores.size(1), actual_t, kk,

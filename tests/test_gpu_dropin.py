@@ -129,8 +129,8 @@ def test_harness_sparse_attention(device):
 
 def test_harness_indexer(device):
     # v1's indices are the canonical contract's (checked against the oracle on the module's own projections,
-    # on rows at both ends of the sequence); against v0, the torch op sequence on the GPU, the chosen sets
-    # agree and positions differ only where v0's own bf16 scores leave the order to rounding or ties
+    # on rows at both ends of the sequence); against v0, the torch op sequence on the GPU, positions differ
+    # only where v0's own bf16 scores leave the order to rounding or ties
     v1 = dropin_harness.load(os.path.join(_OPT, "indexer.py"))
     print("[case] harness indexer B=8 S=2600 H=16 D=64 ratio=4 k=128", flush=True)
     out0, out1, model, v0_inputs = dropin_harness.run_case(torch_models.IndexerModel,
@@ -150,13 +150,42 @@ def test_harness_indexer(device):
                                    True, s0, 4)
         want = oracle.postprocess(oracle.topk_stable(sc, 128), True, s0, 4, 0)
         np.testing.assert_array_equal(got[b, s0:s1], want[0])
+    # the reference harness compares integer outputs with torch.equal (benchmarks/ks/auto_bench.py:307): rows
+    # where v1 and v0 differ are those whose order v0's own bf16 scores leave to rounding.  Every differing
+    # position j of a row, v1 key a and v0 key r, must be an exact tie in v0's scores or within one rounding:
+    #   tol(a, r) = sum_h |w_h| 2 (ulp(d_h(a)) + ulp(d_h(r)))    (each dot rounded to bf16, each product
+    #                                                              relu(d) w rounded to bf16)
+    #             + ulp(s0(a)) + ulp(s0(r))                      (the bf16 rounding of each score)
+    #             + 2^-16 sum_h |w_h| (|d_h(a)| + |d_h(r)|)      (fp32 head sums in either order)
+    # with d_h the exact dots (float64 of the bf16 operands) and ulp the bf16 spacing.
     ref = out0.cpu().numpy()
-    valid = ref >= 0
-    overlap = np.mean([len(set(got[b, s][valid[b, s]]) & set(ref[b, s][valid[b, s]])) / max(1, valid[b, s].sum())
-                       for b in range(8) for s in range(0, 2600, 13)])
-    print(f"[info] rows identical to the torch op sequence: {np.mean(np.all(got == ref, axis=-1)):.4f}, "
-          f"set overlap {overlap:.5f}", flush=True)
-    assert overlap > 0.99
+    row_same = np.all(got == ref, axis=-1)
+    bb, ss, jj = np.nonzero(got != ref)
+    print(f"[info] harness integer check: rows identical to v0 {row_same.mean():.4f} ({int(row_same.sum())} of "
+          f"{row_same.size}), differing positions {bb.size}", flush=True)
+    assert (got[bb, ss, jj] >= 0).all() and (ref[bb, ss, jj] >= 0).all(), "the -1 tails must coincide"
+    with torch.no_grad():
+        sc0 = model.scores(x, qr, start_pos).float().cpu().numpy()  # v0's own bf16 scores
+    qrot = oracle.bf16_to_f32(oracle.rope_bf16(bits(q.cpu()), freqs, 32, 32, pos0=0)).astype(np.float64)
+    kf = oracle.bf16_to_f32(bits(model.kv_cache[:, :T].cpu())).astype(np.float64)
+    wf = oracle.bf16_to_f32(bits(w.cpu())).astype(np.float64)
+
+    def ulp(v):
+        return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126))) - 7)
+
+    a_k, r_k = got[bb, ss, jj], ref[bb, ss, jj]
+    da = np.einsum("nhd,nd->nh", qrot[bb, ss], kf[bb, a_k])
+    dr = np.einsum("nhd,nd->nh", qrot[bb, ss], kf[bb, r_k])
+    aw = np.abs(wf[bb, ss])
+    sa, sr = sc0[bb, ss, a_k], sc0[bb, ss, r_k]
+    tol = ((aw * 2 * (ulp(da) + ulp(dr))).sum(1) + ulp(sa) + ulp(sr)
+           + 2.0 ** -16 * (aw * (np.abs(da) + np.abs(dr))).sum(1))
+    gap = np.abs(sa - sr)
+    tied = int((gap == 0).sum())
+    print(f"[info] differing positions tied in v0's scores {tied}, within one rounding "
+          f"{int((gap <= tol).sum()) - tied}, largest gap / tol {float((gap / tol).max()) if gap.size else 0.0:.3f}",
+          flush=True)
+    assert (gap <= tol).all()
 
 
 def test_torch_ops_registered_and_callable(device):

@@ -284,6 +284,34 @@ def test_sinkhorn_invariants_and_equivariance():
     np.testing.assert_allclose(yt, y, atol=1e-5, rtol=1e-5)
 
 
+def test_sinkhorn_rational_closed_forms_pin_eps_and_iteration_count():
+    # x = log(m): the softmax of a row is m / rowsum exactly, so with a rational eps every step is rational.
+    # repeat = 1 is softmax (+ eps) then one column normalisation; the values below were derived by hand
+    # (row 0 of m sums to 8, so its softmax is [1, 2, 1, 4] / 8; column 0 then sums to 37/40; ...).
+    from fractions import Fraction as Fr
+    m = np.array([[1, 2, 1, 4], [3, 1, 1, 1], [2, 2, 5, 1], [1, 6, 1, 2]], dtype=np.float64)
+    x = np.log(m)[None]
+    one = {Fr(0): [["5/37", "15/73", "15/107", "15/29"], ["20/37", "10/73", "20/107", "5/29"],
+                   ["8/37", "12/73", "60/107", "3/29"], ["4/37", "36/73", "12/107", "6/29"]],
+           Fr(1, 4): [["5/29", "15/74", "45/257", "45/133"], ["10/29", "25/148", "50/257", "25/133"],
+                      ["6/29", "27/148", "90/257", "3/19"], ["14/87", "51/148", "42/257", "27/133"]]}
+    for eps, lit in one.items():
+        want1 = [[Fr(v) for v in row] for row in lit]
+        np.testing.assert_allclose(oracle.sinkhorn(x, 1, float(eps))[0], np.array(want1, dtype=np.float64),
+                                   rtol=1e-13, atol=0)
+        # one more iteration is one row normalisation then one column normalisation of that matrix (each
+        # dividing by the sum + eps), done here in exact rationals
+        rs = [sum(r) + eps for r in want1]
+        v = [[want1[i][j] / rs[i] for j in range(4)] for i in range(4)]
+        cs = [sum(v[i][j] for i in range(4)) + eps for j in range(4)]
+        want2 = [[v[i][j] / cs[j] for j in range(4)] for i in range(4)]
+        got2 = oracle.sinkhorn(x, 2, float(eps))[0]
+        np.testing.assert_allclose(got2, np.array([[float(a) for a in r] for r in want2]), rtol=1e-13, atol=0)
+        # and repeat = 2 is not repeat = 1 or 3 (the count is what the check sees)
+        assert np.abs(got2 - oracle.sinkhorn(x, 1, float(eps))[0]).max() > 1e-3
+        assert np.abs(got2 - oracle.sinkhorn(x, 3, float(eps))[0]).max() > 1e-4
+
+
 # ------------------------------------------------------------------ sparse attention
 def _bf(a):
     return oracle.f32_to_bf16(np.asarray(a, dtype=np.float32))
@@ -317,6 +345,30 @@ def test_sparse_attn_closed_forms():
     out = oracle.sparse_attn(np.zeros((1, 1, H, D), np.uint16), kv, sink, idx, 1.0)
     want = (2 * kvf[0, 3] + kvf[0, 6]) / 4.0
     np.testing.assert_allclose(out[0, 0], np.broadcast_to(want, (H, D)), rtol=1e-12)
+
+
+def test_sparse_attn_two_key_closed_form_pins_scale():
+    # one head, two valid keys: s_i = scale * q.k_i, and with a sink the output is
+    #   (e^s1 v1 + e^s2 v2) / (e^s1 + e^s2 + e^sink),  v_i = k_i (K = V = kv)
+    # q = 2 e_0, k1 = e_0 + 3 e_1, k2 = -e_1 + 5 e_2: s1 = 2 scale, s2 = 0 (every value exact in bf16)
+    D = 16
+    q = np.zeros((1, 1, 1, D), np.float32)
+    q[0, 0, 0, 0] = 2.0
+    kv = np.zeros((1, 2, D), np.float32)
+    kv[0, 0, 0], kv[0, 0, 1] = 1.0, 3.0
+    kv[0, 1, 1], kv[0, 1, 2] = -1.0, 5.0
+    idx = np.array([[[0, 1]]], dtype=np.int32)
+    v1, v2 = kv[0, 0].astype(np.float64), kv[0, 1].astype(np.float64)
+    for scale in (0.3, 128 ** -0.5, 576 ** -0.5, 1.7):
+        for sink in (-np.inf, 0.0, 0.7):
+            e1, e2, es = np.exp(2 * scale), 1.0, np.exp(np.float64(np.float32(sink)))  # the sink is fp32
+            want = (e1 * v1 + e2 * v2) / (e1 + e2 + es)
+            got = oracle.sparse_attn(_bf(q), _bf(kv), np.array([sink], np.float32), idx, scale)[0, 0, 0]
+            np.testing.assert_allclose(got, want, rtol=1e-13, atol=1e-15)
+    # the output moves with the scale: a scale off by any factor is seen
+    a = oracle.sparse_attn(_bf(q), _bf(kv), np.zeros(1, np.float32), idx, 0.3)
+    b = oracle.sparse_attn(_bf(q), _bf(kv), np.zeros(1, np.float32), idx, 0.6)
+    assert np.abs(a - b).max() > 0.05
 
 
 def test_sparse_attn_matches_torch_cpu():

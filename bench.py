@@ -456,24 +456,37 @@ def run_mhc(steps, warmup, do_cpu, cpu_budget, N=4096, C=4096, iters=20):
     return res_d
 
 
-def run_fp8(steps, warmup, do_cpu, cpu_budget):
-    """The indexer on FP8 rows (dtype = "fp8", scale_fmt = "ue8m0"; baseline/indexer.py:14-17) at config 2's shape:
-    q and k rotated, then quantised to e4m3 with one power-of-two scale per row (the cache-write side, timed
-    as ks_fp8_quant_rows), and the indexer call on the codes (dequantisation + statistics pass, bounded scores,
-    exact top-k).  The quantiser is HBM-bound: its roofline is GB/s of bf16 read + codes and scales written."""
-    import torch
-    from kernelswift_amd import _lib, ops, workloads
-    w = workloads.CONFIGS[2]("cuda")
+def _fp8_inputs(cfg):
+    """Config `cfg`'s q and k rotated, then quantised to e4m3 with one power-of-two scale per row."""
+    from kernelswift_amd import ops, workloads
+    w = workloads.CONFIGS[cfg]("cuda")
     t, p = w.tensors, w.params
-    B, S, H, D = t["q"].shape
-    T = t["k"].shape[1]
+    D = t["q"].shape[3]
     qr, kr = t["q"].clone(), t["k"].clone()
     ops.rope_inplace(qr, t["freqs"], rope_start=0, pos0=p["start_pos"])
     ops.rope_inplace(kr, t["freqs"], rope_start=0, pos0=0)
     qc, qs = ops.fp8_quant(qr, D, True)
     kc, ks_ = ops.fp8_quant(kr, D, True)
-    qs, ks_ = qs[..., 0].contiguous(), ks_[..., 0].contiguous()
+    return t, p, qr, qc, qs[..., 0].contiguous(), kc, ks_[..., 0].contiguous()
+
+
+def run_fp8(steps, warmup, do_cpu, cpu_budget):
+    """The indexer on FP8 rows (dtype = "fp8", scale_fmt = "ue8m0"; baseline/indexer.py:14-17) at config 2's shape
+    (and config 4's beside it): q and k rotated, then quantised to e4m3 with one power-of-two scale per row (the
+    cache-write side, timed as ks_fp8_quant_rows), and the indexer call on the codes (a statistics pass, then the
+    bounded score and recomputation kernels reading the codes themselves, exact top-k).  The quantiser is
+    HBM-bound: its roofline is GB/s of bf16 read + codes and scales written."""
+    import torch
+    from kernelswift_amd import _lib
     tops = _lib.torch_ops()
+    t4, p4, _, qc4, qs4, kc4, ks4 = _fp8_inputs(4)
+    dev4, _ = _events_median(
+        lambda: tops.indexer_fp8(qc4, qs4, kc4, ks4, t4["w"], p4["k_top"], True, p4["start_pos"], 1, 0, False, None),
+        steps, warmup)
+    del t4, qc4, qs4, kc4, ks4
+    t, p, qr, qc, qs, kc, ks_ = _fp8_inputs(2)
+    B, S, H, D = qc.shape
+    T = kc.shape[1]
 
     def step():
         return tops.indexer_fp8(qc, qs, kc, ks_, t["w"], p["k_top"], True, p["start_pos"], 1, 0, False, None)
@@ -495,8 +508,9 @@ def run_fp8(steps, warmup, do_cpu, cpu_budget):
     gbs = qbytes / (quant_us * 1e-6) / 1e9
     res = {"us_per_call": round(dev_med, 3), "us_per_call_mean": round(dev_mean, 3),
            "wall_us_per_call_sync": round(wall_med, 3), "ms_per_step": ms_step,
+           "us_per_call_config4_shape": round(dev4, 3),
            "workload": f"config-2 shape on e4m3 rows (ue8m0 row scales): B={B} S_q={S} S_kv={T} H={H} D={D} "
-                       f"causal top-{p['k_top']}",
+                       f"causal top-{p['k_top']}; us_per_call_config4_shape: the same at config 4's shape",
            "kernels_us": {"fp8_quant_kernel (q rows)": round(quant_us, 3)},
            "roofline": {"bound": "hbm", "kernel": "fp8_quant_kernel", "achieved": round(gbs, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),

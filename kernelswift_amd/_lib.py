@@ -69,6 +69,8 @@ DEBUG_SIGNATURES = {
                                           _c_sz, _c_p, _c_p, _c_i32]),
     "ks_dbg_mfma_bf16_chain": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),
     "ks_dbg_mfma_fp8_chain": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),
+    "ks_dbg_mfma_fp8_plain_chain": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),
+    "ks_dbg_fp8_cvt": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i32, _c_p, _c_p]),
     "ks_dbg_exact_dot_wide": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_p]),
     "ks_dbg_score_bound_c": (ctypes.c_float, []),
 }

@@ -97,11 +97,21 @@ int64_t count_words16(const IndexerWs &ws, int64_t B, int64_t S, int64_t T) {
   return ws.part_cap > 0 && ks::scores_count_rows(B, S, T) ? B * S * ks::kTopkCountWords / 4 : 0;
 }
 
-// Scores of the prepared rows (ws.q_rot / ws.k_rot with their statistics) -> exact top-k.  Where the score
-// kernel counts the rows, the bounded path needs the count region cleared by the row preparation launch.
+// FP8 keys read directly by the bounded kernels (codes and row scales at batch stride kbs), or none.
+struct Fp8Direct {
+  const uint8_t *kc = nullptr;
+  const float *ks = nullptr;
+  int64_t kbs = 0;
+};
+
+// Scores of the prepared rows (ws.q_rot / ws.k_rot with their statistics, or the FP8 rows of f8) -> exact top-k.
+// Where the score kernel counts the rows, the bounded path needs the count region cleared by the row preparation
+// launch.
+
 int indexer_select(const char *fn, const IndexerWs &ws, const void *w, int32_t w_bf16, int64_t k_top, int32_t causal,
                    int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
-                   int64_t H, int64_t D, int64_t T, hipStream_t st, float bound_c, uint32_t *stats, int path) {
+                   int64_t H, int64_t D, int64_t T, hipStream_t st, float bound_c, uint32_t *stats, int path,
+                   const Fp8Direct &f8 = Fp8Direct{}) {
   const int64_t kk = k_top < T ? k_top : T;
   const bool can_bound = takes_bounded(k_top, w_bf16, H, D, T, 0);
   KS_CHECK_ARG(path < 2 || can_bound,
@@ -109,13 +119,19 @@ int indexer_select(const char *fn, const IndexerWs &ws, const void *w, int32_t w
   int rc;
   if (can_bound && path != 1) {
     const bool counted = ks::scores_count_rows(B, S, T);
-    rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span, ws.scores, B,
-                                   S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, bound_c, nullptr, st, ws.bounds,
-                                   ws.kmax, counted ? ks::topk_bounded_counts(ws.part, B * S, T) : nullptr);
+    const bool direct = f8.kc != nullptr;
+    // FP8 keys: the codes with their row scales (the statistics are indexed like the rows: B == 1 or kbs == T)
+    const uint16_t *krows = direct ? reinterpret_cast<const uint16_t *>(f8.kc) : ws.k_rot;
+    const int64_t kbs = direct ? f8.kbs : T;
+    rc = ks::launch_indexer_scores(ws.q_rot, krows, w, 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span, ws.scores, B, S,
+                                   H, D, T, kbs, causal ? 1 : 0, start_pos, ratio, bound_c, nullptr, st, ws.bounds,
+                                   ws.kmax, counted ? ks::topk_bounded_counts(ws.part, B * S, T) : nullptr, f8.ks);
     if (rc != KS_OK) return rc;
-    const ks::TopkRecompute trc{ws.bounds, ws.kmax, ws.q_rot, ws.k_rot, static_cast<const float *>(w), ws.q_norm,
-                                ws.q_span, ws.k_norm, ws.k_span, T, bound_c, stats, path == 3 ? 1 : 0, ws.part,
-                                ws.part_cap, counted ? 1 : 0};
+    ks::TopkRecompute trc{ws.bounds, ws.kmax, ws.q_rot, ws.k_rot, static_cast<const float *>(w), ws.q_norm,
+                          ws.q_span, ws.k_norm, ws.k_span, kbs, bound_c, stats, path == 3 ? 1 : 0, ws.part,
+                          ws.part_cap, counted ? 1 : 0};
+    trc.kc = f8.kc;
+    trc.ks = f8.ks;
     return ks::launch_indexer_topk_bounded(ws.scores, T, B, S, T, kk, causal ? 1 : 0, start_pos, ratio, offset, out,
                                            out_i64 ? 1 : 0, trc, st);
   }
@@ -179,16 +195,26 @@ int indexer_fp8_impl(const uint8_t *q, const float *q_scale, const uint8_t *k, c
                "ks_indexer_fp8: workspace of %zu bytes required, %zu given", ws.bytes, workspace_bytes);
   KS_CHECK_ARG(ks::aligned(workspace, 256), "ks_indexer_fp8: workspace must be 256-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool bounded = takes_bounded(k_top, w_bf16, H, D, T, path);
+  // the bounded kernels read the key codes themselves (their key statistics are indexed like the key rows, so the
+  // batches must be contiguous: one batch, or k_batch_stride == T); then this pass forms the keys' statistics only.
+  // q is dequantised here in every case: the score kernel reads each query's rows from T / 256 workgroups.
+  const bool direct = bounded && (B == 1 || k_batch_stride == T);
   // q rows (scale per row) and k rows of every batch (stride k_batch_stride, scale per row, same stride)
   const ks::Fp8RowJob qjob{q, q_scale, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H};
-  const ks::Fp8RowJob kjob{k, k_scale, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride};
-  const bool bounded = takes_bounded(k_top, w_bf16, H, D, T, path);
+  const ks::Fp8RowJob kjob{k, k_scale, direct ? nullptr : ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride};
   rc = ks::launch_fp8_rows(qjob, kjob, static_cast<int>(D), st,
                            bounded ? ks::topk_bounded_counts(ws.part, B * S, T) : nullptr,
                            bounded ? count_words16(ws, B, S, T) : 0);
   if (rc != KS_OK) return rc;
+  Fp8Direct f8;
+  if (direct) {
+    f8.kc = k;
+    f8.ks = k_scale;
+    f8.kbs = k_batch_stride;
+  }
   return indexer_select("ks_indexer_fp8", ws, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B, S,
-                        H, D, T, st, bound_c, stats, path);
+                        H, D, T, st, bound_c, stats, path, f8);
 }
 }  // namespace
 

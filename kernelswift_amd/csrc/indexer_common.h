@@ -59,6 +59,43 @@ __device__ __forceinline__ uint4 rope_chunk(uint4 v, const float2 *__restrict__ 
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// FP8 (OCP e4m3) key rows read directly by the bounded score and recomputation kernels.  The dequantised row the
+// contract defines is bf16(fp32(value(code) * scale)).  Two hardware forms compute it for eight codes (two
+// 32-bit words):
+//  - v_cvt_pk_f32_fp8 gives the codes' values exactly (all 256 codes, NaN codes included: pinned by the GPU
+//    tests), then an fp32 multiply and the RNE conversion to bf16: the contract's arithmetic for any scale;
+//  - v_cvt_scalef32_pk_bf16_fp8 applies only the scale's exponent (its mantissa and sign are ignored: pinned by
+//    the GPU tests), so it equals the contract for a positive power-of-two scale.  With 2^-100 <= s <= 2^100 every
+//    value(code) * s (|value| in [2^-9, 448]) is an exact normal number, and one instruction converts two codes.
+// fp8_scale_pow2 tells which form applies; callers take the one-instruction form when every scale of a wave
+// allows it (a uniform branch).
+__device__ __forceinline__ bool fp8_scale_pow2(float s) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, s);
+  const uint32_t e = u >> 23;  // the sign bit is included: a negative scale fails the range test
+  return (u & 0x7FFFFFu) == 0u && e >= 27u && e <= 227u;
+}
+
+__device__ __forceinline__ uint32_t fp8_dequant2_pow2(uint32_t src, float s, bool hi_word) {
+  return __builtin_bit_cast(uint32_t, hi_word ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(src, s, true)
+                                              : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(src, s, false));
+}
+__device__ __forceinline__ uint32_t fp8_dequant2(uint32_t src, float s, bool hi_word) {
+  const cvt_f32x2_t v = hi_word ? __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(src), true)
+                                : __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(src), false);
+  return cvt_pk_bf16(v[0] * s, v[1] * s);
+}
+// Eight codes in either form (POW2: the one-instruction form).  Callers branch once, uniformly, around all of a
+// prologue's conversions: a branch per call costs two taken jumps each.
+template <bool POW2>
+__device__ __forceinline__ uint4 fp8_dequant8(uint2 c, float s) {
+  if constexpr (POW2)
+    return make_uint4(fp8_dequant2_pow2(c.x, s, false), fp8_dequant2_pow2(c.x, s, true),
+                      fp8_dequant2_pow2(c.y, s, false), fp8_dequant2_pow2(c.y, s, true));
+  else
+    return make_uint4(fp8_dequant2(c.x, s, false), fp8_dequant2(c.x, s, true), fp8_dequant2(c.y, s, false),
+                      fp8_dequant2(c.y, s, true));
+}
+
 // Row-statistics contributions of one chunk: sum of squares (each square is exact: 8-bit significands)
 // and the smallest LSB exponent of its nonzero elements (1 << 20 when all are zero).
 __device__ __forceinline__ void chunk_stats(uint4 v, float &ss, int &lsb) {
@@ -159,7 +196,9 @@ int launch_fp8_rows(const Fp8RowJob &job0, const Fp8RowJob &job1, int D, hipStre
 // [B][ceil(T / kScoreKeyBlock)] then receives each key block's key-norm maximum (the interval half-width
 // of a dot is bound_c 2^-23 ||q_h|| kmax), for an exact recomputation with the same intervals, and
 // row_counts [B S][2048] (zero on entry; may be null) is incremented by each row's counts of the first 11-bit
-// digit of score_key(lower end) over its valid columns (the bounded selection's threshold histogram).
+// digit of score_key(lower end) over its valid columns (the bounded selection's threshold histogram).  With
+// ksc (bound mode, 64 heads, D = 128), k holds e4m3 codes with those row scales (FP8 keys), read directly; kn /
+// ksp are the statistics of the dequantised rows.
 constexpr int kScoreKeyBlock = 256;
 // Whether the fused entry counts the rows in the score kernel: its grid of (key block, 8 queries) workgroups
 // fits the 256 CUs in one round.  The counts' LDS leaves no room for a second workgroup per CU, which a grid
@@ -171,13 +210,14 @@ int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, i
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
                           int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds = nullptr,
-                          float *kmax = nullptr, uint32_t *row_counts = nullptr);
+                          float *kmax = nullptr, uint32_t *row_counts = nullptr, const float *ksc = nullptr);
 
 // Sorted exact top-k of rows of bounded scores (the bound-emitting score kernel's output): a threshold from the
 // lower ends, exact recomputation of the scores that may reach the top k (interval test with the score kernel's
 // half-widths, exact double-precision dots for the near ties, canonical head sum; written back with bound 0),
 // then a sort of the exact scores at or above the threshold.  q / k: the rotated rows and their statistics
-// (64 heads, D = 128), w fp32 [B, S, 64].
+// (64 heads, D = 128), w fp32 [B, S, 64]; with kc / ks set, the keys are e4m3 codes and row scales (the statistics
+// those of the dequantised rows), read directly and dequantised in registers.
 struct TopkRecompute {
   float *bounds;  // recomputed scores get bound 0
   const float *kmax;
@@ -199,6 +239,9 @@ struct TopkRecompute {
   // nonzero: the score kernel has already counted the rows (one slice per row, at topk_bounded_counts) and the
   // row states there are clear, so the selection starts with the threshold
   int counted;
+  // FP8 keys (both set, or neither): codes [rows][128] and row scales, kbs rows per batch
+  const uint8_t *kc = nullptr;
+  const float *ks = nullptr;
 };
 // Slots the bounded selection needs for `rows` rows of T <= 32768 columns (0 outside that range).
 int64_t topk_bounded_part_capacity(int64_t rows, int64_t T);

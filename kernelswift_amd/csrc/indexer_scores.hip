@@ -32,6 +32,12 @@
 // of the lower interval ends and a bound U on its distance from the exact score; its counting form (COUNT) also
 // builds each row's histogram of the first 11-bit digit of the lower ends' keys for the bounded top-k's
 // threshold (per-wave LDS counts, flushed with one global atomic per nonzero bucket).
+//
+// FP8 keys (F8, bound mode): k holds e4m3 codes with one fp32 scale per row, read directly (half the bytes of
+// bf16 rows) and dequantised in registers to the bf16 rows the contract defines, bf16(fp32(value * scale)), before
+// the key block is staged in LDS; the rest of the kernel is the bf16 one.  (q arrives dequantised: each query's
+// rows are read by every key block's workgroup, T / 256 of them, so they are converted once, by the statistics
+// pass, while a key block is read by S / 8 workgroups.)
 #include "common.h"
 #include "indexer_common.h"
 #include "indexer_exact.h"
@@ -273,18 +279,22 @@ struct ScoresLdsBound {
 
 // The non-counting bound kernel runs grids of several workgroups per CU: at most 168 VGPRs (three waves per SIMD)
 // let the next workgroup start as soon as one wave per SIMD of the current one has finished.
-template <int HT, int KD, bool WBF, bool BOUND, bool COUNT = false>
+template <int HT, int KD, bool WBF, bool BOUND, bool COUNT = false, bool F8 = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu((BOUND && !COUNT) ? 3 : 1))) void
 indexer_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
     const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
     int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats, int xcd_pk,
-    float *__restrict__ bounds, float *__restrict__ kmax, uint32_t *__restrict__ row_counts) {
+    float *__restrict__ bounds, float *__restrict__ kmax, uint32_t *__restrict__ row_counts,
+    const float *__restrict__ ksc) {
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
   static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
   static_assert(BOUND || !COUNT, "counts of lower ends need the bounds");
+  static_assert(!F8 || BOUND, "FP8 keys are read by the bound-emitting variant");
+  // F8: k points at e4m3 codes (KD bytes per row) with row scales ksc
+  const uint8_t *__restrict__ k8 = reinterpret_cast<const uint8_t *>(k);
   __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD, COUNT>, ScoresLds<KD, HT>> L;
   // the wave index is uniform per wave; readfirstlane lets the compiler keep the query row, the causal limit
   // and the tile loop in scalar registers
@@ -349,13 +359,22 @@ indexer_scores_kernel(
   const float qn_v = qn[hrow];
   const int32_t qs_v = qsp[hrow];
   const float w_v = WBF ? bf16_to_f32(static_cast<const uint16_t *>(w)[hrow]) : static_cast<const float *>(w)[hrow];
-  constexpr int kKL = kKR * kC / kThreads;  // 16-byte key chunks per thread
-  uint4 kv[kKL];
+  constexpr int kKL = kKR * kC / kThreads;  // 16-byte key chunks per thread (F8: kKL / 2 loads of 16 codes)
+  constexpr int kKV = F8 ? kKL / 2 : kKL;
+  uint4 kv[kKV];
+  float ksv[F8 ? kKV : 1];
 #pragma unroll
-  for (int it = 0; it < kKL; ++it) {
+  for (int it = 0; it < kKV; ++it) {
     const int lin = it * kThreads + tid;
-    const int kr = lin / kC, ch = lin % kC;
-    kv[it] = *reinterpret_cast<const uint4 *>(k + (krow0 + (kr < nk ? kr : nk - 1)) * KD + ch * 8);
+    if constexpr (F8) {
+      const int kr = lin / (kC / 2), ch2 = lin % (kC / 2);
+      const int64_t row = krow0 + (kr < nk ? kr : nk - 1);
+      kv[it] = *reinterpret_cast<const uint4 *>(k8 + row * KD + ch2 * 16);
+      ksv[it] = ksc[row];
+    } else {
+      const int kr = lin / kC, ch = lin % kC;
+      kv[it] = *reinterpret_cast<const uint4 *>(k + (krow0 + (kr < nk ? kr : nk - 1)) * KD + ch * 8);
+    }
   }
   // Every wave's key-block loads are queued ahead of every q load: the memory pipeline serves a CU's loads in
   // issue order, and the waves that issued last would otherwise wait behind the others' q rows (8 x 16 KiB)
@@ -389,14 +408,38 @@ indexer_scores_kernel(
   if constexpr (BOUND) L.wup[wave][hl] = bf16_abs_round_up(w_v);
   L.w[wave][hl] = w_v;
   // the workgroup's whole key block into LDS (zero rows past T)
+  if constexpr (F8) {
+    // one conversion form for the whole wave: the one-instruction form when every scale it holds allows it
+    bool p2 = true;
 #pragma unroll
-  for (int it = 0; it < kKL; ++it) {
-    const int lin = it * kThreads + tid;
-    const int kr = lin / kC, ch = lin % kC;
-    // zero rows past T by a mask, not a select: a select lets the compiler move the load behind a branch and
-    // below the barrier that orders the key-block loads before the q loads
-    const uint32_t msk = kr < nk ? 0xFFFFFFFFu : 0u;
-    L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = make_uint4(kv[it].x & msk, kv[it].y & msk, kv[it].z & msk, kv[it].w & msk);
+    for (int it = 0; it < kKV; ++it) p2 = p2 & fp8_scale_pow2(ksv[it]);  // no short-circuit: no branches
+    p2 = __builtin_amdgcn_ballot_w64(!p2) == 0ull;
+    auto stage = [&](auto POW2) {
+#pragma unroll
+      for (int it = 0; it < kKV; ++it) {
+        const int lin = it * kThreads + tid;
+        const int kr = lin / (kC / 2), ch = 2 * (lin % (kC / 2));
+        const uint32_t msk = kr < nk ? 0xFFFFFFFFu : 0u;
+        const uint4 lo = fp8_dequant8<decltype(POW2)::value>(make_uint2(kv[it].x, kv[it].y), ksv[it]);
+        const uint4 hi = fp8_dequant8<decltype(POW2)::value>(make_uint2(kv[it].z, kv[it].w), ksv[it]);
+        L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = make_uint4(lo.x & msk, lo.y & msk, lo.z & msk, lo.w & msk);
+        L.k[kr * kC + ((ch + 1) ^ (kr & (kC - 1)))] = make_uint4(hi.x & msk, hi.y & msk, hi.z & msk, hi.w & msk);
+      }
+    };
+    if (p2)
+      stage(std::true_type{});
+    else
+      stage(std::false_type{});
+  } else {
+#pragma unroll
+    for (int it = 0; it < kKL; ++it) {
+      const int lin = it * kThreads + tid;
+      const int kr = lin / kC, ch = lin % kC;
+      // zero rows past T by a mask, not a select: a select lets the compiler move the load behind a branch and
+      // below the barrier that orders the key-block loads before the q loads
+      const uint32_t msk = kr < nk ? 0xFFFFFFFFu : 0u;
+      L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = make_uint4(kv[it].x & msk, kv[it].y & msk, kv[it].z & msk, kv[it].w & msk);
+    }
   }
   if constexpr (COUNT) {  // this wave's lower-end counts start at zero
 #pragma unroll
@@ -689,14 +732,14 @@ template <int HT, int KD>
 int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                      const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                      int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c, uint32_t *stats,
-                     float *bounds, float *kmax, uint32_t *row_counts, hipStream_t stream) {
+                     float *bounds, float *kmax, uint32_t *row_counts, const float *ksc, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
   // XCD tiling (Pq x Pk = 8) that minimises the L2 fills: each query group's rows are read by Pk XCDs,
   // each key block by Pq; 0 keeps the launch order (slice not a multiple of 8 or no tiling divides it)
   int xcd_pk = 0;
   if ((static_cast<int64_t>(grid.x) * grid.y) % 8 == 0) {
-    const double qbytes = static_cast<double>(S) * 16 * HT * KD, kbytes = static_cast<double>(T) * KD;
+    const double qbytes = static_cast<double>(S) * 16 * HT * KD, kbytes = static_cast<double>(T) * KD;  // either format
     double best = 0.0;
     for (int pk = 1; pk <= 8; pk *= 2) {
       const int pq = 8 / pk;
@@ -708,18 +751,36 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
       }
     }
   }
-  if (bounds != nullptr) {
+  if (ksc != nullptr && bounds == nullptr)
+    return fail(KS_ERR_INVALID, "indexer scores: FP8 keys need the bound-emitting kernel");
+  if (bounds != nullptr && ksc != nullptr) {
+    if constexpr (HT == 4 && KD == 128) {
+      if (w_bf16) return fail(KS_ERR_INVALID, "indexer scores: score bounds need fp32 weights");
+      if (kmax == nullptr) return fail(KS_ERR_INVALID, "indexer scores: score bounds need the kmax buffer");
+      if (row_counts != nullptr) {
+        hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, true, true>), grid, dim3(kThreads), 0, stream, q,
+                           k, w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio,
+                           bound_c, stats, xcd_pk, bounds, kmax, row_counts, ksc);
+      } else {
+        hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, false, true>), grid, dim3(kThreads), 0, stream,
+                           q, k, w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio,
+                           bound_c, stats, xcd_pk, bounds, kmax, nullptr, ksc);
+      }
+    } else {
+      return fail(KS_ERR_INVALID, "indexer scores: FP8 keys need H = 64 and D = 128");
+    }
+  } else if (bounds != nullptr) {
     if constexpr (HT == 4) {
       if (w_bf16) return fail(KS_ERR_INVALID, "indexer scores: score bounds need fp32 weights");
       if (kmax == nullptr) return fail(KS_ERR_INVALID, "indexer scores: score bounds need the kmax buffer");
       if (row_counts != nullptr) {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, true>), grid, dim3(kThreads), 0, stream, q, k, w,
                            qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
-                           stats, xcd_pk, bounds, kmax, row_counts);
+                           stats, xcd_pk, bounds, kmax, row_counts, nullptr);
       } else {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, false>), grid, dim3(kThreads), 0, stream, q, k,
                            w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
-                           stats, xcd_pk, bounds, kmax, nullptr);
+                           stats, xcd_pk, bounds, kmax, nullptr, nullptr);
       }
     } else {
       return fail(KS_ERR_INVALID, "indexer scores: score bounds need H = 64");
@@ -727,11 +788,11 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
   } else if (w_bf16) {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp,
                        kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk,
-                       nullptr, nullptr, nullptr);
+                       nullptr, nullptr, nullptr, nullptr);
   } else {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn,
                        qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats,
-                       xcd_pk, nullptr, nullptr, nullptr);
+                       xcd_pk, nullptr, nullptr, nullptr, nullptr);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;
@@ -741,17 +802,18 @@ template <int KD>
 int launch_scores_d(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                     const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                     int64_t H, int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c,
-                    uint32_t *stats, float *bounds, float *kmax, uint32_t *row_counts, hipStream_t stream) {
+                    uint32_t *stats, float *bounds, float *kmax, uint32_t *row_counts, const float *ksc,
+                    hipStream_t stream) {
   switch (H) {
     case 16:
       return launch_scores_ht<1, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, row_counts, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream);
     case 32:
       return launch_scores_ht<2, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, row_counts, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream);
     case 64:
       return launch_scores_ht<4, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, row_counts, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream);
     default:
       return fail(KS_ERR_INVALID, "indexer scores: H=%lld, supported: 16, 32, 64", (long long)H);
   }
@@ -767,13 +829,13 @@ int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, i
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
                           int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds,
-                          float *kmax, uint32_t *row_counts) {
+                          float *kmax, uint32_t *row_counts, const float *ksc) {
   if (D == 128)
     return launch_scores_d<128>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                                bound_c, stats, bounds, kmax, row_counts, stream);
+                                bound_c, stats, bounds, kmax, row_counts, ksc, stream);
   if (D == 64)
     return launch_scores_d<64>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                               bound_c, stats, bounds, kmax, row_counts, stream);
+                               bound_c, stats, bounds, kmax, row_counts, ksc, stream);
   return fail(KS_ERR_INVALID, "indexer scores: D=%lld, supported: 64, 128", (long long)D);
 }
 

@@ -574,8 +574,9 @@ struct RecWave {
 // half-widths: bound_c 2^-23 ||q_h|| times the key block's norm maximum) keep the relu'd lower ends of all
 // 64 heads; the tile's near-tie dots are then recomputed exactly, 16 at a time with a quad of lanes per dot
 // (q_h and the key row from LDS: exact_dot_bf16's arithmetic), and the fp32 fma head sum runs in the
-// canonical order over the corrected values.
-template <int NW>
+// canonical order over the corrected values.  F8: the key rows are e4m3 codes with row scales, dequantised in
+// registers to the contract's bf16 rows (q comes dequantised).
+template <int NW, bool F8>
 __device__ void recompute_scores(int32_t *list, int n, float *srow, float *urow, const TopkRecompute &rc,
                                  const RecShared &rs, RecWave &rw, int64_t kbrow0, int64_t kmax_row0, float qpmax,
                                  uint32_t &n_exact, uint32_t &n_unres) {
@@ -589,10 +590,27 @@ __device__ void recompute_scores(int32_t *list, int n, float *srow, float *urow,
     const int64_t krow = kbrow0 + col;
     // the tile's loads go out together (one round trip): key rows, key span, key-block norm maximum
     uint4 kb[kRecD / 32];
+    uint2 kc8[F8 ? kRecD / 32 : 1];
+    float kscale = 0.f;
+    if constexpr (F8) {
 #pragma unroll
-    for (int kk = 0; kk < kRecD / 32; ++kk) kb[kk] = *reinterpret_cast<const uint4 *>(rc.k + krow * kRecD + 32 * kk + 8 * g);
+      for (int kk = 0; kk < kRecD / 32; ++kk) kc8[kk] = *reinterpret_cast<const uint2 *>(rc.kc + krow * kRecD + 32 * kk + 8 * g);
+      kscale = rc.ks[krow];
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < kRecD / 32; ++kk) kb[kk] = *reinterpret_cast<const uint4 *>(rc.k + krow * kRecD + 32 * kk + 8 * g);
+    }
     const int32_t ksv = rc.ksp[krow];
     const float knm = rc.kmax[kmax_row0 + col / kScoreKeyBlock];
+    if constexpr (F8) {
+      if (__builtin_amdgcn_ballot_w64(!fp8_scale_pow2(kscale)) == 0ull) {
+#pragma unroll
+        for (int kk = 0; kk < kRecD / 32; ++kk) kb[kk] = fp8_dequant8<true>(kc8[kk], kscale);
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < kRecD / 32; ++kk) kb[kk] = fp8_dequant8<false>(kc8[kk], kscale);
+      }
+    }
 #pragma unroll
     for (int kk = 0; kk < kRecD / 32; ++kk) rw.k[l16 * kRecC + ((4 * kk + g) ^ l16)] = kb[kk];
     rw.ksp[l16] = ksv;  // the four lanes of a key write the same span; read by the near-tie dots below
@@ -806,7 +824,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_slice_hist_kernel(const flo
 //    reserved on the row's length counter: the exact key of each, or 0 where the exact score fell below tau; the
 //    row state also receives tau and an upper bound of its largest key (the largest upper end).
 // Row state (4 x 32 bits per row): list length (slots reserved), tau, largest key bound, unused.
-template <int KPB>
+template <int KPB, bool F8>
 __global__ __launch_bounds__(kRecThreads, 4) void topk_recompute_kernel(float *scores, int64_t ld, int64_t S, int T,
                                                                     int k, int causal, int64_t start_pos, int ratio,
                                                                     TopkRecompute rc, int segs, int NP,
@@ -961,7 +979,7 @@ __global__ __launch_bounds__(kRecThreads, 4) void topk_recompute_kernel(float *s
   if (ncand > 0) {
     const int64_t kbrow0 = b * rc.kbs;
     const int64_t kmax_row0 = b * ((T + kScoreKeyBlock - 1) / kScoreKeyBlock);
-    recompute_scores<kRecWaves>(list, static_cast<int>(ncand), srow, urow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0, qpmax,
+    recompute_scores<kRecWaves, F8>(list, static_cast<int>(ncand), srow, urow, rc, rs, rw[tid >> 6], kbrow0, kmax_row0, qpmax,
                                 n_exact, n_unres);
   }
   // each wave, its own recomputation done (the atomics wait behind no tile load, and the last wave, which holds
@@ -1230,12 +1248,20 @@ int ks::launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_
     KS_CHECK_LAUNCH("topk_slice_hist_kernel");
   }
   const dim3 rgrid(static_cast<unsigned>(rows * segs));
-#define KS_REC(KPB_)                                                                                             \
-  hipLaunchKernelGGL(topk_recompute_kernel<KPB_>, rgrid, dim3(kRecThreads), 0, st, scores, ld, S, Ti, ki, c, start_pos, \
-                     ratio, rc, segs, NP, hists, lists, cap, rstate)
-  if (kpb == 2) KS_REC(2);
-  else if (kpb == 4) KS_REC(4);
-  else KS_REC(8);
+  const bool f8 = rc.kc != nullptr;
+  KS_CHECK_ARG(f8 == (rc.ks != nullptr), "indexer top-k (bounded): FP8 keys need codes and scales");
+#define KS_REC(KPB_, F8_)                                                                                           \
+  hipLaunchKernelGGL((topk_recompute_kernel<KPB_, F8_>), rgrid, dim3(kRecThreads), 0, st, scores, ld, S, Ti, ki, c, \
+                     start_pos, ratio, rc, segs, NP, hists, lists, cap, rstate)
+  if (f8) {
+    if (kpb == 2) KS_REC(2, true);
+    else if (kpb == 4) KS_REC(4, true);
+    else KS_REC(8, true);
+  } else {
+    if (kpb == 2) KS_REC(2, false);
+    else if (kpb == 4) KS_REC(4, false);
+    else KS_REC(8, false);
+  }
 #undef KS_REC
   KS_CHECK_LAUNCH("topk_recompute_kernel");
   const size_t shmem = static_cast<size_t>(2 * cap) * sizeof(uint64_t);

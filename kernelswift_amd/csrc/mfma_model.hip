@@ -63,6 +63,55 @@ __global__ __launch_bounds__(64) void mfma_fp8_chain_kernel(const uint8_t *__res
   for (int i = 0; i < 4; ++i) d[t * 256 + (4 * g + i) * 16 + r] = acc[i];
 }
 
+// The plain fp8 instruction v_mfma_f32_16x16x32_fp8_fp8 (OCP e4m3 on gfx950): a [t][nchain][16 rows][32 k],
+// bt [t][nchain][16 cols][32 k]; lane l holds row l % 16, k = 8 (l / 16) .. + 7 (8 bytes).
+__global__ __launch_bounds__(64) void mfma_fp8_plain_chain_kernel(const uint8_t *__restrict__ a,
+                                                                 const uint8_t *__restrict__ bt,
+                                                                 const float *__restrict__ c, float *__restrict__ d,
+                                                                 int nchain) {
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+  f32x4_t acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = c[t * 256 + (4 * g + i) * 16 + r];
+  for (int j = 0; j < nchain; ++j) {
+    const int64_t base = (t * nchain + j) * 512;
+    const long av = *reinterpret_cast<const long *>(a + base + r * 32 + 8 * g);
+    const long bv = *reinterpret_cast<const long *>(bt + base + r * 32 + 8 * g);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(av, bv, acc, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[t * 256 + (4 * g + i) * 16 + r] = acc[i];
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Hardware conversions of e4m3 codes, four codes per thread: mode 0 writes fp32 values (v_cvt_pk_f32_fp8), mode 1
+// bf16 values of code * scales[i] (v_cvt_scalef32_pk_bf16_fp8, scale scales[4 t] for the thread's four codes).
+__global__ __launch_bounds__(256) void fp8_cvt_kernel(const uint32_t *__restrict__ codes, const float *__restrict__ scales,
+                                                     int mode, void *__restrict__ out, int64_t n4) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= n4) return;
+  const uint32_t v = codes[t];
+  if (mode == 0) {
+    const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(v), false);
+    const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(v), true);
+    float *o = static_cast<float *>(out) + 4 * t;
+    o[0] = lo[0];
+    o[1] = lo[1];
+    o[2] = hi[0];
+    o[3] = hi[1];
+  } else {
+    const float s = scales[4 * t];
+    const bf16x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, s, false);
+    const bf16x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, s, true);
+    uint32_t *o = static_cast<uint32_t *>(out) + 2 * t;
+    o[0] = __builtin_bit_cast(uint32_t, lo);
+    o[1] = __builtin_bit_cast(uint32_t, hi);
+  }
+}
+
 // out[i] = exact_dot_wide_bf16 of rows q[i] and k[i] (length D), PARTS lanes per dot.
 template <int D, int PARTS>
 __global__ __launch_bounds__(64) void exact_dot_wide_kernel(const uint16_t *__restrict__ q, const uint16_t *__restrict__ k,
@@ -132,5 +181,39 @@ extern "C" int ks_dbg_mfma_bf16_chain(const uint16_t *a, const uint16_t *bt, con
   hipLaunchKernelGGL(ks::mfma_chain_kernel, dim3(static_cast<unsigned>(ntests)), dim3(64), 0,
                      static_cast<hipStream_t>(stream), a, bt, c, d, static_cast<int>(nchain));
   KS_CHECK_LAUNCH("mfma_chain_kernel");
+  return KS_OK;
+}
+
+// Not part of the public header (a test instrument): the plain fp8 instruction, as ks_dbg_mfma_bf16_chain with
+// byte operands (a [t][nchain][16][32], bt [t][nchain][16][32]).
+extern "C" int ks_dbg_mfma_fp8_plain_chain(const uint8_t *a, const uint8_t *bt, const float *c, float *d,
+                                           int64_t ntests, int32_t nchain, void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(ntests >= 0 && ntests < (int64_t(1) << 31), "ks_dbg_mfma_fp8_plain_chain: ntests out of range");
+  KS_CHECK_ARG(nchain >= 1 && nchain <= 64, "ks_dbg_mfma_fp8_plain_chain: nchain must be in [1, 64]");
+  if (ntests == 0) return KS_OK;
+  KS_CHECK_ARG(a && bt && c && d, "ks_dbg_mfma_fp8_plain_chain: null pointer");
+  KS_CHECK_ARG(ks::aligned(a, 8) && ks::aligned(bt, 8), "ks_dbg_mfma_fp8_plain_chain: operands must be 8-byte aligned");
+  hipLaunchKernelGGL(ks::mfma_fp8_plain_chain_kernel, dim3(static_cast<unsigned>(ntests)), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), a, bt, c, d, static_cast<int>(nchain));
+  KS_CHECK_LAUNCH("mfma_fp8_plain_chain_kernel");
+  return KS_OK;
+}
+
+// Not part of the public header (a test instrument): hardware conversions of n codes (n a multiple of 4).
+// mode 0: out fp32 [n] = the codes' values; mode 1: out bf16 [n] = code * scales[4 (i / 4)] as the scaled
+// conversion computes it.
+extern "C" int ks_dbg_fp8_cvt(const uint8_t *codes, const float *scales, int64_t n, int32_t mode, void *out,
+                              void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(n >= 0 && n % 4 == 0 && n < (int64_t(1) << 32), "ks_dbg_fp8_cvt: n must be a multiple of 4");
+  KS_CHECK_ARG(mode == 0 || mode == 1, "ks_dbg_fp8_cvt: mode must be 0 or 1");
+  if (n == 0) return KS_OK;
+  KS_CHECK_ARG(codes && out && (mode == 0 || scales), "ks_dbg_fp8_cvt: null pointer");
+  KS_CHECK_ARG(ks::aligned(codes, 4) && ks::aligned(out, 8), "ks_dbg_fp8_cvt: alignment");
+  hipLaunchKernelGGL(ks::fp8_cvt_kernel, dim3(static_cast<unsigned>(ks::ceil_div(n / 4, 256))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), reinterpret_cast<const uint32_t *>(codes), scales, mode, out,
+                     n / 4);
+  KS_CHECK_LAUNCH("fp8_cvt_kernel");
   return KS_OK;
 }

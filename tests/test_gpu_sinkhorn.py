@@ -62,10 +62,12 @@ def test_sinkhorn_large_doubly_stochastic(device):
     assert np.max(np.abs(y.cpu().numpy() - want)) < 1e-4
 
 
-@pytest.mark.parametrize("shape,repeat", [((65536, 4, 4), 10), ((65536 + 77, 4, 4), 10), ((3, 25001, 4, 4), 5)])
+@pytest.mark.parametrize("shape,repeat", [((65536, 4, 4), 10), ((65536 + 77, 4, 4), 10), ((3, 25001, 4, 4), 5),
+                                          ((786432 + 77, 4, 4), 10), ((2 * 786432 + 5, 4, 4), 2)])
 def test_sinkhorn_matrix_per_lane_ragged(device, shape, repeat):
     # batches from 65536 matrices on take the matrix-per-lane kernel; ragged tails leave part of the last
-    # wave idle
+    # wave idle.  Its waves are persistent (12 workgroups of 4 waves per CU: 786432 matrices per stride on 256
+    # CUs), so the last two shapes end in a ragged batch reached on a wave's second and third pass.
     g = torch.Generator().manual_seed(sum(shape) + repeat)
     x = (torch.randn(shape, generator=g) * 3).to(device)
     got = _run(x, repeat)

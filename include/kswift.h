@@ -104,8 +104,9 @@ int ks_rope_inplace(uint16_t *x, const float *freqs, int64_t B, int64_t S,
  * scores: f32 [B, S, T].  D must be 64 or 128 (the head dims the kernel is
  * built for); H in {16, 32, 64}; T >= 1.
  * Exact for all finite inputs: the MFMA sum is trusted only when an interval of
- * half-width 13 * 2^-23 * (||q|| + 2^-122)(||k|| + 2^-122) + 2^-144 around it
- * rounds to one bf16 value (a bound derived from the instruction's accumulation);
+ * half-width C * 2^-23 * (||q|| + 2^-122)(||k|| + 2^-122) + 2^-144 around it
+ * rounds to one bf16 value (C = 13 for D = 128, 9 for D = 64: a bound derived
+ * from the instruction's accumulation over D / 8 steps);
  * other dots are recomputed exactly (double precision, or an integer accumulator
  * for rows of any dynamic range), and rows whose norm product reaches 2^126 are
  * recomputed in full.  Scores must not come out NaN (an infinite dot times a zero

@@ -73,6 +73,7 @@ DEBUG_SIGNATURES = {
     "ks_dbg_fp8_cvt": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i32, _c_p, _c_p]),
     "ks_dbg_exact_dot_wide": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_p]),
     "ks_dbg_score_bound_c": (ctypes.c_float, []),
+    "ks_dbg_score_bound_c_d": (ctypes.c_float, [_c_i64]),
 }
 
 _lib = None

@@ -225,7 +225,7 @@ extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, i
                           int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream) {
   return indexer_impl(q, k, w, w_bf16, freqs, freq_rows, rope_start, rope_dim, rope_k, k_top, causal, start_pos, ratio,
                       offset, out, out_i64, B, S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream,
-                      ks::kScoreBoundC, nullptr, 0);
+                      ks::score_bound_c(D), nullptr, 0);
 }
 
 // Diagnostic variant (not part of the public header): explicit error-bound constant, path choice (0 auto,
@@ -248,7 +248,8 @@ extern "C" int ks_indexer_fp8(const uint8_t *q, const float *q_scale, const uint
                               int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
                               size_t workspace_bytes, void *stream) {
   return indexer_fp8_impl(q, q_scale, k, k_scale, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B,
-                          S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, ks::kScoreBoundC, nullptr, 0);
+                          S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, ks::score_bound_c(D), nullptr,
+                          0);
 }
 
 // Diagnostic variant of ks_indexer_fp8 with the path choice and counters of ks_dbg_indexer.
@@ -258,6 +259,6 @@ extern "C" int ks_dbg_indexer_fp8(const uint8_t *q, const float *q_scale, const 
                                   int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
                                   size_t workspace_bytes, void *stream, uint32_t *stats, int32_t path) {
   return indexer_fp8_impl(q, q_scale, k, k_scale, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B,
-                          S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, ks::kScoreBoundC, stats,
+                          S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, ks::score_bound_c(D), stats,
                           path);
 }

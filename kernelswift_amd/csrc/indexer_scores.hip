@@ -17,7 +17,8 @@
 // head group g = l/16, so the head sum runs in-lane and two permlane swaps finish ((G0+G1)+(G2+G3)).
 //
 // Exactness: the MFMA fp32 sum A differs from the exact dot by at most the half-width
-//   delta = C * 2^-23 * (||q_h|| + 2^-122)(max_t ||k_t|| + 2^-122) + 2^-144   (C = kScoreBoundC = 13),
+//   delta = C * 2^-23 * (||q_h|| + 2^-122)(max_t ||k_t|| + 2^-122) + 2^-144   (C = score_bound_c(D): 13 for
+//   D = 128, 9 for D = 64),
 // derived from the instruction's accumulation (see dot_halfwidth), so the relu'd bf16 value is exact when
 // RNE(A - delta) and RNE(A + delta) agree after the ReLU (one packed convert and one packed max per pair of
 // dots and interval end).  Keys with a disagreeing ("near-tie") dot are deferred: both interval ends of all
@@ -80,6 +81,30 @@ struct ScoresLds {
   float dl[kQW][64];                 // each wave's interval half-widths, one per head
   float w[kQW][64];                  // each wave's head weights (fp32)
 };
+
+// Canonical sum of one lane's head group (heads 16 m + 4 g + r, m = 0 .. HT - 1, r = 0 .. 3, in that order) from
+// the relu'd bf16 values word(2 m + r / 2) (packed pairs): fp32 weights, G = fma(r_h, w_h, G); bf16 weights,
+// G = G + bf16(r_h w_h), the two products of a pair rounded together by one v_cvt_pk_bf16_f32 (RNE, the same
+// results as the software rounding for every non-NaN value) and added in head order.
+template <int HT, bool WBF, typename Word>
+__device__ __forceinline__ float group_sum(Word word, const float (&wv)[HT][4]) {
+  float G = 0.f;
+#pragma unroll
+  for (int m = 0; m < HT; ++m)
+#pragma unroll
+    for (int rp = 0; rp < 2; ++rp) {
+      const uint32_t p2 = word(2 * m + rp);
+      if constexpr (WBF) {
+        const uint32_t pr = cvt_pk_bf16(unpack_lo(p2) * wv[m][2 * rp], unpack_hi(p2) * wv[m][2 * rp + 1]);
+        G = G + unpack_lo(pr);
+        G = G + unpack_hi(pr);
+      } else {
+        G = __builtin_fmaf(unpack_lo(p2), wv[m][2 * rp], G);
+        G = __builtin_fmaf(unpack_hi(p2), wv[m][2 * rp + 1], G);
+      }
+    }
+  return G;
+}
 
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
@@ -239,19 +264,7 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
   //    e with this lane's own head weights, the rows combine as in the main loop
   for (int eb = 0; eb < nent; eb += 16) {
     const int e = min(eb + l16, nent - 1);
-    float G = 0.f;
-#pragma unroll
-    for (int m = 0; m < HT; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t p2 = E[e].pl[g][2 * m + (r >> 1)];
-        const float rv = (r & 1) ? unpack_hi(p2) : unpack_lo(p2);
-        if constexpr (WBF) {
-          G = G + round_bf16_f(rv * wv[m][r]);
-        } else {
-          G = __builtin_fmaf(rv, wv[m][r], G);
-        }
-      }
+    const float G = group_sum<HT, WBF>([&](int i) { return E[e].pl[g][i]; }, wv);
     const float tot = combine_groups(G);
     const int key = E[e].key;
     if (g == 0 && eb + l16 < nent && key < T) orow[key] = (key < limit) ? (WBF ? round_bf16_f(tot) : tot) : -INFINITY;
@@ -576,18 +589,18 @@ indexer_scores_kernel(
     }
     // canonical head sum of this lane's group, then ((G0+G1)+(G2+G3)) across the rows
     float G = 0.f;
+    if constexpr (WBF) {
+      G = group_sum<HT, WBF>([&](int i) { return pl[i]; }, wv);
+    } else {
 #pragma unroll
-    for (int m = 0; m < HT; ++m)
+      for (int m = 0; m < HT; ++m)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t p2 = pl[2 * m + (r >> 1)];
-        const float rv = (r & 1) ? unpack_hi(p2) : unpack_lo(p2);
-        if constexpr (WBF) {
-          G = G + round_bf16_f(rv * wv[m][r]);
-        } else {
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t p2 = pl[2 * m + (r >> 1)];
+          const float rv = (r & 1) ? unpack_hi(p2) : unpack_lo(p2);
           G = __builtin_fmaf(rv, wv[m][r], G);
         }
-      }
+    }
     if constexpr (BOUND) {
       // the next tile's 16 MFMAs (issued before this epilogue, in the same basic block) spread over the interval
       // test and the head sum, one per 6 VALU instructions: the wave keeps issuing VALU work while the matrix
@@ -871,12 +884,14 @@ extern "C" int ks_indexer_scores(const uint16_t *q, const uint16_t *k, const voi
   if (rc != KS_OK) return rc;
   if (B * S == 0) return KS_OK;
   return ks::launch_indexer_scores(q, k, w, w_bf16 ? 1 : 0, q_norm, q_span, k_norm, k_span, scores, B, S, H, D,
-                                   T, k_batch_stride, causal ? 1 : 0, start_pos, ratio, ks::kScoreBoundC, nullptr,
+                                   T, k_batch_stride, causal ? 1 : 0, start_pos, ratio, ks::score_bound_c(D), nullptr,
                                    static_cast<hipStream_t>(stream));
 }
 
-// Diagnostic (not part of the public header): the interval constant the public entry points use.
+// Diagnostic (not part of the public header): the interval constant the public entry points use for 128-dim
+// dots, and for D-dimensional ones.
 extern "C" float ks_dbg_score_bound_c(void) { return ks::kScoreBoundC; }
+extern "C" float ks_dbg_score_bound_c_d(int64_t D) { return ks::score_bound_c(D); }
 
 // Diagnostic variant (not part of the public header): explicit error-bound constant and a device counter
 // pair stats[0] += exact recomputations, stats[1] += dots outside the provably exact range.

@@ -18,7 +18,10 @@ BOUND_C = 13.0  # the interval constant derived for the MFMA accumulation (check
 
 
 def test_bound_constant_is_the_derived_one(device):
-    assert _lib.load().ks_dbg_score_bound_c() == BOUND_C
+    lib = _lib.load()
+    assert lib.ks_dbg_score_bound_c() == BOUND_C
+    # 64-dim dots (8 accumulation steps, tests/test_mfma_model.py::test_error_bound_of_64_dim_dots)
+    assert lib.ks_dbg_score_bound_c_d(128) == BOUND_C and lib.ks_dbg_score_bound_c_d(64) == 9.0
 
 
 def _u16(t):
@@ -274,6 +277,29 @@ def test_scores_adversarial_accumulation(device):
     want = _oracle_scores(q, k, w, False, 0)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
     assert got[0, 0, 0] == got[0, 0, 1]  # the two keys tie exactly
+
+
+@pytest.mark.parametrize("H", [16, 64])
+def test_scores_adversarial_accumulation_64_dim(device, H):
+    # the 64-dim adversarial row (its MFMA accumulation rounds past the bf16 midpoint) through the public exact
+    # score entry, which takes the 64-dim constant: scores bit-exact against the oracle, both weight formats
+    from tests.test_mfma_model import adversarial_rows
+    qb, kb = adversarial_rows(13, 64)
+    q1 = torch.from_numpy(qb.view(np.int16)).view(torch.bfloat16)
+    k1 = torch.from_numpy(kb.view(np.int16)).view(torch.bfloat16)
+    g = torch.Generator().manual_seed(7)
+    S, T = 4, 96
+    q = torch.randn(1, S, H, 64, generator=g).bfloat16()
+    q[0, 0, :] = q1
+    k = torch.randn(1, T, 64, generator=g).bfloat16()
+    k[0, 0] = 0
+    k[0, 0, 0] = 1.0  # dot with q1 exactly 1
+    k[0, 1] = k1
+    print(f"[case] scores adversarial accumulation D=64 H={H}", flush=True)
+    for w in ((torch.rand(1, S, H, generator=g) + 0.5) / 8, ((torch.rand(1, S, H, generator=g) + 0.5) / 8).bfloat16()):
+        got = ops.indexer_scores(q.to(device), k.to(device), w.to(device), False, 0, 1).cpu().numpy()
+        want = _oracle_scores(q, k, w, False, 0)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 @pytest.mark.parametrize("path", [1, 2])

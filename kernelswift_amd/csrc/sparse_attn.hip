@@ -597,6 +597,14 @@ __device__ __forceinline__ void mfma_agpr_leave(f32x4_t (&o)[2][CT]) {
                  "+a"(o[1][c + 1]), "+a"(o[1][c + 2]), "+a"(o[1][c + 3]));
 }
 
+// Partial ranges of the MLA kernel in its own register layout ("fragment layout"): range `item`, wave w, head tile
+// ht, pair of column tiles cp = cc / 2, lane l = l16 + 16 g holds the 16-byte unit
+//   bf16 of O[head 32 w + 16 ht + 4 g + r][column 16 cc + l16] for (cc, r) = (2 cp, 0..3), (2 cp + 1, 0..3),
+// units ordered [item][w][ht][cp][lane] (the same bytes as row-major partials: H = 32 NW heads x 512 columns).
+__host__ __device__ inline int64_t mla_frag_offset(int64_t item, int NW, int w, int ht, int cp, int lane) {
+  return (((item * NW + w) * 2 + ht) * 16 + cp) * 64 + lane;
+}
+
 template <int NW, int NBUF>
 __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ kv, const float *__restrict__ sink,
@@ -833,19 +841,160 @@ __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
           scale_o = den > 0.f ? e / den : 0.f;
         }
       }
-      uint16_t *orow = (NS == 1 ? out : part_o) + (obase * H + hr) * Sh::DV;
+      if (NS == 1) {
+        uint16_t *orow = out + (obase * H + hr) * Sh::DV;
 #pragma unroll
-      for (int cc = 0; cc < CT; cc += 2) {  // one packed convert per two column tiles
-        const uint32_t pk = pack_bf16x2(o[ht][cc][r] * scale_o, o[ht][cc + 1][r] * scale_o);
-        orow[16 * cc + l16] = static_cast<uint16_t>(pk & 0xFFFFu);
-        orow[16 * (cc + 1) + l16] = static_cast<uint16_t>(pk >> 16);
+        for (int cc = 0; cc < CT; cc += 2) {  // one packed convert per two column tiles
+          const uint32_t pk = pack_bf16x2(o[ht][cc][r] * scale_o, o[ht][cc + 1][r] * scale_o);
+          orow[16 * cc + l16] = static_cast<uint16_t>(pk & 0xFFFFu);
+          orow[16 * (cc + 1) + l16] = static_cast<uint16_t>(pk >> 16);
+        }
       }
+    }
+    if (NS > 1) {
+      // the partial range in the fragment layout (mla_frag_offset): one 16-byte store per lane and pair of column
+      // tiles, the wave's 64 lanes writing 1 KiB contiguously (row-major rows would take 2-byte stores)
+      uint4 *pf = reinterpret_cast<uint4 *>(part_o) + mla_frag_offset(item, NW, wave, ht, 0, lane);
+#pragma unroll
+      for (int cc = 0; cc < CT; cc += 2)
+        pf[(cc / 2) * 64] = make_uint4(pack_bf16x2(o[ht][cc][0], o[ht][cc][1]), pack_bf16x2(o[ht][cc][2], o[ht][cc][3]),
+                                       pack_bf16x2(o[ht][cc + 1][0], o[ht][cc + 1][1]),
+                                       pack_bf16x2(o[ht][cc + 1][2], o[ht][cc + 1][3]));
     }
     if (NS > 1 && g == 0) {
       float *pml = part_ml + (item * H + 32 * wave + 16 * ht + l16) * 2;
       pml[0] = m_ref[ht];
       pml[1] = l_run[ht];
     }
+  }
+}
+
+
+// 16-byte units (two column tiles each) per lane and range: one unit per lane gives 4096 waves at config 5 (two
+// units: 2048 waves, 0.3 us slower, within the noise)
+constexpr int kMlaCombineUnits = 1;
+
+// Merge of the MLA kernel's NS partial ranges (fragment layout) with the sink.  A wave owns (query, w, ht, a slice e
+// of UPW units): lane (l16, g) accumulates heads hb + 4 g + r (hb = 32 w + 16 ht, r = 0..3) over the column tiles
+// 2 UPW e .. 2 UPW e + 2 UPW - 1, so every partial read is a 1 KiB contiguous wave access.  The (max, sum) pairs of a
+// group of 8 ranges x the wave's 16 heads are one float4 per lane (lane 8 s + j: range s, heads hb + 2 j, + 1): the
+// weights are formed there and handed to the accumulating lanes by lane shuffles.  Output: lane pairs (l16, l16 ^ 1)
+// swap two of their four heads, so each lane writes two adjacent columns of two heads as 4-byte stores.
+__global__ __launch_bounds__(256) void sparse_attn_mla_combine_kernel(const uint4 *__restrict__ part_f,
+                                                                     const float *__restrict__ part_ml,
+                                                                     const float *__restrict__ sink,
+                                                                     uint16_t *__restrict__ out, int64_t n_q, int NW,
+                                                                     int NS) {
+  constexpr int DV = 512, UPW = kMlaCombineUnits, EPW = 16 / UPW, kGroup = 8;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  // XCD placement of the attention kernel: a query's ranges were written on one XCD (block id mod 8)
+  const int64_t nblk = gridDim.x;
+  const int64_t lb = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int64_t wv = lb * 4 + (threadIdx.x >> 6);  // (query, w, ht, e)
+  const int64_t per_q = static_cast<int64_t>(NW) * 2 * EPW;
+  if (wv >= n_q * per_q) return;  // uniform per wave
+  const int64_t qm = wv / per_q;
+  const int rem = static_cast<int>(wv % per_q);
+  const int w = rem / (2 * EPW), ht = (rem / EPW) % 2, e = rem % EPW;
+  const int H = 32 * NW;
+  const int hb = 32 * w + 16 * ht;
+  const int ls = lane >> 3, lj = lane & 7;  // (max, sum) loader: range ls of a group, heads hb + 2 lj, + 1
+  auto load_ml = [&](int s0) {
+    const int sr = s0 + ls;
+    const float4 v =
+        *reinterpret_cast<const float4 *>(part_ml + ((qm * NS + (sr < NS ? sr : NS - 1)) * H + hb + 2 * lj) * 2);
+    return sr < NS ? v : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+  };
+  auto load_units = [&](int s0, uint4 (&fv)[kGroup][UPW]) {
+#pragma unroll
+    for (int s = 0; s < kGroup; ++s) {
+      const uint4 *pf = part_f + mla_frag_offset(qm * NS + (s0 + s < NS ? s0 + s : NS - 1), NW, w, ht, UPW * e, lane);
+#pragma unroll
+      for (int u = 0; u < UPW; ++u) fv[s][u] = pf[64 * u];
+    }
+  };
+  // every load of the first group goes out before the first wait
+  const float4 ml0 = load_ml(0);
+  uint4 f0[kGroup][UPW];
+  load_units(0, f0);
+  const float sk0 = sink[hb + 2 * lj], sk1 = sink[hb + 2 * lj + 1];
+  __builtin_amdgcn_sched_barrier(0);  // keep the loads above the reduction
+  // the largest logit of the loader's two heads: the ranges' maxima and the sink
+  float z0 = sk0 * kLog2e, z1 = sk1 * kLog2e;
+  z0 = fmaxf(z0, ml0.x);
+  z1 = fmaxf(z1, ml0.z);
+  for (int s0 = kGroup; s0 < NS; s0 += kGroup) {
+    const float4 v = load_ml(s0);
+    z0 = fmaxf(z0, v.x);
+    z1 = fmaxf(z1, v.z);
+  }
+#pragma unroll
+  for (int d = 8; d < 64; d <<= 1) {
+    z0 = fmaxf(z0, __shfl_xor(z0, d, 64));
+    z1 = fmaxf(z1, __shfl_xor(z1, d, 64));
+  }
+  float acc[4][2 * UPW];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int i = 0; i < 2 * UPW; ++i) acc[r][i] = 0.f;
+  float dp0 = 0.f, dp1 = 0.f;  // the loader's share of the denominators
+  // one group: weights on the loaders, then each range's units weighted per head
+  auto group = [&](int s0, const float4 &v, const uint4 (&fv)[kGroup][UPW]) {
+    const float w0 = (v.x == -INFINITY || z0 == -INFINITY) ? 0.f : exp2f(v.x - z0);
+    const float w1 = (v.z == -INFINITY || z1 == -INFINITY) ? 0.f : exp2f(v.z - z1);
+    dp0 += w0 * v.y;
+    dp1 += w1 * v.w;
+#pragma unroll
+    for (int s = 0; s < kGroup; ++s) {
+      if (s0 + s >= NS) break;  // uniform
+      float ws[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ws[r] = __shfl((r & 1) ? w1 : w0, kGroup * s + 2 * g + (r >> 1), 64);
+#pragma unroll
+      for (int u = 0; u < UPW; ++u) {
+        const uint32_t x[4] = {fv[s][u].x, fv[s][u].y, fv[s][u].z, fv[s][u].w};  // (tile 2u: r 0 1, r 2 3), ...
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          acc[0][2 * u + t] += ws[0] * __builtin_bit_cast(float, x[2 * t] << 16);
+          acc[1][2 * u + t] += ws[1] * __builtin_bit_cast(float, x[2 * t] & 0xFFFF0000u);
+          acc[2][2 * u + t] += ws[2] * __builtin_bit_cast(float, x[2 * t + 1] << 16);
+          acc[3][2 * u + t] += ws[3] * __builtin_bit_cast(float, x[2 * t + 1] & 0xFFFF0000u);
+        }
+      }
+    }
+  };
+  group(0, ml0, f0);
+  for (int s0 = kGroup; s0 < NS; s0 += kGroup) {
+    const float4 v = load_ml(s0);
+    uint4 fv[kGroup][UPW];
+    load_units(s0, fv);
+    group(s0, v, fv);
+  }
+#pragma unroll
+  for (int d = 8; d < 64; d <<= 1) {
+    dp0 += __shfl_xor(dp0, d, 64);
+    dp1 += __shfl_xor(dp1, d, 64);
+  }
+  const float den0 = dp0 + (z0 == -INFINITY ? 0.f : exp2f(sk0 * kLog2e - z0));
+  const float den1 = dp1 + (z1 == -INFINITY ? 0.f : exp2f(sk1 * kLog2e - z1));
+  const float iv0 = den0 > 0.f ? 1.f / den0 : 0.f, iv1 = den1 > 0.f ? 1.f / den1 : 0.f;
+  float inv[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) inv[r] = __shfl((r & 1) ? iv1 : iv0, 2 * g + (r >> 1), 64);
+  // even l16 keeps heads r = 0, 2 and receives its odd neighbour's; odd l16 keeps r = 1, 3
+  const bool odd = (l16 & 1) != 0;
+  uint16_t *obase = out + (qm * H + hb + 4 * g) * DV + 16 * (2 * UPW * e) + (l16 & ~1);
+#pragma unroll
+  for (int i = 0; i < 2 * UPW; ++i) {
+    const float v0 = acc[0][i] * inv[0], v1 = acc[1][i] * inv[1], v2 = acc[2][i] * inv[2], v3 = acc[3][i] * inv[3];
+    const float y0 = __shfl_xor(odd ? v0 : v1, 1, 64);
+    const float y1 = __shfl_xor(odd ? v2 : v3, 1, 64);
+    const int ra = odd ? 1 : 0;  // rows ra and ra + 2
+    const uint32_t wa = odd ? pack_bf16x2(y0, v1) : pack_bf16x2(v0, y0);
+    const uint32_t wb = odd ? pack_bf16x2(y1, v3) : pack_bf16x2(v2, y1);
+    *reinterpret_cast<uint32_t *>(obase + ra * DV + 16 * i) = wa;
+    *reinterpret_cast<uint32_t *>(obase + (ra + 2) * DV + 16 * i) = wb;
   }
 }
 
@@ -994,10 +1143,11 @@ int launch_mla_nw(const uint16_t *q, const uint16_t *kv, const float *sink, cons
                      K, sp.ns, sp.kr, scale * kLog2e);
   KS_CHECK_LAUNCH("sparse_attn_mla_kernel");
   if (sp.ns > 1) {
-    const int64_t rows = B * M * H;
-    hipLaunchKernelGGL((sparse_attn_combine_kernel<512>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
-                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), sp.ns);
-    KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
+    // waves of (query, wave of the attention kernel, head tile, column tiles of kMlaCombineUnits units)
+    const int64_t waves = B * M * NW * 2 * (16 / kMlaCombineUnits);
+    hipLaunchKernelGGL(sparse_attn_mla_combine_kernel, dim3(static_cast<unsigned>(ceil_div(waves, 4))), dim3(256), 0,
+                       stream, reinterpret_cast<const uint4 *>(part_o), part_ml, sink, out, B * M, NW, sp.ns);
+    KS_CHECK_LAUNCH("sparse_attn_mla_combine_kernel");
   }
   return KS_OK;
 }

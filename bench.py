@@ -132,13 +132,13 @@ def _cpu_time(fn, budget_s, min_reps=3, max_reps=10):
     return statistics.median(samples), len(samples)
 
 
-def _traffic(name):
+def _traffic(*names):
+    """HBM bytes per launch of the named kernels (summed), from profiles/traffic.json; None if any is absent."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
             d = json.load(f)
-        e = d[name]
-        return int(e["fetch_bytes"] + e["write_bytes"])
+        return int(sum(d[n]["fetch_bytes"] + d[n]["write_bytes"] for n in names))
     except Exception:
         return None
 
@@ -280,8 +280,8 @@ def run_indexer(cfg, steps, warmup, do_cpu, cpu_budget):
                        "topk_rows_kernel (plain, other shapes)": round(topk_us, 3)},
         "roofline": {"bound": "mfma", "kernel": "indexer_scores_kernel (bounded)", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true, true>@{cfg}")
-                     or _traffic(f"indexer_scores_kernel<4, 128, false, true, false>@{cfg}")},
+                     "traffic": _traffic(f"indexer_scores_kernel<4, 128, false, true, true, false>@{cfg}")
+                     or _traffic(f"indexer_scores_kernel<4, 128, false, true, false, false>@{cfg}")},
         # the product's bounded top-k reads a score and a bound (8 B) per column; the plain one 4 B
         "topk_bounded_GBps": round(S * T * 8 / (topkb_us * 1e-6) / 1e9, 1),
         "topk_plain_GBps": round(S * T * 4 / (topk_us * 1e-6) / 1e9, 1),
@@ -388,8 +388,9 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
            "roofline": {"bound": "mfma", "kernel": ("sparse_attn_kernel" if cfg == 3 else "sparse_attn_mla_kernel")
                         + " (+ combine)", "achieved": round(achieved, 2),
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                        "traffic": _traffic(("sparse_attn_kernel<128, 128, 1>" if cfg == 3
-                                             else "sparse_attn_mla_kernel<4, 3>") + f"@{cfg}"),
+                        "traffic": (_traffic("sparse_attn_kernel<128, 128, 1>@3", "sparse_attn_combine_kernel<128>@3")
+                                    if cfg == 3 else
+                                    _traffic("sparse_attn_mla_kernel<4, 3>@5", "sparse_attn_mla_combine_kernel@5")),
                         "cache": ("warm (the 2 MiB kv fits in L2)" if cfg == 3
                                   else "kv 2.25 GiB: gathered rows come from HBM")},
            "gathered_GBps": round(gathered / (op_us * 1e-6) / 1e9, 1)}

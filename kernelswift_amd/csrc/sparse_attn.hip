@@ -874,12 +874,44 @@ __global__ __launch_bounds__(64 * NW, 1) void sparse_attn_mla_kernel(
 // units: 2048 waves, 0.3 us slower, within the noise)
 constexpr int kMlaCombineUnits = 1;
 
+// One DPP lane movement within each 16-lane row: CTRL = 0x150 + n broadcasts lane n of the row (row_newbcast),
+// 0x120 + n rotates the row by n lanes (row_ror).
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// row_newbcast of lane n, for an n that is a constant once the caller's loop is unrolled
+__device__ __forceinline__ float row_bcast(float v, int n) {
+  switch (n) {
+    case 0: return dpp_row<0x150>(v);
+    case 1: return dpp_row<0x151>(v);
+    case 2: return dpp_row<0x152>(v);
+    case 3: return dpp_row<0x153>(v);
+    case 4: return dpp_row<0x154>(v);
+    case 5: return dpp_row<0x155>(v);
+    case 6: return dpp_row<0x156>(v);
+    case 7: return dpp_row<0x157>(v);
+    case 8: return dpp_row<0x158>(v);
+    case 9: return dpp_row<0x159>(v);
+    case 10: return dpp_row<0x15A>(v);
+    case 11: return dpp_row<0x15B>(v);
+    case 12: return dpp_row<0x15C>(v);
+    case 13: return dpp_row<0x15D>(v);
+    case 14: return dpp_row<0x15E>(v);
+    case 15: return dpp_row<0x15F>(v);
+    default: return v;
+  }
+}
+
 // Merge of the MLA kernel's NS partial ranges (fragment layout) with the sink.  A wave owns (query, w, ht, a slice e
 // of UPW units): lane (l16, g) accumulates heads hb + 4 g + r (hb = 32 w + 16 ht, r = 0..3) over the column tiles
-// 2 UPW e .. 2 UPW e + 2 UPW - 1, so every partial read is a 1 KiB contiguous wave access.  The (max, sum) pairs of a
-// group of 8 ranges x the wave's 16 heads are one float4 per lane (lane 8 s + j: range s, heads hb + 2 j, + 1): the
-// weights are formed there and handed to the accumulating lanes by lane shuffles.  Output: lane pairs (l16, l16 ^ 1)
-// swap two of their four heads, so each lane writes two adjacent columns of two heads as 4-byte stores.
+// 2 UPW e .. 2 UPW e + 2 UPW - 1, so every partial read is a 1 KiB contiguous wave access.  The (max, sum) pairs of
+// a group of 8 ranges x the wave's 16 heads are one float4 per lane, laid out so that each 16-lane row holds its own
+// heads: lane (l16, g) loads range l16 / 2, heads hb + 4 g + 2 (l16 & 1) + {0, 1}.  The weights are formed there, the
+// maxima and denominators are reduced over the row's ranges by row rotations, and each weight reaches the
+// accumulating lanes by one row broadcast (DPP: no LDS traffic, no address arithmetic).  Output: lane pairs
+// (l16, l16 ^ 1) swap two of their four heads, so each lane writes two adjacent columns of two heads as 4-byte stores.
 __global__ __launch_bounds__(256) void sparse_attn_mla_combine_kernel(const uint4 *__restrict__ part_f,
                                                                      const float *__restrict__ part_ml,
                                                                      const float *__restrict__ sink,
@@ -898,17 +930,19 @@ __global__ __launch_bounds__(256) void sparse_attn_mla_combine_kernel(const uint
   const int w = rem / (2 * EPW), ht = (rem / EPW) % 2, e = rem % EPW;
   const int H = 32 * NW;
   const int hb = 32 * w + 16 * ht;
-  const int ls = lane >> 3, lj = lane & 7;  // (max, sum) loader: range ls of a group, heads hb + 2 lj, + 1
+  const int ls = l16 >> 1, hp = hb + 4 * g + 2 * (l16 & 1);  // loader: range ls of a group, heads hp, hp + 1
+  const float *mlq = part_ml + (qm * NS * H + hp) * 2;
   auto load_ml = [&](int s0) {
     const int sr = s0 + ls;
-    const float4 v =
-        *reinterpret_cast<const float4 *>(part_ml + ((qm * NS + (sr < NS ? sr : NS - 1)) * H + hb + 2 * lj) * 2);
+    const float4 v = *reinterpret_cast<const float4 *>(mlq + static_cast<int64_t>(sr < NS ? sr : NS - 1) * H * 2);
     return sr < NS ? v : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
   };
+  const uint4 *pfq = part_f + mla_frag_offset(qm * NS, NW, w, ht, UPW * e, lane);
+  const int64_t range_units = static_cast<int64_t>(NW) * 2 * 16 * 64;  // 16-byte units of one range
   auto load_units = [&](int s0, uint4 (&fv)[kGroup][UPW]) {
 #pragma unroll
     for (int s = 0; s < kGroup; ++s) {
-      const uint4 *pf = part_f + mla_frag_offset(qm * NS + (s0 + s < NS ? s0 + s : NS - 1), NW, w, ht, UPW * e, lane);
+      const uint4 *pf = pfq + (s0 + s < NS ? s0 + s : NS - 1) * range_units;
 #pragma unroll
       for (int u = 0; u < UPW; ++u) fv[s][u] = pf[64 * u];
     }
@@ -917,29 +951,29 @@ __global__ __launch_bounds__(256) void sparse_attn_mla_combine_kernel(const uint
   const float4 ml0 = load_ml(0);
   uint4 f0[kGroup][UPW];
   load_units(0, f0);
-  const float sk0 = sink[hb + 2 * lj], sk1 = sink[hb + 2 * lj + 1];
+  const float sk0 = sink[hp] * kLog2e, sk1 = sink[hp + 1] * kLog2e;
   __builtin_amdgcn_sched_barrier(0);  // keep the loads above the reduction
-  // the largest logit of the loader's two heads: the ranges' maxima and the sink
-  float z0 = sk0 * kLog2e, z1 = sk1 * kLog2e;
-  z0 = fmaxf(z0, ml0.x);
-  z1 = fmaxf(z1, ml0.z);
+  // the largest logit of the loader's two heads: the ranges' maxima (rotations over the row's 8 ranges) and the sink
+  float z0 = ml0.x, z1 = ml0.z;
   for (int s0 = kGroup; s0 < NS; s0 += kGroup) {
     const float4 v = load_ml(s0);
     z0 = fmaxf(z0, v.x);
     z1 = fmaxf(z1, v.z);
   }
-#pragma unroll
-  for (int d = 8; d < 64; d <<= 1) {
-    z0 = fmaxf(z0, __shfl_xor(z0, d, 64));
-    z1 = fmaxf(z1, __shfl_xor(z1, d, 64));
-  }
+  z0 = fmaxf(z0, dpp_row<0x122>(z0));
+  z1 = fmaxf(z1, dpp_row<0x122>(z1));
+  z0 = fmaxf(z0, dpp_row<0x124>(z0));
+  z1 = fmaxf(z1, dpp_row<0x124>(z1));
+  z0 = fmaxf(fmaxf(z0, dpp_row<0x128>(z0)), sk0);
+  z1 = fmaxf(fmaxf(z1, dpp_row<0x128>(z1)), sk1);
   float acc[4][2 * UPW];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int i = 0; i < 2 * UPW; ++i) acc[r][i] = 0.f;
   float dp0 = 0.f, dp1 = 0.f;  // the loader's share of the denominators
-  // one group: weights on the loaders, then each range's units weighted per head
+  // one group: weights on the loaders, then each range's units weighted per head (head hb + 4 g + r: lane
+  // 2 s + (r >> 1) of the row, its weight of head r & 1)
   auto group = [&](int s0, const float4 &v, const uint4 (&fv)[kGroup][UPW]) {
     const float w0 = (v.x == -INFINITY || z0 == -INFINITY) ? 0.f : exp2f(v.x - z0);
     const float w1 = (v.z == -INFINITY || z1 == -INFINITY) ? 0.f : exp2f(v.z - z1);
@@ -948,9 +982,8 @@ __global__ __launch_bounds__(256) void sparse_attn_mla_combine_kernel(const uint
 #pragma unroll
     for (int s = 0; s < kGroup; ++s) {
       if (s0 + s >= NS) break;  // uniform
-      float ws[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) ws[r] = __shfl((r & 1) ? w1 : w0, kGroup * s + 2 * g + (r >> 1), 64);
+      const float ws[4] = {row_bcast(w0, 2 * s), row_bcast(w1, 2 * s), row_bcast(w0, 2 * s + 1),
+                           row_bcast(w1, 2 * s + 1)};
 #pragma unroll
       for (int u = 0; u < UPW; ++u) {
         const uint32_t x[4] = {fv[s][u].x, fv[s][u].y, fv[s][u].z, fv[s][u].w};  // (tile 2u: r 0 1, r 2 3), ...
@@ -971,25 +1004,24 @@ __global__ __launch_bounds__(256) void sparse_attn_mla_combine_kernel(const uint
     load_units(s0, fv);
     group(s0, v, fv);
   }
-#pragma unroll
-  for (int d = 8; d < 64; d <<= 1) {
-    dp0 += __shfl_xor(dp0, d, 64);
-    dp1 += __shfl_xor(dp1, d, 64);
-  }
-  const float den0 = dp0 + (z0 == -INFINITY ? 0.f : exp2f(sk0 * kLog2e - z0));
-  const float den1 = dp1 + (z1 == -INFINITY ? 0.f : exp2f(sk1 * kLog2e - z1));
+  dp0 += dpp_row<0x122>(dp0);
+  dp1 += dpp_row<0x122>(dp1);
+  dp0 += dpp_row<0x124>(dp0);
+  dp1 += dpp_row<0x124>(dp1);
+  dp0 += dpp_row<0x128>(dp0);
+  dp1 += dpp_row<0x128>(dp1);
+  const float den0 = dp0 + (z0 == -INFINITY ? 0.f : exp2f(sk0 - z0));
+  const float den1 = dp1 + (z1 == -INFINITY ? 0.f : exp2f(sk1 - z1));
   const float iv0 = den0 > 0.f ? 1.f / den0 : 0.f, iv1 = den1 > 0.f ? 1.f / den1 : 0.f;
-  float inv[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) inv[r] = __shfl((r & 1) ? iv1 : iv0, 2 * g + (r >> 1), 64);
+  const float inv[4] = {dpp_row<0x150>(iv0), dpp_row<0x150>(iv1), dpp_row<0x151>(iv0), dpp_row<0x151>(iv1)};
   // even l16 keeps heads r = 0, 2 and receives its odd neighbour's; odd l16 keeps r = 1, 3
   const bool odd = (l16 & 1) != 0;
   uint16_t *obase = out + (qm * H + hb + 4 * g) * DV + 16 * (2 * UPW * e) + (l16 & ~1);
 #pragma unroll
   for (int i = 0; i < 2 * UPW; ++i) {
     const float v0 = acc[0][i] * inv[0], v1 = acc[1][i] * inv[1], v2 = acc[2][i] * inv[2], v3 = acc[3][i] * inv[3];
-    const float y0 = __shfl_xor(odd ? v0 : v1, 1, 64);
-    const float y1 = __shfl_xor(odd ? v2 : v3, 1, 64);
+    const float y0 = dpp_row<0xB1>(odd ? v0 : v1);  // quad_perm [1,0,3,2]: the lane's neighbour l16 ^ 1
+    const float y1 = dpp_row<0xB1>(odd ? v2 : v3);
     const int ra = odd ? 1 : 0;  // rows ra and ra + 2
     const uint32_t wa = odd ? pack_bf16x2(y0, v1) : pack_bf16x2(v0, y0);
     const uint32_t wb = odd ? pack_bf16x2(y1, v3) : pack_bf16x2(v2, y1);

@@ -1194,6 +1194,215 @@ int launch_mla(const uint16_t *q, const uint16_t *kv, const float *sink, const i
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Small kv sets (N <= 64 keys per batch, Dqk = Dv = 128): the dense count-mask form.  A batch's whole kv fits in
+// LDS, so it is staged once per workgroup and every query scores all N keys densely on the MFMA; the top-k list
+// only says how often each key counts.  Per query and wave (16 heads): the key counts (LDS atomics over the index
+// list: invalid indices count nowhere, duplicates with multiplicity), S^T = K Q^T for all keys, the softmax over
+// the counted keys with the sink, p = count * exp2(s - m), and O^T = V^T P^T, whose output layout gives each lane
+// four consecutive columns of one head (8-byte stores).  Workgroups are persistent over contiguous ranges of
+// query groups (a group never straddles two batches), and each wave loads the next query's q rows and indices
+// before computing the current one.  This replaces the gather kernel where each query's work is one short chunk
+// and the launch is bound by q and output traffic.
+constexpr int kDenseMaxN = 64;
+constexpr int kDenseMaxK = 256;
+constexpr int kDensePrefetch = 2;  // queries in flight per wave beyond the one computed (1 and 3 measured the same)
+
+template <int NC, int KPL, int PD>  // 32-key chunks: N <= 32 NC; indices per lane: K <= 64 KPL; queries prefetched
+__global__ __launch_bounds__(256) void sparse_attn_dense_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kv, const float *__restrict__ sink,
+    const int32_t *__restrict__ idx, uint16_t *__restrict__ out, int64_t M, int H, int N, int K, int GW, int64_t gpb,
+    int64_t per_wg, int64_t rpb, float scale_log2) {
+  using Sh = SaShape<128, 128, 1>;
+  constexpr int D = 128, UPR = 16, NT = 2 * NC, CT = 8;
+  constexpr int KEYS = 32 * NC;
+  __shared__ __attribute__((aligned(16))) uint16_t kvs[KEYS * D];
+  __shared__ __attribute__((aligned(16))) uint32_t cnt[4][KEYS];
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qpi = 4 / GW;                          // queries per group
+  const int qsub = wave / GW, head = 16 * (wave % GW) + l16;
+  // the workgroup's range: groups [g0, g1) of batch bcur (rpb ranges of per_wg groups per batch), so the staged kv
+  // rows never change during the loop
+  const int64_t bcur = blockIdx.x / rpb;
+  const int64_t g0 = bcur * gpb + (blockIdx.x % rpb) * per_wg;
+  const int64_t g1 = g0 + per_wg < (bcur + 1) * gpb ? g0 + per_wg : (bcur + 1) * gpb;
+  if (g0 >= g1) return;  // uniform per workgroup
+
+  // the batch's kv rows into LDS (swizzled like the gather kernel's chunks); rows N .. KEYS - 1 are zero
+  auto stage = [&](int64_t b) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(kv + b * N * D);
+#pragma unroll
+    for (int i = 0; i < KEYS * UPR / 256; ++i) {
+      const int u = tid + 256 * i, key = u / UPR, un = u % UPR;
+      const uint4 v = key < N ? src[key * UPR + un] : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4 *>(kvs + Sh::slot(key, 0, un) * 8) = v;
+    }
+  };
+  // the wave's query row in the batch for group gq; row >= M for the idle waves of a batch's last group
+  auto query_row = [&](int64_t gq) { return (gq - bcur * gpb) * qpi + qsub; };
+  // q B-fragments Q[head][32j + 8g .. +7] and this lane's indices (lane + 64 i): every load unconditional, from a
+  // clamped address (a load behind a branch makes the compiler wait for all loads where the paths join, which
+  // would drain the prefetch); indices past K are masked where they are used (a select on a loaded value here
+  // would wait for the load)
+  auto load = [&](int64_t gq, uint4 (&qf)[4], int32_t (&ix)[KPL]) {
+    const int64_t m = query_row(gq);
+    const int64_t qm = bcur * M + (m < M ? m : M - 1);
+    const uint16_t *qrow = q + (qm * H + head) * D + 8 * g;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qf[j] = *reinterpret_cast<const uint4 *>(qrow + 32 * j);
+    const int32_t *irow = idx + qm * K;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int t = lane + 64 * i;
+      ix[i] = irow[t < K ? t : K - 1];
+    }
+  };
+
+  // per-lane LDS element offsets: QK key 16t + l16, unit 4j + g; PV (transpose reads) keys 4g + (l16 >> 2) (+16),
+  // unit 2cc + ((l16 & 3) >> 1), 8-byte half l16 & 1 (the gather kernel's layout)
+  int qk0[4], pv0[CT];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) qk0[j] = Sh::slot(l16, 0, 4 * j + g) * 8;
+#pragma unroll
+  for (int cc = 0; cc < CT; ++cc)
+    pv0[cc] = Sh::slot(4 * g + (l16 >> 2), 0, 2 * cc + ((l16 & 3) >> 1)) * 8 + 4 * (l16 & 1);
+  const float skl = sink[head] * kLog2e;
+
+  // a ring of PD + 1 queries' q rows and indices in registers: the step computing query gq (slot s) first loads
+  // query gq + PD into the slot that query gq - 1 used.  The loop is unrolled over the ring, so every slot is a
+  // fixed set of registers: moving a value whose load is in flight would make the wave wait for it.
+  stage(bcur);
+  uint4 qr[PD + 1][4];
+  int32_t ir[PD + 1][KPL];
+#pragma unroll
+  for (int d = 0; d < PD; ++d) load(g0 + d < g1 ? g0 + d : g1 - 1, qr[d], ir[d]);
+  __syncthreads();
+  uint32_t *cw = cnt[wave];
+  auto compute = [&](int64_t gq, const uint4 (&qf)[4], const int32_t (&ix)[KPL]) {
+    const int64_t m = query_row(gq);
+    // idle waves (m >= M: past the batch's last row) compute row M - 1 and store nothing: the compute is not
+    // behind a branch, where the compiler would wait for every prefetched load at the join
+    {
+      const int64_t qm = bcur * M + (m < M ? m : M - 1);
+      // key counts of this query (the wave's own copy)
+      if (lane < KEYS) cw[lane] = 0u;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        if (lane + 64 * i < K && ix[i] >= 0 && ix[i] < N) atomicAdd(&cw[ix[i]], 1u);
+      uint4 c4[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) c4[t] = *reinterpret_cast<const uint4 *>(&cw[16 * t + 4 * g]);
+      // S^T = K Q^T: lane holds keys 16t + 4g + r of head l16
+      f32x4_t st[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        st[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          st[t] = mfma16(*reinterpret_cast<const uint4 *>(kvs + qk0[j] + 16 * t * UPR * 8), qf[j], st[t]);
+      }
+      // softmax over the counted keys and the sink
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint32_t cv[4] = {c4[t].x, c4[t].y, c4[t].z, c4[t].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (cv[r] != 0u) mx = fmaxf(mx, st[t][r] * scale_log2);
+      }
+      mx = fmaxf(rows_max(mx), skl);
+      float p[NT][4], psum = 0.f;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const uint32_t cv[4] = {c4[t].x, c4[t].y, c4[t].z, c4[t].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[t][r] = (cv[r] != 0u && mx != -INFINITY)
+                        ? static_cast<float>(cv[r]) * fast_exp2(st[t][r] * scale_log2 - mx) : 0.f;
+          psum += p[t][r];
+        }
+      }
+      const float den = rows_sum(psum) + (mx == -INFINITY ? 0.f : fast_exp2(skl - mx));
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      // O^T = V^T P^T: P^T is the B operand in the key order of the gather kernel's PV (keys 4g + r, 16 + 4g + r
+      // of each 32-key chunk), V^T its V fragments as the A operand
+      f32x4_t ot[CT];
+#pragma unroll
+      for (int cc = 0; cc < CT; ++cc) ot[cc] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 pb = make_uint4(pack_bf16x2(p[2 * c][0], p[2 * c][1]), pack_bf16x2(p[2 * c][2], p[2 * c][3]),
+                                    pack_bf16x2(p[2 * c + 1][0], p[2 * c + 1][1]),
+                                    pack_bf16x2(p[2 * c + 1][2], p[2 * c + 1][3]));
+        const uint16_t *kc = kvs + c * 32 * UPR * 8;
+#pragma unroll
+        for (int cc = 0; cc < CT; ++cc) {
+          const uint2 b0 = lds_read_tr16(kc + pv0[cc]);
+          const uint2 b1 = lds_read_tr16(kc + pv0[cc] + 16 * UPR * 8);
+          ot[cc] = mfma16(make_uint4(b0.x, b0.y, b1.x, b1.y), pb, ot[cc]);
+        }
+      }
+      // lane: O[head l16][16cc + 4g .. + 3]
+      uint16_t *orow = out + (qm * H + head) * D + 4 * g;
+      if (m < M) {  // uniform per wave
+#pragma unroll
+        for (int cc = 0; cc < CT; ++cc)
+          *reinterpret_cast<uint2 *>(orow + 16 * cc) = make_uint2(pack_bf16x2(ot[cc][0] * inv, ot[cc][1] * inv),
+                                                                pack_bf16x2(ot[cc][2] * inv, ot[cc][3] * inv));
+      }
+    }
+  };
+  for (int64_t gb = g0; gb < g1; gb += PD + 1) {
+#pragma unroll
+    for (int sl = 0; sl <= PD; ++sl) {
+      const int64_t gq = gb + sl;
+      if (gq >= g1) break;  // uniform per workgroup
+      load(gq + PD < g1 ? gq + PD : g1 - 1, qr[(sl + PD) % (PD + 1)], ir[(sl + PD) % (PD + 1)]);
+      compute(gq, qr[sl], ir[sl]);
+    }
+  }
+}
+
+inline bool use_dense(int64_t Dqk, int64_t Dv, int64_t H, int64_t N, int64_t K, const void *out) {
+  static_assert(kDenseMaxK == 256, "the launcher instantiates 1 and 4 indices per lane");
+  return Dqk == 128 && Dv == 128 && N <= kDenseMaxN && K <= kDenseMaxK && (H == 16 || H == 32 || H == 64) &&
+         aligned(out, 8);
+}
+
+int launch_sa_dense(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
+                    int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, hipStream_t stream) {
+  const int gw = static_cast<int>(H / 16);  // waves per query: 1, 2 or 4
+  const int64_t qpi = 4 / gw;
+  const int64_t gpb = ceil_div(M, qpi);     // query groups per batch
+  int dev = 0, cus = 0;
+  KS_CHECK_HIP(hipGetDevice(&dev));
+  KS_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const float sl2 = scale * kLog2e;
+  const int h32 = static_cast<int>(H), n32 = static_cast<int>(N), k32 = static_cast<int>(K);
+  // about as many workgroups as fit at once (the kernel's occupancy), each over a contiguous range of one batch's
+  // query groups: rpb ranges of `per` groups per batch
+  auto run = [&](auto kern) -> int {
+    int per_cu = 0;
+    KS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0));
+    const int64_t target = static_cast<int64_t>(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+    const int64_t want_rpb = ceil_div(target, B) < gpb ? ceil_div(target, B) : gpb;
+    const int64_t per = ceil_div(gpb, want_rpb);
+    const int64_t rpb = ceil_div(gpb, per);
+    const int64_t wgs = B * rpb;
+    KS_CHECK_ARG(wgs < (int64_t(1) << 31), "sparse attention (dense): %lld workgroups", (long long)wgs);
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(wgs)), dim3(256), 0, stream, q, kv, sink, idx, out, M, h32,
+                       n32, k32, gw, gpb, per, rpb, sl2);
+    KS_CHECK_LAUNCH("sparse_attn_dense_kernel");
+    return KS_OK;
+  };
+  constexpr int PD = kDensePrefetch;
+  if (N <= 32 && K <= 64) return run(sparse_attn_dense_kernel<1, 1, PD>);
+  if (N <= 32) return run(sparse_attn_dense_kernel<1, 4, PD>);
+  if (K <= 64) return run(sparse_attn_dense_kernel<2, 1, PD>);
+  return run(sparse_attn_dense_kernel<2, 4, PD>);
+}
+
 template <int DQK, int DV>
 int launch_sa(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
               int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
@@ -1241,6 +1450,7 @@ extern "C" int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float
                "ks_sparse_attn: workspace of %zu bytes required, %zu given", need, workspace_bytes);
   KS_CHECK_ARG(need == 0 || ks::aligned(workspace, 16), "ks_sparse_attn: workspace must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (ks::use_dense(Dqk, Dv, H, N, K, out)) return ks::launch_sa_dense(q, kv, sink, idx, out, B, M, H, N, K, scale, st);
   if (d128) return ks::launch_sa<128, 128>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
   if (ks::use_mla(Dqk, Dv, H, K)) return ks::launch_mla(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
   return ks::launch_sa<576, 512>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);

@@ -88,6 +88,30 @@ def test_sparse_attn_split_counts(device, K):
     np.testing.assert_allclose(got, want, **TOL)
 
 
+# Small kv sets (N <= 64, Dqk = Dv = 128, H in {16, 32, 64}, K <= 256) take the dense count-mask kernel: duplicates
+# count with multiplicity, indices < 0 or >= N count nowhere, an all-invalid row gives 0.  Every (N, K) tier and head
+# count; M not a multiple of the queries a workgroup step covers (idle waves at each batch's end); batch boundaries
+# inside a workgroup's range (restaging the kv rows); a single key; K above N (many duplicates).
+@pytest.mark.parametrize("H,B,M,N,K", [(64, 2, 5, 32, 16), (16, 3, 7, 20, 40), (32, 2, 9, 64, 256), (16, 2, 3, 1, 1),
+                                       (64, 3, 33, 48, 100), (32, 4, 130, 32, 64), (16, 1, 4097, 17, 65),
+                                       (64, 8, 301, 32, 16)])
+def test_sparse_attn_dense_small_kv(device, H, B, M, N, K):
+    g = torch.Generator().manual_seed(H * 31 + N * 7 + K)
+    q = torch.randn(B, M, H, 128, generator=g).bfloat16()
+    kv = torch.randn(B, N, 128, generator=g).bfloat16()
+    idx = torch.randint(-2, N + 2, (B, M, K), generator=g, dtype=torch.int32)  # invalid: < 0 and >= N
+    idx[0, 0] = -1  # an all-invalid row -> output 0
+    if M > 1:
+        idx[0, 1, : (K + 1) // 2] = 0  # duplicates count with multiplicity
+    sink = torch.randn(H, generator=g)
+    got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), 128 ** -0.5, 128,
+               f"dense H={H} B={B} M={M} N={N} K={K}")
+    ok = (idx >= 0) & (idx < N)
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), torch.where(ok, idx, -1).numpy(), 128 ** -0.5, 128)
+    np.testing.assert_allclose(got, want, **TOL)
+    assert np.all(got[0, 0] == 0)
+
+
 def test_sparse_attn_errors(device):
     q = torch.zeros(1, 1, 16, 64, dtype=torch.bfloat16, device=device)
     kv = torch.zeros(1, 8, 64, dtype=torch.bfloat16, device=device)

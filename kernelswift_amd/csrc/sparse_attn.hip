@@ -1200,13 +1200,16 @@ int launch_mla(const uint16_t *q, const uint16_t *kv, const float *sink, const i
 // only says how often each key counts.  Per query and wave (16 heads): the key counts (LDS atomics over the index
 // list: invalid indices count nowhere, duplicates with multiplicity), S^T = K Q^T for all keys, the softmax over
 // the counted keys with the sink, p = count * exp2(s - m), and O^T = V^T P^T, whose output layout gives each lane
-// four consecutive columns of one head (8-byte stores).  Workgroups are persistent over contiguous ranges of
-// query groups (a group never straddles two batches), and each wave loads the next query's q rows and indices
-// before computing the current one.  This replaces the gather kernel where each query's work is one short chunk
-// and the launch is bound by q and output traffic.
+// four consecutive columns of one head, staged through LDS into contiguous 16-byte stores.  Each workgroup covers
+// a contiguous range of one batch's query groups (so its staged kv never changes), and each wave loads the next
+// query's q rows and indices before computing the current one.  This replaces the gather kernel where each
+// query's work is one short chunk and the launch is bound by q and output traffic.
 constexpr int kDenseMaxN = 64;
 constexpr int kDenseMaxK = 256;
-constexpr int kDensePrefetch = 2;  // queries in flight per wave beyond the one computed (1 and 3 measured the same)
+constexpr int kDenseOutRow = 136;  // bf16 elements per staged output row (128 + 8 of padding)
+// queries in flight per wave beyond the one computed: 1 keeps the kernel at 124 VGPRs, four waves per SIMD
+// (139.8 us at the drop-in shape; 2 and 3 prefetched: 141.3 and 144.5 us at three waves per SIMD)
+constexpr int kDensePrefetch = 1;
 
 template <int NC, int KPL, int PD>  // 32-key chunks: N <= 32 NC; indices per lane: K <= 64 KPL; queries prefetched
 __global__ __launch_bounds__(256) void sparse_attn_dense_kernel(
@@ -1218,6 +1221,7 @@ __global__ __launch_bounds__(256) void sparse_attn_dense_kernel(
   constexpr int KEYS = 32 * NC;
   __shared__ __attribute__((aligned(16))) uint16_t kvs[KEYS * D];
   __shared__ __attribute__((aligned(16))) uint32_t cnt[4][KEYS];
+  __shared__ __attribute__((aligned(16))) uint16_t ost[4][16 * kDenseOutRow];  // each wave's output rows
   const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qpi = 4 / GW;                          // queries per group
@@ -1343,13 +1347,22 @@ __global__ __launch_bounds__(256) void sparse_attn_dense_kernel(
           ot[cc] = mfma16(make_uint4(b0.x, b0.y, b1.x, b1.y), pb, ot[cc]);
         }
       }
-      // lane: O[head l16][16cc + 4g .. + 3]
-      uint16_t *orow = out + (qm * H + head) * D + 4 * g;
-      if (m < M) {  // uniform per wave
+      // lane: O[head l16][16cc + 4g .. + 3].  The wave's 16 output rows (4 KiB, contiguous in out) go through LDS
+      // (rows padded to 272 bytes: no bank conflicts) and leave as 1 KiB runs of 16-byte stores; storing the lanes'
+      // 8-byte pieces directly writes 32 bytes into each of 16 rows per instruction, 23% slower at the drop-in shape.
+      // Unconditional: an idle wave computes row M - 1 with the same head block as the wave that owns that row, so
+      // it writes the same bytes to the same place (a store behind a branch would make the compiler's wait for the
+      // next prefetched rows also wait for these stores to complete).
+      uint16_t *ob = ost[wave];
 #pragma unroll
-        for (int cc = 0; cc < CT; ++cc)
-          *reinterpret_cast<uint2 *>(orow + 16 * cc) = make_uint2(pack_bf16x2(ot[cc][0] * inv, ot[cc][1] * inv),
-                                                                pack_bf16x2(ot[cc][2] * inv, ot[cc][3] * inv));
+      for (int cc = 0; cc < CT; ++cc)
+        *reinterpret_cast<uint2 *>(ob + l16 * kDenseOutRow + 16 * cc + 4 * g) =
+            make_uint2(pack_bf16x2(ot[cc][0] * inv, ot[cc][1] * inv), pack_bf16x2(ot[cc][2] * inv, ot[cc][3] * inv));
+      uint4 *odst = reinterpret_cast<uint4 *>(out + (qm * H + 16 * (wave % GW)) * D);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = lane + 64 * i;  // 16-byte chunk c of the wave's 4 KiB: row c / 16, chunk c % 16
+        odst[c] = *reinterpret_cast<const uint4 *>(ob + (c >> 4) * kDenseOutRow + 8 * (c & 15));
       }
     }
   };
@@ -1367,7 +1380,7 @@ __global__ __launch_bounds__(256) void sparse_attn_dense_kernel(
 inline bool use_dense(int64_t Dqk, int64_t Dv, int64_t H, int64_t N, int64_t K, const void *out) {
   static_assert(kDenseMaxK == 256, "the launcher instantiates 1 and 4 indices per lane");
   return Dqk == 128 && Dv == 128 && N <= kDenseMaxN && K <= kDenseMaxK && (H == 16 || H == 32 || H == 64) &&
-         aligned(out, 8);
+         aligned(out, 16);
 }
 
 int launch_sa_dense(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,

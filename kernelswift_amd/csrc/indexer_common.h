@@ -45,6 +45,21 @@ __device__ __forceinline__ float dot_halfwidth(float qn, float knm, float bound_
   return p < 0x1p126f ? bound_c * 0x1p-23f * p + 0x1p-144f : __builtin_inff();
 }
 
+// Per-dot form of the same bound, for kernels that also run the MFMA on |q| and |k| (bf16 magnitudes, exact
+// products): the derivation above bounds the error by bound_c * 2^-23 * sum_k (|q_k| + 2^-126)(|k_k| + 2^-126)
+// before Cauchy-Schwarz, so
+//   half-width = dot_halfwidth_scale(bound_c) * S + dot_halfwidth_add(qn, knm, bound_c),
+// S the MFMA sum of |q_k| |k_k|.  S itself is a sum of nonnegative products in the same accumulation, whose loss
+// (the same step model) is below (8 + n + n 2^-7) 2^-24 of the exact sum over n <= 16 steps, < 2^-19: the exact
+// sum is below S (1 + 2^-18).  The padding terms add 2^-126 (||q||_1 + ||k||_1) + D 2^-252 <= 2^-122
+// (||q|| + ||k||) + 2^-245 for D <= 128 (||x||_1 <= sqrt(D) ||x||), covered by the additive part with the
+// norms' upper bounds.  The same overflow guard as dot_halfwidth: +inf where the norm product could overflow.
+__device__ __forceinline__ float dot_halfwidth_scale(float bound_c) { return bound_c * 0x1.00004p-23f; }
+__device__ __forceinline__ float dot_halfwidth_add(float qn, float knm, float bound_c) {
+  const float p = (qn + 0x1p-122f) * (knm + 0x1p-122f);
+  return p < 0x1p126f ? bound_c * 0x1p-145f * (qn + knm + 0x1p-120f) + 0x1p-143f : __builtin_inff();
+}
+
 // Canonical RoPE of one 16-byte chunk (4 consecutive pairs (2j, 2j+1)) with (cos, sin) pairs cs[0..3]:
 // y0 = fl(x0*c) - fl(x1*s), y1 = fl(x0*s) + fl(x1*c), then RNE to bf16 (the library is built with
 // -ffp-contract=off, so the products round separately, exactly like the CPU oracle).

@@ -306,6 +306,10 @@ indexer_scores_kernel(
   static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
   static_assert(BOUND || !COUNT, "counts of lower ends need the bounds");
   static_assert(!F8 || BOUND, "FP8 keys are read by the bound-emitting variant");
+  // per-dot interval half-widths (bound_c 2^-23 sum |q_k||k_k|, the magnitudes' sum on the MFMA) instead of the
+  // per-head bound_c 2^-23 ||q_h|| max ||k||: about half as wide on typical rows, so about half the near ties and
+  // their exact recomputation, for one more MFMA per 16-key tile.  Built where the registers allow it (16 heads).
+  constexpr bool PDD = !BOUND && HT == 1;
   // F8: k points at e4m3 codes (KD bytes per row) with row scales ksc
   const uint8_t *__restrict__ k8 = reinterpret_cast<const uint8_t *>(k);
   __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD, COUNT>, ScoresLds<KD, HT>> L;
@@ -406,6 +410,9 @@ indexer_scores_kernel(
 #pragma unroll
     for (int m = 0; m < HT; ++m)
       qa[m][kk] = *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g);
+  auto abs8 = [](uint4 v) {  // |x| of 8 packed bf16
+    return make_uint4(v.x & 0x7FFF7FFFu, v.y & 0x7FFF7FFFu, v.z & 0x7FFF7FFFu, v.w & 0x7FFF7FFFu);
+  };
   // max key norm over this workgroup's range (the error bound uses it for every key)
   L.knorm[kt] = kin ? kn_v : 0.f;
   L.kspan[kt] = kin ? ks_v : 0;
@@ -416,8 +423,9 @@ indexer_scores_kernel(
   for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
   L.qspan[wave][hl] = qs_v;
   L.qnorm[wave][hl] = qn_v;
-  // per-head data formed once per head (lane h), not by each of the 16 lanes that use it
-  L.dl[wave][hl] = dot_halfwidth(qn_v, knm, bound_c);
+  // per-head data formed once per head (lane h), not by each of the 16 lanes that use it.  PDD (the exact kernel
+  // at 16 heads): per-dot half-widths from the MFMA sum of the magnitudes, dl then holds their additive part
+  L.dl[wave][hl] = PDD ? dot_halfwidth_add(qn_v, knm, bound_c) : dot_halfwidth(qn_v, knm, bound_c);
   if constexpr (BOUND) L.wup[wave][hl] = bf16_abs_round_up(w_v);
   L.w[wave][hl] = w_v;
   // the workgroup's whole key block into LDS (zero rows past T)
@@ -526,15 +534,26 @@ indexer_scores_kernel(
   const int64_t lim_rel = limit - kb0;
   const int nlive = lim_rel <= 0 ? 0 : (lim_rel >= 16 * ntiles ? ntiles : static_cast<int>((lim_rel + 15) / 16));
 
-  auto tile_mfma = [&](int t, f32x4_t(&acc)[HT]) {
+  // PDD: accs holds the MFMA sums of |q_k||k_k|, from |q| fragments formed once (qab) and |k| per tile
+  uint4 qab[HT][KD / 32];
+#pragma unroll
+  for (int m = 0; m < HT; ++m)
+#pragma unroll
+    for (int kk = 0; kk < KD / 32; ++kk) qab[m][kk] = PDD ? abs8(qa[m][kk]) : make_uint4(0, 0, 0, 0);
+  auto tile_mfma = [&](int t, f32x4_t(&acc)[HT], f32x4_t(&accs)[HT]) {
     const int key_l = 16 * t + l16;
 #pragma unroll
-    for (int m = 0; m < HT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < HT; ++m) acc[m] = accs[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KD / 32; ++kk) {
       const uint4 bv = L.k[key_l * kC + ((4 * kk + g) ^ (key_l & (kC - 1)))];
 #pragma unroll
       for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv, acc[m]);
+      if constexpr (PDD) {
+        const uint4 ba = abs8(bv);
+#pragma unroll
+        for (int m = 0; m < HT; ++m) accs[m] = mfma16(qab[m][kk], ba, accs[m]);
+      }
     }
   };
   // the same in two halves (BOUND, from -delta): the B fragments of a tile are read one tile ahead of its MFMAs
@@ -555,7 +574,9 @@ indexer_scores_kernel(
   // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot; pl / ph keep the
   // interval ends for them.  FC (std::true_type / std::false_type) is the wave's `forced` flag as a constant in
   // the bound kernels, whose tile loop is compiled once per value, so that no branch splits the epilogue.
-  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], uint32_t(&pl)[2 * HT], uint32_t(&ph)[2 * HT]) {
+  const float dsc = dot_halfwidth_scale(bound_c);
+  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
+                           uint32_t(&ph)[2 * HT]) {
     const bool fcd = BOUND ? decltype(FC)::value : forced;
     const int key_l = 16 * t + l16;
     const int key = kb0 + key_l;
@@ -573,7 +594,8 @@ indexer_scores_kernel(
           pl[2 * m + rp] = cvt_relu_pk(A0, A1);
           ph[2 * m + rp] = cvt_relu_pk(__builtin_fmaf(-2.f, n0, A0), __builtin_fmaf(-2.f, n1, A1));
         } else {
-          const float d0 = dl[m][2 * rp], d1 = dl[m][2 * rp + 1];
+          const float d0 = PDD ? __builtin_fmaf(accs[m][2 * rp], dsc, dl[m][2 * rp]) : dl[m][2 * rp];
+          const float d1 = PDD ? __builtin_fmaf(accs[m][2 * rp + 1], dsc, dl[m][2 * rp + 1]) : dl[m][2 * rp + 1];
           pl[2 * m + rp] = cvt_relu_pk(A0 - d0, A1 - d1);
           ph[2 * m + rp] = cvt_relu_pk(A0 + d0, A1 + d1);
         }
@@ -663,11 +685,11 @@ indexer_scores_kernel(
         uint32_t pl[2 * HT], ph[2 * HT];
         tile_mfma_b(bb, nxt);
         tile_b(t + 2 < nlive ? t + 2 : last, ba);
-        (void)tile_epilogue(FC, t, acc, pl, ph);
+        (void)tile_epilogue(FC, t, acc, acc, pl, ph);
         if (t + 1 >= nlive) break;
         tile_mfma_b(ba, acc);
         tile_b(t + 3 < nlive ? t + 3 : last, bb);
-        (void)tile_epilogue(FC, t + 1, nxt, pl, ph);
+        (void)tile_epilogue(FC, t + 1, nxt, nxt, pl, ph);
       }
     };
     if (nlive > 0) {
@@ -677,14 +699,15 @@ indexer_scores_kernel(
         run(std::false_type{});
     }
   }
-  if (!BOUND && nlive > 0) tile_mfma(0, acc);
+  f32x4_t accs[HT], nxts[HT];
+  if (!BOUND && nlive > 0) tile_mfma(0, acc, accs);
   for (int t = 0; t <= (BOUND ? -1 : nlive); ++t) {
     const bool live_t = t < nlive;
     uint32_t pl[2 * HT], ph[2 * HT];
     uint32_t km = 0;
     if (live_t) {
-      if (t + 1 < nlive) tile_mfma(t + 1, nxt);
-      km = tile_epilogue(std::false_type{}, t, acc, pl, ph);
+      if (t + 1 < nlive) tile_mfma(t + 1, nxt, nxts);
+      km = tile_epilogue(std::false_type{}, t, acc, accs, pl, ph);
     }
     if constexpr (BOUND) km = 0u;  // the bound replaces the exact recomputation
     const int cnt = __builtin_popcount(km);
@@ -713,7 +736,10 @@ indexer_scores_kernel(
     }
     if (live_t) {
 #pragma unroll
-      for (int m = 0; m < HT; ++m) acc[m] = nxt[m];
+      for (int m = 0; m < HT; ++m) {
+        acc[m] = nxt[m];
+        if constexpr (PDD) accs[m] = nxts[m];
+      }
     }
   }
   // masked tiles (at or past the causal limit)

@@ -52,8 +52,8 @@ namespace {
 constexpr int kQW = 8;        // queries (= waves) per workgroup
 constexpr int kThreads = kQW * 64;
 constexpr int kKR = kScoreKeyBlock;  // keys per workgroup
-constexpr int kEntCap = 36;   // deferred key entries per wave (flushed before a tile would overflow them)
-static_assert(kEntCap >= 16, "one tile can defer 16 keys");
+constexpr int kEntCap = 32;   // deferred key entries per wave (flushed before another 16 could overflow them)
+static_assert(kEntCap >= 16, "16 listed keys are resolved at a time");
 static_assert(4 * kEntCap <= 255, "list entries hold the (entry, group) pair in 8 bits");
 constexpr int kDotCap = 256;  // near-tie dots listed at a time per wave
 
@@ -71,6 +71,8 @@ struct alignas(16) KeyEntry {
 template <int KD, int HT>
 struct ScoresLds {
   uint4 k[kKR * KD / 8];             // swizzled key block of this workgroup (KD / 8 16-byte chunks per key)
+  uint8_t klist[kQW][kKR];           // per wave: block rows of the keys holding a near-tie dot (a wave's tiles
+                                     // defer at most every key of the block)
   KeyEntry<HT> ent[kQW][kEntCap];
   uint32_t dots[kQW][kDotCap];       // near-tie dots: head << 24 | key row << 16 | pair << 4 | slot,
                                      // pair = 4 entry + group
@@ -290,10 +292,16 @@ struct ScoresLdsBound {
   uint16_t wup[kQW][64];  // |w| rounded up to bf16, for the bound MFMAs
 };
 
-// The non-counting bound kernel runs grids of several workgroups per CU: at most 168 VGPRs (three waves per SIMD)
-// let the next workgroup start as soon as one wave per SIMD of the current one has finished.
+// Waves per SIMD a kernel form is built for.  The non-counting bound kernel runs grids of several workgroups per
+// CU: at most 168 VGPRs (three waves per SIMD) let the next workgroup start as soon as one wave per SIMD of the
+// current one has finished.  The exact kernel at 16 heads of 64 dims (the drop-in shape: 4 dots per lane and tile,
+// a tile one chain of dependent steps) at 128 VGPRs and 72 KiB of LDS holds two workgroups per CU: four waves per
+// SIMD hide each other's tile latency, and one workgroup's prologue loads overlap the other's tiles.
+template <int HT, int KD, bool BOUND, bool COUNT>
+constexpr int score_waves() { return (BOUND && !COUNT) ? 3 : (!BOUND && HT == 1 && KD == 64) ? 4 : 1; }
+
 template <int HT, int KD, bool WBF, bool BOUND, bool COUNT = false, bool F8 = false>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu((BOUND && !COUNT) ? 3 : 1))) void
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(score_waves<HT, KD, BOUND, COUNT>()))) void
 indexer_scores_kernel(
     const uint16_t *__restrict__ q, const uint16_t *__restrict__ k, const void *__restrict__ w,
     const float *__restrict__ qn, const int32_t *__restrict__ qsp, const float *__restrict__ kn,
@@ -540,8 +548,8 @@ indexer_scores_kernel(
   for (int m = 0; m < HT; ++m)
 #pragma unroll
     for (int kk = 0; kk < KD / 32; ++kk) qab[m][kk] = PDD ? abs8(qa[m][kk]) : make_uint4(0, 0, 0, 0);
-  auto tile_mfma = [&](int t, f32x4_t(&acc)[HT], f32x4_t(&accs)[HT]) {
-    const int key_l = 16 * t + l16;
+  // the MFMAs of 16 keys, lane l16 holding block row key_l (a tile: 16 t + l16; or rows from the deferred list)
+  auto tile_mfma = [&](int key_l, f32x4_t(&acc)[HT], f32x4_t(&accs)[HT]) {
 #pragma unroll
     for (int m = 0; m < HT; ++m) acc[m] = accs[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -571,18 +579,11 @@ indexer_scores_kernel(
       for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv[kk], acc[m]);
   };
 
-  // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot; pl / ph keep the
-  // interval ends for them.  FC (std::true_type / std::false_type) is the wave's `forced` flag as a constant in
-  // the bound kernels, whose tile loop is compiled once per value, so that no branch splits the epilogue.
   const float dsc = dot_halfwidth_scale(bound_c);
-  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
+  // interval test: RNE(A - delta) == RNE(A + delta) (after ReLU) <=> the exact dot rounds to the same relu'd bf16
+  // value; pl holds that value for the head sum.  Returns the ballot of the lanes holding a near-tie dot.
+  auto interval_ends = [&](bool fcd, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
                            uint32_t(&ph)[2 * HT]) {
-    const bool fcd = BOUND ? decltype(FC)::value : forced;
-    const int key_l = 16 * t + l16;
-    const int key = kb0 + key_l;
-    const bool kvalid = key_l < nk;
-    // interval test: RNE(A - delta) == RNE(A + delta) (after ReLU) <=> the exact dot rounds to the same
-    // relu'd bf16 value; pl holds that value for the head sum
     uint64_t anyr = 0;
 #pragma unroll
     for (int m = 0; m < HT; ++m)
@@ -609,6 +610,21 @@ indexer_scores_kernel(
       }
       anyr = ~0ull;
     }
+    return anyr;
+  };
+  // the key mask (bit = key column) of a ballot over the four head-group rows
+  auto key_mask = [](uint64_t r) { return static_cast<uint32_t>((r | (r >> 16) | (r >> 32) | (r >> 48)) & 0xFFFFull); };
+  // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot and lie before the causal
+  // limit (a key past it keeps the -inf stored here); pl / ph keep the interval ends.  FC (std::true_type /
+  // std::false_type) is the wave's `forced` flag as a constant in the bound kernels, whose tile loop is compiled
+  // once per value, so that no branch splits the epilogue.
+  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
+                           uint32_t(&ph)[2 * HT]) {
+    const bool fcd = BOUND ? decltype(FC)::value : forced;
+    const int key_l = 16 * t + l16;
+    const int key = kb0 + key_l;
+    const bool kvalid = key_l < nk;
+    uint64_t anyr = interval_ends(fcd, acc, accs, pl, ph);
     // canonical head sum of this lane's group, then ((G0+G1)+(G2+G3)) across the rows
     float G = 0.f;
     if constexpr (WBF) {
@@ -637,8 +653,9 @@ indexer_scores_kernel(
     const float tot = combine_groups(G);
     const float outv = WBF ? round_bf16_f(tot) : tot;
     if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
-    anyr &= __builtin_amdgcn_ballot_w64(kvalid);  // keys past T are zero rows, never deferred
-    const uint32_t km = static_cast<uint32_t>((anyr | (anyr >> 16) | (anyr >> 32) | (anyr >> 48)) & 0xFFFFull);
+    // keys past T are zero rows and keys past the causal limit are -inf: neither is deferred
+    anyr &= __builtin_amdgcn_ballot_w64(kvalid && key < limit);
+    const uint32_t km = key_mask(anyr);
     if constexpr (BOUND) {
       // |exact score - tot| <= sum_h |w_h| (ph_h - pl_h) + (rounding of the canonical sum: 38 roundings of
       // at most 2^-24 of sum_h |w_h| ph_h, < 2^-18 of it) <= dph - dpl + 2^-16 (dph + dpl), dph / dpl the
@@ -667,9 +684,7 @@ indexer_scores_kernel(
     return km;
   };
 
-  // software pipeline: the MFMAs of the next tile are in flight during the current tile's epilogue.  The
-  // deferred keys are flushed at one place: before a tile's deferred keys would overflow the list, and in
-  // one extra round after the last tile.
+  // software pipeline: the MFMAs of the next tile are in flight during the current tile's epilogue.
   f32x4_t acc[HT], nxt[HT];
   if constexpr (BOUND) {
     // no deferred keys: two tiles per iteration, alternating the accumulator sets (no copy between them) and
@@ -699,46 +714,56 @@ indexer_scores_kernel(
         run(std::false_type{});
     }
   }
-  f32x4_t accs[HT], nxts[HT];
-  if (!BOUND && nlive > 0) tile_mfma(0, acc, accs);
-  for (int t = 0; t <= (BOUND ? -1 : nlive); ++t) {
-    const bool live_t = t < nlive;
-    uint32_t pl[2 * HT], ph[2 * HT];
-    uint32_t km = 0;
-    if (live_t) {
-      if (t + 1 < nlive) tile_mfma(t + 1, nxt, nxts);
-      km = tile_epilogue(std::false_type{}, t, acc, accs, pl, ph);
-    }
-    if constexpr (BOUND) km = 0u;  // the bound replaces the exact recomputation
-    const int cnt = __builtin_popcount(km);
-    if (!BOUND && (live_t ? (nent + cnt > kEntCap) : (nent > 0))) {  // never taken with BOUND
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if constexpr (!BOUND)
-        flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
-      nent = 0;
-    }
-    if constexpr (!BOUND) {
-      if (km != 0u) {
-        // defer the keys holding a near-tie dot: save all four groups' interval ends
-        if ((km >> l16) & 1u) {
-          const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
-          KeyEntry<HT> &en = L.ent[wave][e];
-#pragma unroll
-          for (int p = 0; p < 2 * HT; ++p) {
-            en.pl[g][p] = pl[p];
-            en.ph[g][p] = ph[p];
-          }
-          if (g == 0) en.key = kb0 + 16 * t + l16;
-        }
-        nent += cnt;
-      }
-    }
-    if (live_t) {
+  if constexpr (!BOUND) {
+    // the exact kernel: the tile loop only lists the keys holding a near-tie dot (their block rows, in LDS); the
+    // listed keys are resolved after it.  Nothing of the recomputation is live in the loop, so the loop keeps its
+    // pipeline in few registers.  The next tile's MFMAs past the last live tile repeat that tile (results unused).
+    f32x4_t accs[HT], nxts[HT];
+    uint8_t *klist = L.klist[wave];
+    int nlist = 0;
+    if (nlive > 0) tile_mfma(l16, acc, accs);
+    for (int t = 0; t < nlive; ++t) {
+      uint32_t pl[2 * HT], ph[2 * HT];
+      tile_mfma(16 * (t + 1 < nlive ? t + 1 : t) + l16, nxt, nxts);
+      const uint32_t km = tile_epilogue(std::false_type{}, t, acc, accs, pl, ph);
+      if (g == 0 && ((km >> l16) & 1u))
+        klist[nlist + __builtin_popcount(km & ((1u << l16) - 1u))] = static_cast<uint8_t>(16 * t + l16);
+      nlist += __builtin_popcount(km);
 #pragma unroll
       for (int m = 0; m < HT; ++m) {
         acc[m] = nxt[m];
         if constexpr (PDD) accs[m] = nxts[m];
+      }
+    }
+    // resolution, 16 listed keys at a time: the same MFMAs and interval test on their rows (the same operands, so
+    // the same interval ends), all four groups' ends of each key saved as a deferred entry, and the entries'
+    // near-tie dots computed exactly and their scores rewritten whenever another 16 could overflow the entries
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int base = 0; base < nlist; base += 16) {
+      const int key_l = klist[min(base + l16, nlist - 1)];
+      tile_mfma(key_l, acc, accs);
+      uint32_t pl[2 * HT], ph[2 * HT];
+      // every listed key is in range and before the causal limit; lanes past the list repeat its last key
+      const uint32_t km = key_mask(interval_ends(forced, acc, accs, pl, ph) &
+                                   __builtin_amdgcn_ballot_w64(base + l16 < nlist));
+      if ((km >> l16) & 1u) {
+        const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
+        KeyEntry<HT> &en = L.ent[wave][e];
+#pragma unroll
+        for (int p = 0; p < 2 * HT; ++p) {
+          en.pl[g][p] = pl[p];
+          en.ph[g][p] = ph[p];
+        }
+        if (g == 0) en.key = kb0 + key_l;
+      }
+      nent += __builtin_popcount(km);
+      if (nent + 16 > kEntCap || base + 16 >= nlist) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (nent > 0)
+          flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
+        nent = 0;
       }
     }
   }

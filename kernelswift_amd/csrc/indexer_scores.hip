@@ -108,16 +108,25 @@ __device__ __forceinline__ float group_sum(Word word, const float (&wv)[HT][4]) 
   return G;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-  const int lane = threadIdx.x & 63;
+// Exclusive prefix sum over the 64 lanes of a wave of values below 2^NB, and the wave's total: one ballot per bit
+// and the count of the lanes below (mbcnt), with no data moved between lanes.
+template <int NB>
+__device__ __forceinline__ uint32_t wave_excl_scan_bits(uint32_t v, uint32_t &total) {
+  uint32_t pre = 0, tot = 0;
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
+  for (int b = 0; b < NB; ++b) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64((v >> b) & 1u);
+    pre += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))
+           << b;
+    tot += static_cast<uint32_t>(__builtin_popcountll(m)) << b;
   }
-  return v;
+  total = tot;
+  return pre;
 }
+
+// A score's bf16 rounding (bf16 weights) with the hardware conversion: RNE, the same as the software rounding for
+// every non-NaN value.
+__device__ __forceinline__ float round_score_bf16(float x) { return unpack_lo(cvt_pk_bf16(x, x)); }
 
 // Near-tie slot bits (16 per head group) of an entry: positions where the two interval ends differ.
 template <int HT>
@@ -135,8 +144,8 @@ __device__ __forceinline__ uint32_t entry_mask(const KeyEntry<HT> &en, int gg) {
 // Exact recomputation of the deferred near-tie dots of one wave, then of the affected scores.
 template <int HT, int KD, bool WBF>
 __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
-                              int64_t qrow0, float *orow, int64_t limit, int T, int kb0, const float (&wv)[HT][4],
-                              uint32_t &n_exact, uint32_t &n_unres) {
+                              const uint4 (&qa)[HT][KD / 32], int64_t qrow0, float *orow, int64_t limit, int T, int kb0,
+                              const float (&wv)[HT][4], uint32_t &n_exact, uint32_t &n_unres) {
   KeyEntry<HT> *E = L.ent[wave];
   uint32_t *D = L.dots[wave];
   const int g = lane >> 4, l16 = lane & 15;
@@ -154,10 +163,10 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
     const int pair = 64 * i + lane;
     mset[i] = pair < npairs ? entry_mask<HT>(E[pair >> 2], pair & 3) : 0u;
     rset[i] = pair < npairs ? key_row(pair) : 0u;
-    cset[i] = __builtin_popcount(mset[i]);
-    const uint32_t incl = wave_incl_scan(cset[i]);
-    first[i] = ndots_u + incl - cset[i];  // list position of this pair's first dot
-    ndots_u += __shfl(incl, 63, 64);
+    cset[i] = __builtin_popcount(mset[i]);  // at most 4 HT near-tie slots per pair
+    uint32_t tot;
+    first[i] = ndots_u + wave_excl_scan_bits<HT == 1 ? 3 : HT == 2 ? 4 : 5>(cset[i], tot);  // list position of the
+    ndots_u += tot;                                                                       // pair's first dot
   }
   const int ndots = static_cast<int>(ndots_u);
   n_exact += ndots_u;
@@ -187,16 +196,28 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
     const int nd = min(kDotCap, ndots - base);
     const int dq = lane >> 2, sub = lane & 3;
     for (int b0 = 0; b0 < nd; b0 += 16) {
-      // list entry of this quad (idle quads repeat the last one; the result is identical), its q row
-      // quarter (global, L2-resident), its key row quarter (LDS) and the span sum that decides the path
+      // list entry of this quad (idle quads repeat the last one; the result is identical), its quarter of the q
+      // row and of the key row (LDS), and the span sum that decides the path.  16 heads: quarter `sub` takes the
+      // 16-byte chunks 4c + sub, which lane h + 16 sub holds as its A-fragment qa[0][c] (read with ds_bpermute);
+      // more heads: the chunks kLC sub + c, read from global memory (L2-resident).
       const uint32_t dcur = D[min(b0 + dq, nd - 1)];
       const int h = static_cast<int>(dcur >> 24), kl = static_cast<int>((dcur >> 16) & 255u);
       uint4 qcur[kLC], kcur[kLC];
-      const uint4 *qp = reinterpret_cast<const uint4 *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
+      if constexpr (HT == 1) {
+        const int src = 4 * (h + 16 * sub);
+        auto bp = [&](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(v))); };
 #pragma unroll
-      for (int c = 0; c < kLC; ++c) qcur[c] = qp[c];
+        for (int c = 0; c < kLC; ++c) {
+          qcur[c] = make_uint4(bp(qa[0][c].x), bp(qa[0][c].y), bp(qa[0][c].z), bp(qa[0][c].w));
+          kcur[c] = L.k[kl * kC + ((4 * c + sub) ^ (kl & (kC - 1)))];
+        }
+      } else {
+        const uint4 *qp = reinterpret_cast<const uint4 *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
 #pragma unroll
-      for (int c = 0; c < kLC; ++c) kcur[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
+        for (int c = 0; c < kLC; ++c) qcur[c] = qp[c];
+#pragma unroll
+        for (int c = 0; c < kLC; ++c) kcur[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
+      }
       const int scur = L.qspan[wave][h] + L.kspan[kl];
       const int pr = static_cast<int>((dcur >> 4) & 255u), slot = static_cast<int>(dcur & 15u);
       uint16_t r;
@@ -269,7 +290,7 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
     const float G = group_sum<HT, WBF>([&](int i) { return E[e].pl[g][i]; }, wv);
     const float tot = combine_groups(G);
     const int key = E[e].key;
-    if (g == 0 && eb + l16 < nent && key < T) orow[key] = (key < limit) ? (WBF ? round_bf16_f(tot) : tot) : -INFINITY;
+    if (g == 0 && eb + l16 < nent && key < T) orow[key] = (key < limit) ? (WBF ? round_score_bf16(tot) : tot) : -INFINITY;
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -651,7 +672,7 @@ indexer_scores_kernel(
       }
     }
     const float tot = combine_groups(G);
-    const float outv = WBF ? round_bf16_f(tot) : tot;
+    const float outv = WBF ? round_score_bf16(tot) : tot;
     if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
     // keys past T are zero rows and keys past the causal limit are -inf: neither is deferred
     anyr &= __builtin_amdgcn_ballot_w64(kvalid && key < limit);
@@ -762,7 +783,7 @@ indexer_scores_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (nent > 0)
-          flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
+          flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qa, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
         nent = 0;
       }
     }

@@ -122,7 +122,7 @@ def test_scores_small_bit_exact(device, H, w_bf16, D):
 
 
 @pytest.mark.parametrize("D", [128, 64])
-@pytest.mark.parametrize("H", [16, 64])
+@pytest.mark.parametrize("H", [16, 32, 64])
 @pytest.mark.parametrize("w_bf16", [False, True])
 def test_scores_every_dot_deferred(device, H, w_bf16, D):
     # a huge error-bound constant makes every positive dot a near-tie: every key of every tile is deferred,

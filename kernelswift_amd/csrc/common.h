@@ -101,23 +101,24 @@ __device__ __forceinline__ uint32_t lds_addr(T *p) {
 
 template <int S>
 __device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
+  // (every lane's DPP source lies in its row, so the moves need no initial value)
   if constexpr (S == 1) {
-    return __builtin_amdgcn_update_dpp(0u, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
   } else if constexpr (S == 2) {
-    return __builtin_amdgcn_update_dpp(0u, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
   } else if constexpr (S == 4) {  // i ^ 4 = (i ^ 7) ^ 3: half-row mirror, then quad_perm [3,2,1,0]
-    const uint32_t m = __builtin_amdgcn_update_dpp(0u, x, 0x141, 0xF, 0xF, false);
-    return __builtin_amdgcn_update_dpp(0u, m, 0x1B, 0xF, 0xF, false);
+    const uint32_t m = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(m, 0x1B, 0xF, 0xF, false);
   } else if constexpr (S == 8) {
-    return __builtin_amdgcn_update_dpp(0u, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+    return __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
   } else if constexpr (S == 16) {  // rows (0,1), (2,3) trade: even rows read the second result
     uint32_t a = x, b = x;
     permlane16_swap(a, b);
-    return ((__lane_id() >> 4) & 1) ? a : b;
+    return __builtin_amdgcn_inverse_ballot_w64(0xFFFF0000FFFF0000ull) ? a : b;
   } else {  // S == 32: rows (0,2), (1,3) trade
     uint32_t a = x, b = x;
     permlane32_swap(a, b);
-    return (__lane_id() >> 5) ? a : b;
+    return __builtin_amdgcn_inverse_ballot_w64(0xFFFFFFFF00000000ull) ? a : b;
   }
 }
 

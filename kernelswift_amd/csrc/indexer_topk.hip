@@ -153,29 +153,50 @@ __device__ __forceinline__ void merge_first(const uint64_t *x, int nx, const uin
   if (d0 < m) merge_path(x, nx, y, ny, d0, d0 + E < m ? d0 + E : m, emit);
 }
 
+// Lanes l of register r whose element r*64 + l keeps the larger value in the bitonic stage (SIZE, S): a
+// compile-time lane mask.
+template <int SIZE, int S, int R>
+constexpr uint64_t keep_max_lanes() {
+  uint64_t m = 0;
+  for (int l = 0; l < 64; ++l) {
+    const int e = R * 64 + l;
+    if (((e & SIZE) == 0) == ((e & S) == 0)) m |= uint64_t(1) << l;
+  }
+  return m;
+}
+
 // Bitonic sort (descending) of a wave's run of 128 composites, element r*64 + lane in v[r]: the exchange at
-// distance 64 stays in the lane, the others go through DPP / permlane.
-template <int SIZE, int S>
-__device__ __forceinline__ void run_stage(uint64_t (&v)[2], int lane) {
+// distance 64 stays in the lane, the others go through DPP / permlane.  V is uint64_t (key, ~column) or uint32_t
+// (a narrower composite of the same order: one lane exchange and one compare per element and stage).  The
+// direction of each exchange is a constant lane mask: the compare's lane mask is flipped by it with scalar
+// instructions and selects directly (one compare and one select per element and stage).
+template <int SIZE, int S, typename V>
+__device__ __forceinline__ void run_stage(V (&v)[2], int lane) {
   if constexpr (S == 64) {
-    const uint64_t a = v[0], c = v[1];  // SIZE == 128: one descending pair
+    const V a = v[0], c = v[1];  // SIZE == 128: one descending pair
     v[0] = a > c ? a : c;
     v[1] = a > c ? c : a;
   } else {
+    V pv[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int e = r * 64 + lane;
-      const uint32_t lo = lane_xor<S>(static_cast<uint32_t>(v[r]));
-      const uint32_t hi = lane_xor<S>(static_cast<uint32_t>(v[r] >> 32));
-      const uint64_t pv = (static_cast<uint64_t>(hi) << 32) | lo;
-      const bool keep_max = ((e & SIZE) == 0) == ((e & S) == 0);
-      v[r] = ((pv > v[r]) == keep_max) ? pv : v[r];
+      if constexpr (sizeof(V) == 8) {
+        const uint32_t lo = lane_xor<S>(static_cast<uint32_t>(v[r]));
+        const uint32_t hi = lane_xor<S>(static_cast<uint32_t>(v[r] >> 32));
+        pv[r] = (static_cast<uint64_t>(hi) << 32) | lo;
+      } else {
+        pv[r] = lane_xor<S>(v[r]);
+      }
     }
+    const uint64_t take0 = ~(__builtin_amdgcn_ballot_w64(pv[0] > v[0]) ^ keep_max_lanes<SIZE, S, 0>());
+    const uint64_t take1 = ~(__builtin_amdgcn_ballot_w64(pv[1] > v[1]) ^ keep_max_lanes<SIZE, S, 1>());
+    v[0] = __builtin_amdgcn_inverse_ballot_w64(take0) ? pv[0] : v[0];
+    v[1] = __builtin_amdgcn_inverse_ballot_w64(take1) ? pv[1] : v[1];
   }
   if constexpr (S > 1) run_stage<SIZE, S / 2>(v, lane);
 }
-template <int SIZE>
-__device__ __forceinline__ void run_sort(uint64_t (&v)[2], int lane) {
+template <int SIZE, typename V>
+__device__ __forceinline__ void run_sort(V (&v)[2], int lane) {
   run_stage<SIZE, SIZE / 2>(v, lane);
   if constexpr (SIZE < 128) run_sort<SIZE * 2>(v, lane);
 }
@@ -344,7 +365,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
 // above it are collected with ballots, keys equal to it in column order (j, then lane) up to the count
 // needed; the k winners are then sorted as composites (key, ~column) by the in-register bitonic network
 // of 128 (two per lane) and stored with the post-processing: the order of topk_rows_kernel.
-constexpr int kWaveRows = kTopkThreads / 64;  // rows per workgroup
+// The kernel is bound by its VALU work per row, so work that cannot change the result is skipped, by
+// wave-uniform branches: column groups j past the row's valid prefix (the causal limit leaves most rows far
+// fewer valid columns than T); the whole selection when every valid column is taken; and, when every key's low
+// 16 bits follow from its sign (bf16-valued scores, as with bf16 weights), so that a key is fixed by its top 16
+// bits, the last two radix passes and half of the sort's work (32-bit composites).
+// Rows (waves) per workgroup: small workgroups leave and are replaced independently, so that the waves of a CU are
+// spread over the load, selection and sort phases instead of moving through them together (16-row workgroups
+// kept every wave of a CU in the same phase: 35.5 -> 30.3 us at the drop-in shape; 2 or 1 rows time the same as 4).
+constexpr int kWaveRows = 4;
+constexpr int kWaveThreads = kWaveRows * 64;
 
 __device__ __forceinline__ void wave_lds_order() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -356,16 +386,19 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t b) {
 }
 
 template <int KPT>
-__global__ __launch_bounds__(kTopkThreads) void topk_wave_kernel(const float *__restrict__ scores, int64_t ld,
+__global__ __launch_bounds__(kWaveThreads) void topk_wave_kernel(const float *__restrict__ scores, int64_t ld,
                                                                 int64_t rows, int64_t S, int T, int k, int causal,
                                                                 int64_t start_pos, int ratio, int64_t offset,
                                                                 void *__restrict__ out, int out_i64) {
   __shared__ uint32_t hist[kWaveRows][256];
   __shared__ uint64_t cand[kWaveRows][128];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaveRows + wave;
+  // the row index in scalar registers (rows < 2^31, checked by the caller): its remainder by S is a 32-bit scalar
+  // division, not a 64-bit vector one
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t row32 = blockIdx.x * kWaveRows + static_cast<uint32_t>(wave);
+  const int64_t row = row32;
   if (row >= rows) return;  // uniform per wave; the kernel has no barrier
-  const int64_t s = row % S;
+  const int64_t s = row32 % static_cast<uint32_t>(S);
   int64_t limit = INT64_MAX;
   int n_valid = T;
   if (causal) {
@@ -373,6 +406,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_wave_kernel(const float *__
     n_valid = static_cast<int>(limit < 0 ? 0 : (limit < T ? limit : T));
   }
   const int k_sel = k < n_valid ? k : n_valid;
+  const int jn = (n_valid + 63) / 64;  // column groups holding a valid column (uniform)
   const float *src = scores + row * ld;
   float f[KPT];
 #pragma unroll
@@ -381,20 +415,31 @@ __global__ __launch_bounds__(kTopkThreads) void topk_wave_kernel(const float *__
     f[j] = src[col < n_valid ? col : 0];
   }
   uint32_t key[KPT];
+  bool odd_low = false;  // a valid key whose low 16 bits do not follow from its sign
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) key[j] = 64 * j + lane < n_valid ? score_key(f[j]) : 0u;
+  for (int j = 0; j < KPT; ++j) {
+    key[j] = 64 * j + lane < n_valid ? score_key(f[j]) : 0u;
+    const uint32_t low = key[j] & 0xFFFFu;
+    odd_low = odd_low || (key[j] != 0u && low != ((key[j] >> 31) ? 0u : 0xFFFFu));
+  }
+  // every key fixed by its top 16 bits (uniform)
+  const bool top16 = __builtin_amdgcn_ballot_w64(odd_low) == 0ull;
   if (k_sel > 0) {  // uniform
     uint32_t *h = hist[wave];
     uint32_t prefix = 0, mask = 0, k_rem = static_cast<uint32_t>(k_sel), eq_total = 0;
+    // every valid key taken: no selection (key 0 marks the columns past the prefix, which no key exceeds)
+    const bool take_all = k_sel == n_valid;
+    const int npass = take_all ? 0 : (top16 ? 2 : 4);
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
+      if (pass >= npass) break;
       const int shift = 24 - 8 * pass;
 #pragma unroll
       for (int i = 0; i < 4; ++i) h[64 * i + lane] = 0u;
       wave_lds_order();
 #pragma unroll
       for (int j = 0; j < KPT; ++j)
-        if (key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&h[(key[j] >> shift) & 255u], 1u);
+        if (j < jn && key[j] != 0u && (key[j] & mask) == prefix) atomicAdd(&h[(key[j] >> shift) & 255u], 1u);
       wave_lds_order();
       // lane l owns bins 255 - 4l .. 252 - 4l: a lane-order inclusive scan is a suffix sum from the top bin
       uint32_t c[4];
@@ -429,13 +474,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_wave_kernel(const float *__
       k_rem = rem;
       eq_total = cnt;
     }
-    const uint32_t kstar = prefix;  // >= 1: the k_sel-th of nonzero keys
-    const uint32_t take_eq = k_rem, n_gt = static_cast<uint32_t>(k_sel) - take_eq;
+    // the k_sel-th of the nonzero keys (>= 1); after two passes the low 16 bits follow from the sign bit.  With
+    // every key taken, kstar = 0 and take_eq = 0: every nonzero key is above it.
+    const uint32_t kstar = take_all ? 0u : (npass == 2 ? (prefix | ((prefix >> 31) ? 0u : 0xFFFFu)) : prefix);
+    const uint32_t take_eq = take_all ? 0u : k_rem, n_gt = static_cast<uint32_t>(k_sel) - take_eq;
     (void)eq_total;
     uint64_t *cw = cand[wave];
     uint32_t base_gt = 0, base_eq = 0;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
+      if (j >= jn) break;
       const bool gt = key[j] > kstar, eq = key[j] == kstar;
       const uint64_t bg = __builtin_amdgcn_ballot_w64(gt), be = __builtin_amdgcn_ballot_w64(eq);
       const uint32_t col = static_cast<uint32_t>(64 * j + lane);
@@ -446,19 +494,39 @@ __global__ __launch_bounds__(kTopkThreads) void topk_wave_kernel(const float *__
       base_eq += static_cast<uint32_t>(__builtin_popcountll(be));
     }
     wave_lds_order();
-    uint64_t v[2];
+    if (top16) {
+      // keys fixed by their top 16 bits, columns below 1024: the 32-bit composite (key bits 31-16,
+      // 0xFFFF - column) orders the winners as (key, ~column) does (absent = 0 still sorts last: a valid key's
+      // top 16 bits are nonzero)
+      uint32_t v[2];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int e = r * 64 + lane;
-      v[r] = e < k_sel ? cw[e] : 0ull;
-    }
-    run_sort<2>(v, lane);
+      for (int r = 0; r < 2; ++r) {
+        const int e = r * 64 + lane;
+        const uint64_t c = e < k_sel ? cw[e] : 0ull;
+        v[r] = (static_cast<uint32_t>(c >> 32) & 0xFFFF0000u) | (static_cast<uint32_t>(c) & 0xFFFFu);
+      }
+      run_sort<2>(v, lane);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int e = r * 64 + lane;
-      if (e < k_sel) {
-        const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[r] & 0xFFFFFFFFull));
-        store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+      for (int r = 0; r < 2; ++r) {
+        const int e = r * 64 + lane;
+        if (e < k_sel) store_index(out, out_i64, row * k + e, 0xFFFF - static_cast<int64_t>(v[r] & 0xFFFFu), causal,
+                                   limit, offset);
+      }
+    } else {
+      uint64_t v[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e = r * 64 + lane;
+        v[r] = e < k_sel ? cw[e] : 0ull;
+      }
+      run_sort<2>(v, lane);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e = r * 64 + lane;
+        if (e < k_sel) {
+          const int64_t col = static_cast<int64_t>(~static_cast<uint32_t>(v[r] & 0xFFFFFFFFull));
+          store_index(out, out_i64, row * k + e, col, causal, limit, offset);
+        }
       }
     }
   }
@@ -471,7 +539,7 @@ template <int KPT>
 int launch_topk_wave(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
                      int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream) {
   hipLaunchKernelGGL(topk_wave_kernel<KPT>, dim3(static_cast<unsigned>(ceil_div(rows, kWaveRows))),
-                     dim3(kTopkThreads), 0, stream, scores, ld, rows, S, T, k, causal, start_pos, ratio, offset, out,
+                     dim3(kWaveThreads), 0, stream, scores, ld, rows, S, T, k, causal, start_pos, ratio, offset, out,
                      out_i64);
   KS_CHECK_LAUNCH("topk_wave_kernel");
   return KS_OK;
@@ -1189,6 +1257,7 @@ extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64
     if (T <= 128) return ks::launch_topk_wave<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
     if (T <= 256) return ks::launch_topk_wave<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
     if (T <= 512) return ks::launch_topk_wave<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+    if (T <= 768) return ks::launch_topk_wave<12>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
     return ks::launch_topk_wave<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   }
   if (T <= 1024) return ks::launch_topk<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);

@@ -85,6 +85,19 @@ def test_topk_causal_limits_and_garbage_padding(device):
     _check(s, 600, causal=True, start_pos=600, ratio=1, offset=5, out_dtype=torch.int32)
 
 
+@pytest.mark.parametrize("start_pos", [0, 1500])
+def test_topk_wave_bf16_causal_prefixes(device, start_pos):
+    # the drop-in geometry (650 columns, ratio 4, k = 128) with bf16-valued scores: rows whose valid prefix is at
+    # most k (every valid column taken), prefixes ending inside a column group, and rows with exact ties at the
+    # threshold; then the same rows with one non-bf16 value per row, which needs all four radix passes
+    S, T = 700, 650
+    g = torch.Generator(device=device).manual_seed(start_pos + 11)
+    s = (torch.round(torch.randn(2, S, T, device=device, generator=g) * 8) / 8).bfloat16().float()
+    _check(s.contiguous(), 128, causal=True, start_pos=start_pos, ratio=4, offset=3)
+    s[:, :, 0] += 1.0 / 3.0  # not a bf16 value for any multiple of 1/8
+    _check(s.contiguous(), 128, causal=True, start_pos=start_pos, ratio=4, offset=3)
+
+
 def test_topk_leading_dimension_and_odd_rows(device):
     g = torch.Generator(device=device).manual_seed(4)
     base = torch.randn(3, 37, 1000, device=device, generator=g)

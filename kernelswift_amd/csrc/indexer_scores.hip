@@ -601,10 +601,45 @@ indexer_scores_kernel(
   };
 
   const float dsc = dot_halfwidth_scale(bound_c);
-  // interval test: RNE(A - delta) == RNE(A + delta) (after ReLU) <=> the exact dot rounds to the same relu'd bf16
-  // value; pl holds that value for the head sum.  Returns the ballot of the lanes holding a near-tie dot.
-  auto interval_ends = [&](bool fcd, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
+  // the exact kernel's interval test (the tile epilogue's, below) on the 16 keys of a resolution round: pl, ph and the
+  // ballot of the lanes holding a near-tie dot.  (The tile epilogue keeps its own copy: sharing this lambda with
+  // the bound kernels' epilogue made the compiler spill registers in their tile loop.)
+  auto interval_ends = [&](const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
                            uint32_t(&ph)[2 * HT]) {
+    uint64_t anyr = 0;
+#pragma unroll
+    for (int m = 0; m < HT; ++m)
+#pragma unroll
+      for (int rp = 0; rp < 2; ++rp) {
+        const float A0 = acc[m][2 * rp], A1 = acc[m][2 * rp + 1];
+        const float d0 = PDD ? __builtin_fmaf(accs[m][2 * rp], dsc, dl[m][2 * rp]) : dl[m][2 * rp];
+        const float d1 = PDD ? __builtin_fmaf(accs[m][2 * rp + 1], dsc, dl[m][2 * rp + 1]) : dl[m][2 * rp + 1];
+        pl[2 * m + rp] = cvt_relu_pk(A0 - d0, A1 - d1);
+        ph[2 * m + rp] = cvt_relu_pk(A0 + d0, A1 + d1);
+        anyr |= __builtin_amdgcn_ballot_w64(pl[2 * m + rp] != ph[2 * m + rp]);
+      }
+    if (forced) {
+#pragma unroll
+      for (int p = 0; p < 2 * HT; ++p) {
+        pl[p] = 0u;
+        ph[p] = 0x7F807F80u;
+      }
+      anyr = ~0ull;
+    }
+    return anyr;
+  };
+  // the key mask (bit = key column) of a ballot over the four head-group rows
+  auto key_mask = [](uint64_t r) { return static_cast<uint32_t>((r | (r >> 16) | (r >> 32) | (r >> 48)) & 0xFFFFull); };
+  // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot (in the exact kernel, before
+  // the causal limit: a key past it keeps the -inf stored here); pl / ph keep the interval ends.
+  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
+                           uint32_t(&ph)[2 * HT]) {
+    const bool fcd = BOUND ? decltype(FC)::value : forced;
+    const int key_l = 16 * t + l16;
+    const int key = kb0 + key_l;
+    const bool kvalid = key_l < nk;
+    // interval test: RNE(A - delta) == RNE(A + delta) (after ReLU) <=> the exact dot rounds to the same
+    // relu'd bf16 value; pl holds that value for the head sum
     uint64_t anyr = 0;
 #pragma unroll
     for (int m = 0; m < HT; ++m)
@@ -631,21 +666,6 @@ indexer_scores_kernel(
       }
       anyr = ~0ull;
     }
-    return anyr;
-  };
-  // the key mask (bit = key column) of a ballot over the four head-group rows
-  auto key_mask = [](uint64_t r) { return static_cast<uint32_t>((r | (r >> 16) | (r >> 32) | (r >> 48)) & 0xFFFFull); };
-  // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot and lie before the causal
-  // limit (a key past it keeps the -inf stored here); pl / ph keep the interval ends.  FC (std::true_type /
-  // std::false_type) is the wave's `forced` flag as a constant in the bound kernels, whose tile loop is compiled
-  // once per value, so that no branch splits the epilogue.
-  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
-                           uint32_t(&ph)[2 * HT]) {
-    const bool fcd = BOUND ? decltype(FC)::value : forced;
-    const int key_l = 16 * t + l16;
-    const int key = kb0 + key_l;
-    const bool kvalid = key_l < nk;
-    uint64_t anyr = interval_ends(fcd, acc, accs, pl, ph);
     // canonical head sum of this lane's group, then ((G0+G1)+(G2+G3)) across the rows
     float G = 0.f;
     if constexpr (WBF) {
@@ -674,8 +694,9 @@ indexer_scores_kernel(
     const float tot = combine_groups(G);
     const float outv = WBF ? round_score_bf16(tot) : tot;
     if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
-    // keys past T are zero rows and keys past the causal limit are -inf: neither is deferred
-    anyr &= __builtin_amdgcn_ballot_w64(kvalid && key < limit);
+    // keys past T are zero rows and, in the exact kernel, keys past the causal limit are -inf: neither is deferred
+    // (the bound kernel stores bound 0 past the limit, below)
+    anyr &= __builtin_amdgcn_ballot_w64(BOUND ? kvalid : (kvalid && key < limit));
     const uint32_t km = key_mask(anyr);
     if constexpr (BOUND) {
       // |exact score - tot| <= sum_h |w_h| (ph_h - pl_h) + (rounding of the canonical sum: 38 roundings of
@@ -766,7 +787,7 @@ indexer_scores_kernel(
       tile_mfma(key_l, acc, accs);
       uint32_t pl[2 * HT], ph[2 * HT];
       // every listed key is in range and before the causal limit; lanes past the list repeat its last key
-      const uint32_t km = key_mask(interval_ends(forced, acc, accs, pl, ph) &
+      const uint32_t km = key_mask(interval_ends(acc, accs, pl, ph) &
                                    __builtin_amdgcn_ballot_w64(base + l16 < nlist));
       if ((km >> l16) & 1u) {
         const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));

@@ -11,7 +11,11 @@ no kernel sets it.
 Flat loads and stores count in lgkmcnt as well as vmcnt, so every wait for an LDS read (lgkmcnt(0) before an
 LDS-fed MFMA) also waits for them: one pointer rebuilt from an integer, which the compiler treats as generic,
 turned a sparse-attention kernel's index prefetch into flat loads that stalled each chunk's LDS reads.  The
-same compile checks that no kernel contains a flat memory instruction."""
+same compile checks that no kernel contains a flat memory instruction.
+
+Some kernels' speed rests on their register, scratch and LDS budgets, which a small source change can break
+silently (a lambda shared between two epilogues made the bound score kernel's tile loop reload spilled registers
+every iteration: config 4's score kernel went from 61 to 76 us).  The same compile checks those budgets."""
 import concurrent.futures
 import glob
 import os
@@ -61,24 +65,76 @@ def test_checker_pins():
     assert flat_memory_kernels(code) == ["_Zb", "_Zc"]
 
 
-@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
-                    reason="hipcc is not installed")
-def test_no_dispatch_packet_reads_or_flat_memory(tmp_path):
+def kernel_resources(asm: str):
+    """{kernel name: (VGPRs, scratch bytes per lane, LDS bytes)} from the kernel descriptors."""
+    out = {}
+    for m in re.finditer(r"\.amdhsa_kernel (\S+)(.*?)\.end_amdhsa_kernel", asm, re.S):
+        field = lambda f: int(re.search(r"\.amdhsa_" + f + r"\s+(\d+)", m.group(2)).group(1))
+        out[m.group(1)] = (field("next_free_vgpr"), field("private_segment_fixed_size"),
+                           field("group_segment_fixed_size"))
+    return out
+
+
+# (mangled-name fragment, what the budget buys, max VGPRs, max scratch bytes, max LDS bytes)
+BUDGETS = [
+    # bound score kernel, non-counting (config 4): three waves per SIMD; 8 bytes of scratch outside the tile loop
+    ("indexer_scores_kernelILi4ELi128ELb0ELb1ELb0ELb0E", "3 waves/SIMD, no spill in the tile loop", 168, 8, 80 * 1024),
+    # bound score kernel, counting (config 2): one workgroup per CU, no scratch
+    ("indexer_scores_kernelILi4ELi128ELb0ELb1ELb1ELb0E", "no spill", 256, 0, 160 * 1024),
+    # exact score kernel at the drop-in shape: four waves per SIMD, two workgroups per CU (scratch only on the
+    # flush's rare wide-range paths)
+    ("indexer_scores_kernelILi1ELi64ELb1ELb0ELb0ELb0E", "2 workgroups/CU at 4 waves/SIMD", 128, 32, 80 * 1024),
+    # wave top-k: no scratch
+    ("topk_wave_kernelILi12E", "no spill", 64, 0, 64 * 1024),
+]
+
+
+def test_checker_pins_resources():
+    desc = ("\t.amdhsa_kernel _Za\n\t\t.amdhsa_group_segment_fixed_size 4096\n"
+            "\t\t.amdhsa_private_segment_fixed_size 8\n\t\t.amdhsa_next_free_vgpr 97\n\t.end_amdhsa_kernel\n")
+    assert kernel_resources(desc) == {"_Za": (97, 8, 4096)}
+
+
+@pytest.fixture(scope="module")
+def compiled(tmp_path_factory):
+    """Every library source compiled for gfx950 with the library's flags: {source: assembly}."""
+    if shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"):
+        pytest.skip("hipcc is not installed")
     sys.path.insert(0, REPO)
     from kernelswift_amd import build as ksbuild
     srcs = sorted(glob.glob(os.path.join(REPO, "kernelswift_amd", "csrc", "*.hip")))
     assert srcs
+    tmp = tmp_path_factory.mktemp("asm")
 
     def compile_one(src):
-        out = tmp_path / (os.path.basename(src) + ".s")
+        out = tmp / (os.path.basename(src) + ".s")
         r = subprocess.run([ksbuild.HIPCC, *ksbuild.COMMON, "--cuda-device-only", "-S", src, "-o", str(out)],
                            capture_output=True, text=True)
         assert r.returncode == 0, r.stderr[-2000:]
-        asm = out.read_text()
-        return src, dispatch_ptr_kernels(asm), flat_memory_kernels(asm)
+        return src, out.read_text()
 
     with concurrent.futures.ThreadPoolExecutor(max_workers=4) as ex:
-        results = list(ex.map(compile_one, srcs))
-    bad = [f"{os.path.basename(src)}: {k} (dispatch pointer)" for src, ks, _ in results for k in ks]
-    bad += [f"{os.path.basename(src)}: {k} (flat memory instruction)" for src, _, fl in results for k in fl]
+        return dict(ex.map(compile_one, srcs))
+
+
+def test_no_dispatch_packet_reads_or_flat_memory(compiled):
+    bad = [f"{os.path.basename(src)}: {k} (dispatch pointer)" for src, asm in compiled.items()
+           for k in dispatch_ptr_kernels(asm)]
+    bad += [f"{os.path.basename(src)}: {k} (flat memory instruction)" for src, asm in compiled.items()
+            for k in flat_memory_kernels(asm)]
+    assert bad == [], "\n".join(bad)
+
+
+def test_register_scratch_and_lds_budgets(compiled):
+    res = {}
+    for asm in compiled.values():
+        res.update(kernel_resources(asm))
+    bad = []
+    for frag, why, vmax, smax, lmax in BUDGETS:
+        hits = [(k, r) for k, r in res.items() if frag in k]
+        assert hits, f"no kernel matches {frag}"
+        for k, (v, sc, lds) in hits:
+            if v > vmax or sc > smax or lds > lmax:
+                bad.append(f"{frag} ({why}): {v} VGPRs (max {vmax}), {sc} B scratch (max {smax}), "
+                           f"{lds} B LDS (max {lmax})")
     assert bad == [], "\n".join(bad)

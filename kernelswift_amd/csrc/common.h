@@ -122,4 +122,14 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t x) {
   }
 }
 
+// Maximum of x over the 64 lanes of a wave (every lane receives it), by lane_xor exchanges: no LDS round trips.
+__device__ __forceinline__ float wave_max_f32(float x) {
+  x = fmaxf(x, __builtin_bit_cast(float, lane_xor<32>(__builtin_bit_cast(uint32_t, x))));
+  x = fmaxf(x, __builtin_bit_cast(float, lane_xor<16>(__builtin_bit_cast(uint32_t, x))));
+  x = fmaxf(x, __builtin_bit_cast(float, lane_xor<8>(__builtin_bit_cast(uint32_t, x))));
+  x = fmaxf(x, __builtin_bit_cast(float, lane_xor<4>(__builtin_bit_cast(uint32_t, x))));
+  x = fmaxf(x, __builtin_bit_cast(float, lane_xor<2>(__builtin_bit_cast(uint32_t, x))));
+  return fmaxf(x, __builtin_bit_cast(float, lane_xor<1>(__builtin_bit_cast(uint32_t, x))));
+}
+
 }  // namespace ks

@@ -71,6 +71,8 @@ struct alignas(16) KeyEntry {
 template <int KD, int HT>
 struct ScoresLds {
   uint4 k[kKR * KD / 8];             // swizzled key block of this workgroup (KD / 8 16-byte chunks per key)
+  uint16_t kstep[HT == 1 ? kKR : 0][KD / 8];  // 16 heads: per key, the step exponents of |k| (step_exponent_pow2 of
+                                              // each 16-byte chunk: a chunk is one accumulation step)
   uint8_t klist[kQW][kKR];           // per wave: block rows of the keys holding a near-tie dot (a wave's tiles
                                      // defer at most every key of the block)
   KeyEntry<HT> ent[kQW][kEntCap];
@@ -335,10 +337,12 @@ indexer_scores_kernel(
   static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
   static_assert(BOUND || !COUNT, "counts of lower ends need the bounds");
   static_assert(!F8 || BOUND, "FP8 keys are read by the bound-emitting variant");
-  // per-dot interval half-widths (bound_c 2^-23 sum |q_k||k_k|, the magnitudes' sum on the MFMA) instead of the
-  // per-head bound_c 2^-23 ||q_h|| max ||k||: about half as wide on typical rows, so about half the near ties and
-  // their exact recomputation, for one more MFMA per 16-key tile.  Built where the registers allow it (16 heads).
+  // per-dot interval half-widths (step_halfwidth_scale: the step-weighted magnitude sum and the step exponents, on
+  // the MFMA) instead of the per-head bound_c 2^-23 ||q_h|| max ||k||: under half as wide on typical rows, so
+  // under half the near ties and their exact recomputation, for three more MFMAs per 16-key tile (D = 64).  Built
+  // where the registers allow it (16 heads).
   constexpr bool PDD = !BOUND && HT == 1;
+  constexpr int kSteps = KD / 8;  // accumulation steps of a dot
   // F8: k points at e4m3 codes (KD bytes per row) with row scales ksc
   const uint8_t *__restrict__ k8 = reinterpret_cast<const uint8_t *>(k);
   __shared__ std::conditional_t<BOUND, ScoresLdsBound<KD, COUNT>, ScoresLds<KD, HT>> L;
@@ -448,13 +452,12 @@ indexer_scores_kernel(
   float knm = 0.f;
 #pragma unroll
   for (int j = 0; j < kKR / 64; ++j) knm = fmaxf(knm, lane + 64 * j < nk ? kn4[j] : 0.f);
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) knm = fmaxf(knm, __shfl_xor(knm, m, 64));
+  knm = wave_max_f32(knm);
   L.qspan[wave][hl] = qs_v;
   L.qnorm[wave][hl] = qn_v;
   // per-head data formed once per head (lane h), not by each of the 16 lanes that use it.  PDD (the exact kernel
   // at 16 heads): per-dot half-widths from the MFMA sum of the magnitudes, dl then holds their additive part
-  L.dl[wave][hl] = PDD ? dot_halfwidth_add(qn_v, knm, bound_c) : dot_halfwidth(qn_v, knm, bound_c);
+  L.dl[wave][hl] = PDD ? step_halfwidth_add(qn_v, knm, bound_c, KD) : dot_halfwidth(qn_v, knm, bound_c);
   if constexpr (BOUND) L.wup[wave][hl] = bf16_abs_round_up(w_v);
   L.w[wave][hl] = w_v;
   // the workgroup's whole key block into LDS (zero rows past T)
@@ -489,6 +492,7 @@ indexer_scores_kernel(
       // below the barrier that orders the key-block loads before the q loads
       const uint32_t msk = kr < nk ? 0xFFFFFFFFu : 0u;
       L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = make_uint4(kv[it].x & msk, kv[it].y & msk, kv[it].z & msk, kv[it].w & msk);
+      if constexpr (PDD) L.kstep[kr][ch] = static_cast<uint16_t>(step_exponent_pow2(kv[it]) & msk);
     }
   }
   if constexpr (COUNT) {  // this wave's lower-end counts start at zero
@@ -563,25 +567,52 @@ indexer_scores_kernel(
   const int64_t lim_rel = limit - kb0;
   const int nlive = lim_rel <= 0 ? 0 : (lim_rel >= 16 * ntiles ? ntiles : static_cast<int>((lim_rel + 15) / 16));
 
-  // PDD: accs holds the MFMA sums of |q_k||k_k|, from |q| fragments formed once (qab) and |k| per tile
-  uint4 qab[HT][KD / 32];
-#pragma unroll
-  for (int m = 0; m < HT; ++m)
-#pragma unroll
-    for (int kk = 0; kk < KD / 32; ++kk) qab[m][kk] = PDD ? abs8(qa[m][kk]) : make_uint4(0, 0, 0, 0);
-  // the MFMAs of 16 keys, lane l16 holding block row key_l (a tile: 16 t + l16; or rows from the deferred list)
-  auto tile_mfma = [&](int key_l, f32x4_t(&acc)[HT], f32x4_t(&accs)[HT]) {
-#pragma unroll
-    for (int m = 0; m < HT; ++m) acc[m] = accs[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // PDD: accs holds V >= W + 8 M of the per-dot half-width (step_halfwidth_scale): the step-weighted magnitudes of
+  // q (qw, formed once: fragment kk of this lane is step 4 kk + g, weight 2^j >= kSteps + 1 - step) against |k|,
+  // then one MFMA of the step exponents: aprime holds 8 A'_s of this lane's head in k-slots 8 g .. 8 g + 7 (steps
+  // 8 g ..; zeros past the last step), gathered through the wave's dot-list LDS (unused until the first flush);
+  // the keys' B'_s are staged with the key block.
+  uint4 qw[HT][KD / 32];
+  uint4 aprime = make_uint4(0, 0, 0, 0);
+  if constexpr (PDD) {
+    uint16_t *sq = reinterpret_cast<uint16_t *>(L.dots[wave]);  // [16 heads][kSteps]: 8 A'_s
 #pragma unroll
     for (int kk = 0; kk < KD / 32; ++kk) {
-      const uint4 bv = L.k[key_l * kC + ((4 * kk + g) ^ (key_l & (kC - 1)))];
+      const int st = 4 * kk + g;
+      qw[0][kk] = step_weighted_q(qa[0][kk], step_weight_log2(kSteps, st));
+      const uint32_t p = step_exponent_pow2(qa[0][kk]);
+      sq[l16 * kSteps + st] = static_cast<uint16_t>(p == 0u ? 0u : p + (3u << 7));  // 8 A'_s: exponent + 3
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint4 t = reinterpret_cast<const uint4 *>(sq)[(l16 * kSteps + 8 * (g % (kSteps / 8))) / 8];
+    aprime = g < kSteps / 8 ? t : make_uint4(0, 0, 0, 0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  // the MFMAs of 16 keys, lane l16 holding block row key_l (a tile: 16 t + l16; or rows from the deferred list)
+  // (every LDS read first; PDD: the magnitude chain starts with the step exponents, so that its dependent MFMAs
+  // alternate with the independent ones of the dot)
+  auto tile_mfma = [&](int key_l, f32x4_t(&acc)[HT], f32x4_t(&accs)[HT]) {
+    uint4 bv[KD / 32];
 #pragma unroll
-      for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv, acc[m]);
+    for (int kk = 0; kk < KD / 32; ++kk) bv[kk] = L.k[key_l * kC + ((4 * kk + g) ^ (key_l & (kC - 1)))];
+#pragma unroll
+    for (int m = 0; m < HT; ++m) acc[m] = accs[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (PDD) {
+      // the step exponents: lane (key row, g) reads the key's B'_s of steps 8 g .. (lanes past the last step read
+      // the first ones: their A' slots are zero, so those products leave the sum unchanged)
+      const uint4 bp = *reinterpret_cast<const uint4 *>(&L.kstep[key_l][8 * (g % (kSteps / 8))]);
+      accs[0] = mfma16(aprime, bp, accs[0]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KD / 32; ++kk) {
+#pragma unroll
+      for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv[kk], acc[m]);
       if constexpr (PDD) {
-        const uint4 ba = abs8(bv);
+        const uint4 ba = abs8(bv[kk]);
 #pragma unroll
-        for (int m = 0; m < HT; ++m) accs[m] = mfma16(qab[m][kk], ba, accs[m]);
+        for (int m = 0; m < HT; ++m) accs[m] = mfma16(qw[m][kk], ba, accs[m]);
       }
     }
   };
@@ -600,7 +631,7 @@ indexer_scores_kernel(
       for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv[kk], acc[m]);
   };
 
-  const float dsc = dot_halfwidth_scale(bound_c);
+  const float dsc = PDD ? step_halfwidth_scale(bound_c, KD) : 0.f;
   // the exact kernel's interval test (the tile epilogue's, below) on the 16 keys of a resolution round: pl, ph and the
   // ballot of the lanes holding a near-tie dot.  (The tile epilogue keeps its own copy: sharing this lambda with
   // the bound kernels' epilogue made the compiler spill registers in their tile loop.)

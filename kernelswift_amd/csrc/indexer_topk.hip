@@ -966,8 +966,7 @@ __global__ __launch_bounds__(kRecThreads, 4) void topk_recompute_kernel(float *s
   // the query's largest padded head norm (lane h of every wave holds head h): decides per tile whether the
   // one-fma half-widths apply
   float qpmax = qnv + 0x1p-122f;
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) qpmax = fmaxf(qpmax, __shfl_xor(qpmax, d, 64));
+  qpmax = wave_max_f32(qpmax);
   qpmax = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int32_t, qpmax)));
 
   // ---- tau: bucket e of the thread's kBPT is 2048 - kBPT (tid + 1) + e (the top one is e = kBPT - 1)

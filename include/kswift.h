@@ -156,6 +156,20 @@ int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf
                int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D,
                int64_t T, int64_t k_batch_stride, void *workspace,
                size_t workspace_bytes, void *stream);
+/* The same with the head weights multiplied by w_scale on the way, as the
+ * reference's caller computes weights_proj(x) * (softmax_scale * n_heads^-0.5)
+ * (baseline/indexer.py:174-175) before the indexer: each weight becomes
+ * fp32(w * fp32(w_scale)), rounded to bf16 (nearest even) for bf16 weights,
+ * which is torch's rounding of a tensor times a Python float; the scaled
+ * weights live in the workspace, the input is not modified.  w_scale finite. */
+int ks_indexer_scaled(const uint16_t *q, const uint16_t *k, const void *w,
+                      int32_t w_bf16, float w_scale, const float *freqs,
+                      int64_t freq_rows, int64_t rope_start, int64_t rope_dim,
+                      int32_t rope_k, int64_t k_top, int32_t causal,
+                      int64_t start_pos, int32_t ratio, int64_t offset, void *out,
+                      int32_t out_i64, int64_t B, int64_t S, int64_t H, int64_t D,
+                      int64_t T, int64_t k_batch_stride, void *workspace,
+                      size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------
  * FP8 block quantisation of bf16 rows (e4m3fn codes, one fp32 scale per block),

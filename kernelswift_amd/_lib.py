@@ -33,6 +33,9 @@ SIGNATURES = {
     "ks_indexer": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32,
                                   _c_i64, _c_i32, _c_i64, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                   _c_i64, _c_p, _c_sz, _c_p]),
+    "ks_indexer_scaled": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i32, _c_f, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64,
+                                         _c_i32, _c_i64, _c_i32, _c_i64, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64,
+                                         _c_i64, _c_i64, _c_p, _c_sz, _c_p]),
     "ks_fp8_quant_rows": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p, _c_p, _c_p]),
     "ks_indexer_fp8": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i64, _c_i32, _c_i64, _c_i32, _c_i64,
                                       _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_sz,

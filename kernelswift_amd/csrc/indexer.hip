@@ -31,6 +31,7 @@ struct IndexerWs {
   float *kmax;    // per key block norm maxima of the bounded path
   uint64_t *part;  // the bounded selection's lists, bucket counts and list lengths
   int64_t part_cap;
+  void *w_scaled;  // the head weights times w_scale (ks_indexer_scaled), in the weights' format
   size_t bytes;
 };
 
@@ -56,6 +57,7 @@ IndexerWs carve(void *base, int64_t B, int64_t S, int64_t H, int64_t D, int64_t 
   // the bounded selection's lists and counts (only shapes that can take the bounded path)
   w.part_cap = (H == 64 && D == 128) ? ks::topk_bounded_part_capacity(B * S, T) : 0;
   w.part = reinterpret_cast<uint64_t *>(take(size_t(w.part_cap) * 8));
+  w.w_scaled = take(size_t(B * S * H) * 4);
   w.bytes = off;
   return w;
 }
@@ -145,7 +147,7 @@ int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_
                  int64_t freq_rows, int64_t rope_start, int64_t rope_dim, int32_t rope_k, int64_t k_top,
                  int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64,
                  int64_t B, int64_t S, int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
-                 size_t workspace_bytes, void *stream, float bound_c, uint32_t *stats, int path) {
+                 size_t workspace_bytes, void *stream, float bound_c, uint32_t *stats, int path, float w_scale) {
   ks::last_error().clear();
   int rc = check_indexer_args("ks_indexer", k_top, start_pos, ratio, B, S, H, D, T, k_batch_stride, path);
   if (rc != KS_OK) return rc;
@@ -170,12 +172,15 @@ int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_
   const ks::RowJob qjob{q, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H, H, S, start_pos, rd};
   const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
   const bool bounded = takes_bounded(k_top, w_bf16, H, D, T, path);
+  // w_scale != 1: the row preparation also writes the scaled weights (one per q row), which the later launches read
+  const bool scaled = w_scale != 1.0f;
+  const ks::WeightScale wsc{w, ws.w_scaled, w_scale, w_bf16 ? 1 : 0};
   rc = ks::launch_rope_rows(qjob, kjob, freqs, static_cast<int>(D), static_cast<int>(rope_start), st,
                             bounded ? ks::topk_bounded_counts(ws.part, B * S, T) : nullptr,
-                            bounded ? count_words16(ws, B, S, T) : 0);
+                            bounded ? count_words16(ws, B, S, T) : 0, scaled ? &wsc : nullptr);
   if (rc != KS_OK) return rc;
-  return indexer_select("ks_indexer", ws, w, w_bf16, k_top, causal, start_pos, ratio, offset, out, out_i64, B, S, H,
-                        D, T, st, bound_c, stats, path);
+  return indexer_select("ks_indexer", ws, scaled ? ws.w_scaled : w, w_bf16, k_top, causal, start_pos, ratio, offset,
+                        out, out_i64, B, S, H, D, T, st, bound_c, stats, path);
 }
 
 int indexer_fp8_impl(const uint8_t *q, const float *q_scale, const uint8_t *k, const float *k_scale, const void *w,
@@ -225,7 +230,20 @@ extern "C" int ks_indexer(const uint16_t *q, const uint16_t *k, const void *w, i
                           int64_t k_batch_stride, void *workspace, size_t workspace_bytes, void *stream) {
   return indexer_impl(q, k, w, w_bf16, freqs, freq_rows, rope_start, rope_dim, rope_k, k_top, causal, start_pos, ratio,
                       offset, out, out_i64, B, S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream,
-                      ks::score_bound_c(D), nullptr, 0);
+                      ks::score_bound_c(D), nullptr, 0, 1.0f);
+}
+
+extern "C" int ks_indexer_scaled(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16,
+                                 float w_scale, const float *freqs, int64_t freq_rows, int64_t rope_start,
+                                 int64_t rope_dim, int32_t rope_k, int64_t k_top, int32_t causal, int64_t start_pos,
+                                 int32_t ratio, int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
+                                 int64_t H, int64_t D, int64_t T, int64_t k_batch_stride, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(__builtin_isfinite(w_scale), "ks_indexer_scaled: w_scale must be finite");
+  return indexer_impl(q, k, w, w_bf16, freqs, freq_rows, rope_start, rope_dim, rope_k, k_top, causal, start_pos, ratio,
+                      offset, out, out_i64, B, S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream,
+                      ks::score_bound_c(D), nullptr, 0, w_scale);
 }
 
 // Diagnostic variant (not part of the public header): explicit error-bound constant, path choice (0 auto,
@@ -239,7 +257,7 @@ extern "C" int ks_dbg_indexer(const uint16_t *q, const uint16_t *k, const void *
                               float bound_c, uint32_t *stats, int32_t path) {
   return indexer_impl(q, k, w, w_bf16, freqs, freq_rows, rope_start, rope_dim, rope_k, k_top, causal, start_pos, ratio,
                       offset, out, out_i64, B, S, H, D, T, k_batch_stride, workspace, workspace_bytes, stream, bound_c,
-                      stats, path);
+                      stats, path, 1.0f);
 }
 
 extern "C" int ks_indexer_fp8(const uint8_t *q, const float *q_scale, const uint8_t *k, const float *k_scale,

@@ -232,8 +232,18 @@ struct RowJob {
 // otherwise.  Rotated dims [rope_start, rope_start + job.rope_dim), freqs = (cos, sin) per position.  The
 // launch also clears zero16 16-byte words at zero (the bounded selection's counts, which the score kernel
 // that follows accumulates into).
+// Head weights scaled on the way (the fused indexer's w_scale): out[r] = w[r] * scale for the first job's rows r
+// (one weight per q row), rounded as torch rounds a tensor times a Python float: fp32(w * fp32(scale)), then
+// bf16 (nearest even) for bf16 weights.
+struct WeightScale {
+  const void *w;
+  void *out;
+  float scale;
+  int bf16;
+};
+
 int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
-                     hipStream_t stream, void *zero = nullptr, int64_t zero16 = 0);
+                     hipStream_t stream, void *zero = nullptr, int64_t zero16 = 0, const WeightScale *wscale = nullptr);
 
 // One set of e4m3 rows for the dequantisation / row-statistics launch: row r is source row
 // (r / rows_per_batch) * src_batch_rows + r % rows_per_batch of src (D code bytes) with fp32 scale

@@ -53,7 +53,8 @@ RowJobK kernel_job(const RowJob &j) {
 template <int CPR>
 __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, uint32_t blocks0,
                                                        const float *__restrict__ freqs, int D, FastDiv cpr,
-                                                       int rope_start, uint4 *__restrict__ zero, uint32_t zero16) {
+                                                       int rope_start, uint4 *__restrict__ zero, uint32_t zero16,
+                                                       WeightScale wsc) {
   const bool second = blockIdx.x >= blocks0;
 #define KS_PICK(f) (second ? j1.f : j0.f)
   const uint16_t *__restrict__ src = KS_PICK(src);
@@ -99,6 +100,15 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, 
       row_norm_span(ss, lsb, norm[row], span[row]);
     }
   }
+  // the first job's head weights scaled, one per row (torch's rounding of a tensor times a Python float)
+  if (wsc.out != nullptr && !second && live && j == 0) {
+    if (wsc.bf16) {
+      const float x = bf16_to_f32(static_cast<const uint16_t *>(wsc.w)[row]) * wsc.scale;
+      static_cast<uint16_t *>(wsc.out)[row] = f32_to_bf16_rne(x);
+    } else {
+      static_cast<float *>(wsc.out)[row] = static_cast<const float *>(wsc.w)[row] * wsc.scale;
+    }
+  }
   // after the row's own stores, so that its loads do not wait behind these
   for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < zero16; i += gridDim.x * 256u) zero[i] = make_uint4(0, 0, 0, 0);
 }
@@ -106,7 +116,7 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, 
 }  // namespace
 
 int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs, int D, int rope_start,
-                     hipStream_t stream, void *zero, int64_t zero16) {
+                     hipStream_t stream, void *zero, int64_t zero16, const WeightScale *wscale) {
   KS_CHECK_ARG(zero16 >= 0 && zero16 < (int64_t(1) << 31) && (zero16 == 0 || aligned(zero, 16)),
                "rope rows: clear range of %lld words", (long long)zero16);
   const int64_t c0 = job0.rows * (D / 8), c1 = job1.rows * (D / 8);
@@ -129,12 +139,13 @@ int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs,
   const uint32_t n0 = static_cast<uint32_t>(b0);
   uint4 *zp = static_cast<uint4 *>(zero);
   const uint32_t zn = static_cast<uint32_t>(zero16);
+  const WeightScale ws = wscale != nullptr ? *wscale : WeightScale{nullptr, nullptr, 1.f, 0};
   if (stats && D == 128) {
-    hipLaunchKernelGGL(rope_rows_kernel<16>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn);
+    hipLaunchKernelGGL(rope_rows_kernel<16>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn, ws);
   } else if (stats) {
-    hipLaunchKernelGGL(rope_rows_kernel<8>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn);
+    hipLaunchKernelGGL(rope_rows_kernel<8>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn, ws);
   } else {
-    hipLaunchKernelGGL(rope_rows_kernel<0>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn);
+    hipLaunchKernelGGL(rope_rows_kernel<0>, grid, dim3(256), 0, stream, k0, k1, n0, freqs, D, cpr, rope_start, zp, zn, ws);
   }
   KS_CHECK_LAUNCH("rope_rows_kernel");
   return KS_OK;

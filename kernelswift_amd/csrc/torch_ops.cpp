@@ -115,7 +115,7 @@ at::Tensor indexer_topk(const at::Tensor& scores, bool causal, int64_t ratio, in
 at::Tensor indexer(const at::Tensor& q, const at::Tensor& k, const at::Tensor& weights,
                    const c10::optional<at::Tensor>& freqs, int64_t k_top, bool causal, int64_t start_pos, int64_t ratio,
                    int64_t offset, int64_t rope_start, int64_t rope_dim, bool rope_k, bool out_i64,
-                   c10::optional<int64_t> T_opt) {
+                   c10::optional<int64_t> T_opt, double w_scale) {
   check_gpu(q, "q");
   check_gpu(weights, "weights");
   check_gpu(k, "k", false);
@@ -144,10 +144,11 @@ at::Tensor indexer(const at::Tensor& q, const at::Tensor& k, const at::Tensor& w
   at::Tensor ws = at::empty({static_cast<int64_t>(std::max<size_t>(need, 1))}, q.options().dtype(at::kByte));
   const int64_t kk = std::min(k_top, T);
   at::Tensor out = at::empty({B, S, kk}, q.options().dtype(out_i64 ? at::kLong : at::kInt));
-  check_rc(ks_indexer(reinterpret_cast<const uint16_t*>(q.data_ptr()), reinterpret_cast<const uint16_t*>(k.data_ptr()),
-                      weights.data_ptr(), wbf, fp, frows, rope_start, rope_dim, rope_k ? 1 : 0, k_top, causal ? 1 : 0,
-                      start_pos, static_cast<int32_t>(ratio), offset, out.data_ptr(), out_i64 ? 1 : 0, B, S, H, D, T, kbs,
-                      ws.data_ptr(), ws.numel(), current_stream(q)),
+  check_rc(ks_indexer_scaled(reinterpret_cast<const uint16_t*>(q.data_ptr()),
+                             reinterpret_cast<const uint16_t*>(k.data_ptr()), weights.data_ptr(), wbf,
+                             static_cast<float>(w_scale), fp, frows, rope_start, rope_dim, rope_k ? 1 : 0, k_top,
+                             causal ? 1 : 0, start_pos, static_cast<int32_t>(ratio), offset, out.data_ptr(),
+                             out_i64 ? 1 : 0, B, S, H, D, T, kbs, ws.data_ptr(), ws.numel(), current_stream(q)),
            "ks_mi355x::indexer");
   return out;
 }
@@ -295,7 +296,7 @@ TORCH_LIBRARY(ks_mi355x, m) {
         "bool out_i64=True) -> Tensor");
   m.def("indexer(Tensor q, Tensor k, Tensor weights, Tensor? freqs, int k_top, bool causal, int start_pos, "
         "int ratio=1, int offset=0, int rope_start=0, int rope_dim=64, bool rope_k=True, bool out_i64=False, "
-        "int? T=None) -> Tensor");
+        "int? T=None, float w_scale=1.0) -> Tensor");
   m.def("sparse_attn(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, float softmax_scale, "
         "int? dv=None) -> Tensor");
   m.def("fp8_quant(Tensor x, int block=128, bool ue8m0=True) -> (Tensor, Tensor)");

@@ -157,9 +157,10 @@ def indexer_workspace_size(B: int, S: int, H: int, D: int, T: int) -> int:
 def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Optional[torch.Tensor], k_top: int,
             causal: bool, start_pos: int, ratio: int = 1, offset: int = 0, rope_start: int = 0, rope_dim: int = 64,
             rope_k: bool = True, out_dtype: torch.dtype = torch.int32,
-            workspace: Optional[torch.Tensor] = None, T: Optional[int] = None) -> torch.Tensor:
+            workspace: Optional[torch.Tensor] = None, T: Optional[int] = None, w_scale: float = 1.0) -> torch.Tensor:
     """Fused RoPE -> exact scores -> exact top-k (the reference wrapper's three-op sequence,
-    optimized/indexer_project/indexer.py:197-222).  Inputs are not modified.
+    optimized/indexer_project/indexer.py:197-222).  Inputs are not modified.  w_scale: the weights are used as
+    weights * w_scale with torch's rounding (ks_indexer_scaled), without a separate multiply.
 
     q: bf16 [B, S, H, D] (D = 64 or 128); k: bf16 [B, Tk, D] whose rows are contiguous (a batch-strided view
     such as kv_cache[:B] is accepted without a copy), the first T (default Tk) rows are the keys;
@@ -188,11 +189,11 @@ def indexer(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor, freqs: Opti
     kk = min(k_top, T)
     out = torch.empty((B, S, kk), dtype=out_dtype, device=q.device)
     fr = freqs.shape[0] if freqs is not None else 0
-    _lib.check(_lib.load().ks_indexer(_p(q), _p(k), _p(weights), 1 if weights.dtype == torch.bfloat16 else 0,
-                                      _p(freqs), fr, rope_start, rope_dim, 1 if rope_k else 0, k_top,
-                                      1 if causal else 0, start_pos, ratio, offset, _p(out),
-                                      1 if out_dtype == torch.int64 else 0, B, S, H, D, T, kbs, _p(workspace),
-                                      workspace.numel(), _stream(q)), "indexer")
+    _lib.check(_lib.load().ks_indexer_scaled(_p(q), _p(k), _p(weights), 1 if weights.dtype == torch.bfloat16 else 0,
+                                             float(w_scale), _p(freqs), fr, rope_start, rope_dim, 1 if rope_k else 0,
+                                             k_top, 1 if causal else 0, start_pos, ratio, offset, _p(out),
+                                             1 if out_dtype == torch.int64 else 0, B, S, H, D, T, kbs, _p(workspace),
+                                             workspace.numel(), _stream(q)), "indexer")
     return out
 
 

@@ -8,7 +8,8 @@ reduction and the causal mask, and the exact sorted top-k with the -1 / +offset 
 call of the fused gfx950 operator torch.ops.ks_mi355x.indexer (ks_indexer), without a transposed or padded copy
 of the cache.
 
-Semantics kept from the baseline: weights = weights_proj(x) * (head_dim^-0.5 * n_heads^-0.5) in bf16;
+Semantics kept from the baseline: weights = weights_proj(x) * (head_dim^-0.5 * n_heads^-0.5) in bf16 (the product
+is taken inside the fused call, w_scale, with torch's rounding: no separate multiply launch);
 keys are kv_cache[:B, :(start_pos + S) // ratio] (not rotated); the causal mask and the -1 post-processing
 apply only when start_pos == 0; output int64 [B, S, min(index_topk, (start_pos + S) // ratio)].  Scores
 follow the exact canonical arithmetic of include/kswift.h, and ties keep the lowest key index first.
@@ -60,13 +61,19 @@ class ModelNew(nn.Module):
         self.compress_ratio = compress_ratio
         self.register_buffer("kv_cache", kv_cache)
         self.register_buffer("freqs_cis", freqs_cis)
+        self._freqs_key = None
+        self._freqs_val = None
 
     def _freqs(self) -> torch.Tensor:
-        """(cos, sin) float32 [rows, rope_head_dim/2, 2] from the complex table (or its real view)."""
+        """(cos, sin) float32 [rows, rope_head_dim/2, 2] from the complex table (or its real view); kept between
+        calls while the buffer (storage, version, dtype, shape) is unchanged."""
         f = self.freqs_cis
-        if f.is_complex():
-            f = torch.view_as_real(f)
-        return f.reshape(f.shape[0], -1, 2).to(torch.float32).contiguous()
+        key = (f.data_ptr(), f._version, f.dtype, tuple(f.shape), f.device)
+        if key != self._freqs_key:
+            g = torch.view_as_real(f) if f.is_complex() else f
+            self._freqs_val = g.reshape(g.shape[0], -1, 2).to(torch.float32).contiguous()
+            self._freqs_key = key
+        return self._freqs_val
 
     def forward(self, x: torch.Tensor, qr: torch.Tensor, start_pos: int, offset: int) -> torch.Tensor:
         ops = _ops()
@@ -78,9 +85,10 @@ class ModelNew(nn.Module):
         if k_top == 0:
             return torch.empty((bsz, seqlen, 0), dtype=torch.int64, device=x.device)
         q = self.wq_b(qr).unflatten(-1, (self.n_local_heads, self.head_dim)).contiguous()
-        weights = (self.weights_proj(x) * (self.softmax_scale * self.n_heads ** -0.5)).contiguous()
+        weights = self.weights_proj(x).contiguous()
         return ops.indexer(q, self.kv_cache[:bsz], weights, self._freqs(), k_top, start_pos == 0, start_pos, ratio,
-                           offset, self.head_dim - self.rope_head_dim, self.rope_head_dim, False, True, T)
+                           offset, self.head_dim - self.rope_head_dim, self.rope_head_dim, False, True, T,
+                           w_scale=self.softmax_scale * self.n_heads ** -0.5)
 
 
 def _example_args() -> ModelArgs:

@@ -646,3 +646,57 @@ def test_indexer_multi_item_grids(device, B, S, T):
     torch.cuda.synchronize()
     want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), k_top, True, start_pos, 1, 0, 0, 64, True)
     np.testing.assert_array_equal(got.cpu().numpy().astype(np.int64), want)
+
+
+@pytest.mark.parametrize("H,D,w_bf16", [(16, 64, True), (64, 128, False), (32, 128, True), (64, 128, True)])
+def test_indexer_weight_scale(device, H, D, w_bf16):
+    # w_scale (ks_indexer_scaled, the drop-in's weights_proj(x) * scale): the same indices as the weights multiplied
+    # by torch first, with a scale that is not a power of two (so the product's rounding matters); 64 heads of 128
+    # with fp32 weights take the bounded path, whose recomputation reads the scaled weights too
+    g = torch.Generator().manual_seed(H + D + w_bf16)
+    B, S, T = 2, 24, 700
+    q = torch.randn(B, S, H, D, generator=g).bfloat16().to(device)
+    k = torch.randn(B, T, D, generator=g).bfloat16().to(device)
+    w = (torch.randn(B, S, H, generator=g) / 8).to(device)
+    if w_bf16:
+        w = w.bfloat16()
+    tab = workloads.freqs_table(64, 1024).to(device)
+    scale = 128 ** -0.5 * 48 ** -0.5
+    print(f"[case] indexer w_scale H={H} D={D} w_bf16={w_bf16}", flush=True)
+    got = ops.indexer(q, k, w, tab, 128, True, T - S, rope_start=0, rope_dim=64, w_scale=scale)
+    want = ops.indexer(q, k, (w * scale).contiguous(), tab, 128, True, T - S, rope_start=0, rope_dim=64)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    # a negative scale selects other keys: the scale is applied, not dropped
+    neg = ops.indexer(q, k, w, tab, 128, True, T - S, rope_start=0, rope_dim=64, w_scale=-scale)
+    assert torch.equal(neg, ops.indexer(q, k, (w * -scale).contiguous(), tab, 128, True, T - S, rope_start=0,
+                                        rope_dim=64))
+    assert not torch.equal(neg, want)
+    # the torch operator takes the same argument
+    tops = _lib.torch_ops()
+    got2 = tops.indexer(q, k, w, tab, 128, True, T - S, 1, 0, 0, 64, True, False, None, w_scale=scale)
+    assert torch.equal(got2, want)
+
+
+@pytest.mark.parametrize("D,rs,rd,rope_k,w_bf16,causal", [(64, 32, 32, False, True, True),
+                                                         (64, 16, 32, True, False, True),
+                                                         (64, 0, 0, False, True, True),
+                                                         (128, 0, 64, True, True, True),
+                                                         (128, 40, 64, False, False, True),
+                                                         (128, 24, 96, True, True, False)])
+def test_indexer_16_heads_rope_layouts(device, D, rs, rd, rope_k, w_bf16, causal):
+    # the fused indexer at 16 heads (the exact path with its per-dot half-widths): rotated ranges that start inside
+    # a 32-element fragment or straddle two, none at all, rotated keys, fp32 and bf16 weights, causal and not (an
+    # offset and a start position past zero), bit for bit against the oracle
+    g = torch.Generator().manual_seed(D + rs + rd + rope_k)
+    B, S, H, T = 2, 40, 16, 700
+    q = torch.randn(B, S, H, D, generator=g).bfloat16()
+    k = torch.randn(B, T, D, generator=g).bfloat16()
+    w = torch.randn(B, S, H, generator=g) / 8
+    if w_bf16:
+        w = w.bfloat16()
+    tab = workloads.freqs_table(max(rd, 2), 1024)
+    start = T - S if causal else 123
+    print(f"[case] indexer 16 heads D={D} rope=[{rs},{rs + rd}) rope_k={rope_k} w_bf16={w_bf16} causal={causal}",
+          flush=True)
+    _indexer_vs_oracle(q, k, w, tab, 96, causal, start, 1, 0 if causal else 5, rs, rd, rope_k, T)

@@ -665,7 +665,7 @@ indexer_scores_kernel(
   // the causal limit: a key past it keeps the -inf stored here); pl / ph keep the interval ends.
   auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
                            uint32_t(&ph)[2 * HT]) {
-    const bool fcd = BOUND ? decltype(FC)::value : forced;
+    const bool fcd = decltype(FC)::value;
     const int key_l = 16 * t + l16;
     const int key = kb0 + key_l;
     const bool kvalid = key_l < nk;
@@ -791,22 +791,34 @@ indexer_scores_kernel(
     // the exact kernel: the tile loop only lists the keys holding a near-tie dot (their block rows, in LDS); the
     // listed keys are resolved after it.  Nothing of the recomputation is live in the loop, so the loop keeps its
     // pipeline in few registers.  The next tile's MFMAs past the last live tile repeat that tile (results unused).
+    // Two tiles per iteration alternate the accumulator sets (no copies between them); the loop is built twice,
+    // for forced waves (every key listed) and the others, so that the tile epilogue carries no select for it.
     f32x4_t accs[HT], nxts[HT];
     uint8_t *klist = L.klist[wave];
     int nlist = 0;
-    if (nlive > 0) tile_mfma(l16, acc, accs);
-    for (int t = 0; t < nlive; ++t) {
-      uint32_t pl[2 * HT], ph[2 * HT];
-      tile_mfma(16 * (t + 1 < nlive ? t + 1 : t) + l16, nxt, nxts);
-      const uint32_t km = tile_epilogue(std::false_type{}, t, acc, accs, pl, ph);
-      if (g == 0 && ((km >> l16) & 1u))
-        klist[nlist + __builtin_popcount(km & ((1u << l16) - 1u))] = static_cast<uint8_t>(16 * t + l16);
-      nlist += __builtin_popcount(km);
-#pragma unroll
-      for (int m = 0; m < HT; ++m) {
-        acc[m] = nxt[m];
-        if constexpr (PDD) accs[m] = nxts[m];
+    auto run = [&](auto FC) {
+      auto epilogue = [&](int t, const f32x4_t(&a)[HT], const f32x4_t(&as)[HT]) {
+        uint32_t pl[2 * HT], ph[2 * HT];
+        const uint32_t km = tile_epilogue(FC, t, a, as, pl, ph);
+        if (g == 0 && ((km >> l16) & 1u))
+          klist[nlist + __builtin_popcount(km & ((1u << l16) - 1u))] = static_cast<uint8_t>(16 * t + l16);
+        nlist += __builtin_popcount(km);
+      };
+      const int last = nlive - 1;
+      tile_mfma(l16, acc, accs);
+      for (int t = 0; t < nlive; t += 2) {
+        tile_mfma(16 * (t + 1 < nlive ? t + 1 : last) + l16, nxt, nxts);
+        epilogue(t, acc, accs);
+        if (t + 1 >= nlive) break;
+        tile_mfma(16 * (t + 2 < nlive ? t + 2 : last) + l16, acc, accs);
+        epilogue(t + 1, nxt, nxts);
       }
+    };
+    if (nlive > 0) {
+      if (forced)
+        run(std::true_type{});
+      else
+        run(std::false_type{});
     }
     // resolution, 16 listed keys at a time: the same MFMAs and interval test on their rows (the same operands, so
     // the same interval ends), all four groups' ends of each key saved as a deferred entry, and the entries'

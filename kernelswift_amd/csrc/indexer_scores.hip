@@ -558,6 +558,7 @@ indexer_scores_kernel(
     }
   }
   const int64_t limit = causal ? (start_pos + s + 1) / ratio : INT64_MAX;
+  const int limit32 = static_cast<int>(limit < INT32_MAX ? limit : INT32_MAX);  // keys are below T < 2^31
   float *orow = scores + (b * S + s) * T;
   float *urow = BOUND ? bounds + (b * S + s) * T : nullptr;
   uint32_t n_exact = 0, n_unres = 0;
@@ -663,12 +664,15 @@ indexer_scores_kernel(
   auto key_mask = [](uint64_t r) { return static_cast<uint32_t>((r | (r >> 16) | (r >> 32) | (r >> 48)) & 0xFFFFull); };
   // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot (in the exact kernel, before
   // the causal limit: a key past it keeps the -inf stored here); pl / ph keep the interval ends.
-  auto tile_epilogue = [&](auto FC, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT], uint32_t(&pl)[2 * HT],
-                           uint32_t(&ph)[2 * HT]) {
+  // FULL (the exact kernel's tiles before its last live one): every key of the tile is in range and before the
+  // causal limit, so the tile needs no per-lane key tests.
+  auto tile_epilogue = [&](auto FC, auto FULL, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT],
+                           uint32_t(&pl)[2 * HT], uint32_t(&ph)[2 * HT]) {
     const bool fcd = decltype(FC)::value;
+    constexpr bool full = decltype(FULL)::value;
     const int key_l = 16 * t + l16;
     const int key = kb0 + key_l;
-    const bool kvalid = key_l < nk;
+    const bool kvalid = full || key_l < nk;
     // interval test: RNE(A - delta) == RNE(A + delta) (after ReLU) <=> the exact dot rounds to the same
     // relu'd bf16 value; pl holds that value for the head sum
     uint64_t anyr = 0;
@@ -724,10 +728,10 @@ indexer_scores_kernel(
     }
     const float tot = combine_groups(G);
     const float outv = WBF ? round_score_bf16(tot) : tot;
-    if (g == 0 && kvalid) orow[key] = (key < limit) ? outv : -INFINITY;
+    if (g == 0 && kvalid) orow[key] = (full || key < limit32) ? outv : -INFINITY;
     // keys past T are zero rows and, in the exact kernel, keys past the causal limit are -inf: neither is deferred
     // (the bound kernel stores bound 0 past the limit, below)
-    anyr &= __builtin_amdgcn_ballot_w64(BOUND ? kvalid : (kvalid && key < limit));
+    if constexpr (!full) anyr &= __builtin_amdgcn_ballot_w64(BOUND ? kvalid : (kvalid && key < limit32));
     const uint32_t km = key_mask(anyr);
     if constexpr (BOUND) {
       // |exact score - tot| <= sum_h |w_h| (ph_h - pl_h) + (rounding of the canonical sum: 38 roundings of
@@ -744,7 +748,7 @@ indexer_scores_kernel(
       }
       float u = (dph[0] - dpl[0]) + 0x1p-16f * (dph[0] + dpl[0]) + 0x1p-21f * fabsf(tot) + 0x1p-100f;
       if (fcd) u = __builtin_inff();  // score 0 with an infinite bound: always recomputed
-      const bool live_key = kvalid && key < limit;
+      const bool live_key = kvalid && key < limit32;
       const float us = (live_key && ((km >> l16) & 1u)) ? u : 0.f;
       if (g == 0 && kvalid) urow[key] = us;
       // the row's threshold histogram: first 11-bit digit of the lower end's key, counted for the valid columns
@@ -773,11 +777,11 @@ indexer_scores_kernel(
         uint32_t pl[2 * HT], ph[2 * HT];
         tile_mfma_b(bb, nxt);
         tile_b(t + 2 < nlive ? t + 2 : last, ba);
-        (void)tile_epilogue(FC, t, acc, acc, pl, ph);
+        (void)tile_epilogue(FC, std::false_type{}, t, acc, acc, pl, ph);
         if (t + 1 >= nlive) break;
         tile_mfma_b(ba, acc);
         tile_b(t + 3 < nlive ? t + 3 : last, bb);
-        (void)tile_epilogue(FC, t + 1, nxt, nxt, pl, ph);
+        (void)tile_epilogue(FC, std::false_type{}, t + 1, nxt, nxt, pl, ph);
       }
     };
     if (nlive > 0) {
@@ -796,29 +800,38 @@ indexer_scores_kernel(
     f32x4_t accs[HT], nxts[HT];
     uint8_t *klist = L.klist[wave];
     int nlist = 0;
-    auto run = [&](auto FC) {
-      auto epilogue = [&](int t, const f32x4_t(&a)[HT], const f32x4_t(&as)[HT]) {
-        uint32_t pl[2 * HT], ph[2 * HT];
-        const uint32_t km = tile_epilogue(FC, t, a, as, pl, ph);
+    // Tiles before the last live one are full (every key in range and before the limit).
+    auto epilogue = [&](auto FC, auto FULL, int t, const f32x4_t(&a)[HT], const f32x4_t(&as)[HT]) {
+      uint32_t pl[2 * HT], ph[2 * HT];
+      const uint32_t km = tile_epilogue(FC, FULL, t, a, as, pl, ph);
+      if (km != 0u) {  // wave-uniform
         if (g == 0 && ((km >> l16) & 1u))
           klist[nlist + __builtin_popcount(km & ((1u << l16) - 1u))] = static_cast<uint8_t>(16 * t + l16);
         nlist += __builtin_popcount(km);
-      };
-      const int last = nlive - 1;
-      tile_mfma(l16, acc, accs);
-      for (int t = 0; t < nlive; t += 2) {
-        tile_mfma(16 * (t + 1 < nlive ? t + 1 : last) + l16, nxt, nxts);
-        epilogue(t, acc, accs);
-        if (t + 1 >= nlive) break;
-        tile_mfma(16 * (t + 2 < nlive ? t + 2 : last) + l16, acc, accs);
-        epilogue(t + 1, nxt, nxts);
       }
     };
-    if (nlive > 0) {
-      if (forced)
-        run(std::true_type{});
-      else
-        run(std::false_type{});
+    const int last = nlive - 1;
+    if (nlive > 0 && !forced) {
+      const std::true_type full;
+      const std::false_type fc, partial;
+      tile_mfma(l16, acc, accs);
+      int t = 0;
+      for (; t + 2 <= last; t += 2) {
+        tile_mfma(16 * (t + 1) + l16, nxt, nxts);
+        epilogue(fc, full, t, acc, accs);
+        tile_mfma(16 * (t + 2) + l16, acc, accs);
+        epilogue(fc, full, t + 1, nxt, nxts);
+      }
+      if (t < last) {
+        tile_mfma(16 * last + l16, nxt, nxts);
+        epilogue(fc, full, t, acc, accs);
+        epilogue(fc, partial, last, nxt, nxts);
+      } else {
+        epilogue(fc, partial, last, acc, accs);
+      }
+    } else if (nlive > 0) {
+      // a forced wave lists every key (its interval ends are not used)
+      for (int t = 0; t < nlive; ++t) epilogue(std::true_type{}, std::false_type{}, t, acc, accs);
     }
     // resolution, 16 listed keys at a time: the same MFMAs and interval test on their rows (the same operands, so
     // the same interval ends), all four groups' ends of each key saved as a deferred entry, and the entries'

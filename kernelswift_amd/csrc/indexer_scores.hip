@@ -665,9 +665,10 @@ indexer_scores_kernel(
   // returns the mask of this tile's keys (bit = key column) that hold a near-tie dot (in the exact kernel, before
   // the causal limit: a key past it keeps the -inf stored here); pl / ph keep the interval ends.
   // FULL (the exact kernel's tiles before its last live one): every key of the tile is in range and before the
-  // causal limit, so the tile needs no per-lane key tests.
-  auto tile_epilogue = [&](auto FC, auto FULL, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT],
-                           uint32_t(&pl)[2 * HT], uint32_t(&ph)[2 * HT]) {
+  // causal limit, so the tile needs no per-lane key tests.  PAIR (the exact kernel): the lane's group sum is
+  // returned in gsum, and store_pair combines two tiles' sums at once; otherwise the tile stores its own scores.
+  auto tile_epilogue = [&](auto FC, auto FULL, auto PAIR, int t, const f32x4_t(&acc)[HT], const f32x4_t(&accs)[HT],
+                           uint32_t(&pl)[2 * HT], uint32_t(&ph)[2 * HT], float &gsum) {
     const bool fcd = decltype(FC)::value;
     constexpr bool full = decltype(FULL)::value;
     const int key_l = 16 * t + l16;
@@ -726,9 +727,14 @@ indexer_scores_kernel(
         __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
       }
     }
-    const float tot = combine_groups(G);
-    const float outv = WBF ? round_score_bf16(tot) : tot;
-    if (g == 0 && kvalid) orow[key] = (full || key < limit32) ? outv : -INFINITY;
+    float tot = 0.f, outv = 0.f;
+    if constexpr (decltype(PAIR)::value) {
+      gsum = G;
+    } else {
+      tot = combine_groups(G);
+      outv = WBF ? round_score_bf16(tot) : tot;
+      if (g == 0 && kvalid) orow[key] = (full || key < limit32) ? outv : -INFINITY;
+    }
     // keys past T are zero rows and, in the exact kernel, keys past the causal limit are -inf: neither is deferred
     // (the bound kernel stores bound 0 past the limit, below)
     if constexpr (!full) anyr &= __builtin_amdgcn_ballot_w64(BOUND ? kvalid : (kvalid && key < limit32));
@@ -777,11 +783,12 @@ indexer_scores_kernel(
         uint32_t pl[2 * HT], ph[2 * HT];
         tile_mfma_b(bb, nxt);
         tile_b(t + 2 < nlive ? t + 2 : last, ba);
-        (void)tile_epilogue(FC, std::false_type{}, t, acc, acc, pl, ph);
+        float gs;
+        (void)tile_epilogue(FC, std::false_type{}, std::false_type{}, t, acc, acc, pl, ph, gs);
         if (t + 1 >= nlive) break;
         tile_mfma_b(ba, acc);
         tile_b(t + 3 < nlive ? t + 3 : last, bb);
-        (void)tile_epilogue(FC, std::false_type{}, t + 1, nxt, nxt, pl, ph);
+        (void)tile_epilogue(FC, std::false_type{}, std::false_type{}, t + 1, nxt, nxt, pl, ph, gs);
       }
     };
     if (nlive > 0) {
@@ -801,37 +808,59 @@ indexer_scores_kernel(
     uint8_t *klist = L.klist[wave];
     int nlist = 0;
     // Tiles before the last live one are full (every key in range and before the limit).
-    auto epilogue = [&](auto FC, auto FULL, int t, const f32x4_t(&a)[HT], const f32x4_t(&as)[HT]) {
+    auto epilogue = [&](auto FC, auto FULL, auto PAIR, int t, const f32x4_t(&a)[HT], const f32x4_t(&as)[HT]) {
       uint32_t pl[2 * HT], ph[2 * HT];
-      const uint32_t km = tile_epilogue(FC, FULL, t, a, as, pl, ph);
+      float gs = 0.f;
+      const uint32_t km = tile_epilogue(FC, FULL, PAIR, t, a, as, pl, ph, gs);
       if (km != 0u) {  // wave-uniform
         if (g == 0 && ((km >> l16) & 1u))
           klist[nlist + __builtin_popcount(km & ((1u << l16) - 1u))] = static_cast<uint8_t>(16 * t + l16);
         nlist += __builtin_popcount(km);
       }
+      return gs;
+    };
+    // The scores of tiles t and t + 1 from their lanes' group sums ga, gb: ((G0 + G1) + (G2 + G3)) of both tiles
+    // with one exchange of each kind (combine_groups with two different registers in place of one copied twice):
+    // after the row-pair swap, rows 0 / 2 hold tile t's pair sums and rows 1 / 3 tile t + 1's; after the half swap
+    // row 0 holds tile t's score and row 1 tile t + 1's.  PB: tile t + 1 is the last live tile (key tests).
+    auto store_pair = [&](auto PB, int t, float ga, float gb) {
+      float a = ga, b = gb;
+      asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+      float c = a + b, d = c;
+      asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+      const float tot = c + d;
+      const float outv = WBF ? round_score_bf16(tot) : tot;
+      const int key_l = 16 * (t + (g & 1)) + l16;
+      if constexpr (decltype(PB)::value) {
+        if (g == 0 || (g == 1 && key_l < nk)) orow[kb0 + key_l] = (g == 0 || kb0 + key_l < limit32) ? outv : -INFINITY;
+      } else {
+        if (g < 2) orow[static_cast<uint32_t>(kb0 + key_l)] = outv;
+      }
     };
     const int last = nlive - 1;
     if (nlive > 0 && !forced) {
-      const std::true_type full;
-      const std::false_type fc, partial;
+      const std::true_type full, pair;
+      const std::false_type fc, partial, single;
       tile_mfma(l16, acc, accs);
       int t = 0;
       for (; t + 2 <= last; t += 2) {
         tile_mfma(16 * (t + 1) + l16, nxt, nxts);
-        epilogue(fc, full, t, acc, accs);
+        const float ga = epilogue(fc, full, pair, t, acc, accs);
         tile_mfma(16 * (t + 2) + l16, acc, accs);
-        epilogue(fc, full, t + 1, nxt, nxts);
+        const float gb = epilogue(fc, full, pair, t + 1, nxt, nxts);
+        store_pair(std::false_type{}, t, ga, gb);
       }
       if (t < last) {
         tile_mfma(16 * last + l16, nxt, nxts);
-        epilogue(fc, full, t, acc, accs);
-        epilogue(fc, partial, last, nxt, nxts);
+        const float ga = epilogue(fc, full, pair, t, acc, accs);
+        const float gb = epilogue(fc, partial, pair, last, nxt, nxts);
+        store_pair(std::true_type{}, t, ga, gb);
       } else {
-        epilogue(fc, partial, last, acc, accs);
+        (void)epilogue(fc, partial, single, last, acc, accs);
       }
     } else if (nlive > 0) {
       // a forced wave lists every key (its interval ends are not used)
-      for (int t = 0; t < nlive; ++t) epilogue(std::true_type{}, std::false_type{}, t, acc, accs);
+      for (int t = 0; t < nlive; ++t) (void)epilogue(std::true_type{}, std::false_type{}, std::false_type{}, t, acc, accs);
     }
     // resolution, 16 listed keys at a time: the same MFMAs and interval test on their rows (the same operands, so
     // the same interval ends), all four groups' ends of each key saved as a deferred entry, and the entries'

@@ -63,20 +63,17 @@ __device__ __forceinline__ float dot_halfwidth(float qn, float knm, float bound_
 // normal values, an upper bound for subnormals and zeros), all exact bf16 values or upper bounds.  The chain sums nonnegative products,
 // so its own loss is below 2^-19 of the exact sum over its <= 20 steps (the same model), its operands' subnormal
 // padding adding < 2^-117 (||q|| + ||k||) to that sum.  Then
-//   half-width = step_halfwidth_scale(bound_c, D) * V + step_halfwidth_add(qn, knm, bound_c, D),
+//   half-width = step_halfwidth_scale(bound_r) * V + step_halfwidth_add(qn, knm, bound_r),
 // scale (1 + 2^-6) 2^-24 >= K (1 + 2^-18) with room for the fp32 fma that evaluates it, and an additive part
-// 2^-150 (qn + knm) + 2^-144 over the subnormal terms (< 2^-145.9 + 2^-160 (qn + knm)).  bound_c scales both
-// relative to the derived constant of D (score_bound_c: the derived half-width there; 0 for timing, a large
-// value to force the exact path).  +inf as dot_halfwidth where the norms could overflow the MFMA, and where
+// 2^-150 (qn + knm) + 2^-144 over the subnormal terms (< 2^-145.9 + 2^-160 (qn + knm)).  bound_r = bound_c /
+// score_bound_c(D) scales both relative to the derived constant of D (1: the derived half-width; 0 for timing, a
+// large value to force the exact path; formed by the launch, so no kernel divides).  +inf as dot_halfwidth where the norms could overflow the MFMA, and where
 // qn >= 2^122 (the weighted |q| and 8 A' must stay finite bf16).  Pinned on the MFMA model by the CPU tests
 // (random chains of five families; rows whose every step loses most of its grid, which W alone does not cover).
-__device__ __forceinline__ float step_halfwidth_scale(float bound_c, int D) {
-  return bound_c / score_bound_c(D) * 0x1.04p-24f;
-}
-__device__ __forceinline__ float step_halfwidth_add(float qn, float knm, float bound_c, int D) {
+__device__ __forceinline__ float step_halfwidth_scale(float bound_r) { return bound_r * 0x1.04p-24f; }
+__device__ __forceinline__ float step_halfwidth_add(float qn, float knm, float bound_r) {
   const float p = (qn + 0x1p-122f) * (knm + 0x1p-122f);
-  return p < 0x1p126f && qn < 0x1p122f ? bound_c / score_bound_c(D) * (0x1p-150f * (qn + knm) + 0x1p-144f)
-                                      : __builtin_inff();
+  return p < 0x1p126f && qn < 0x1p122f ? bound_r * (0x1p-150f * (qn + knm) + 0x1p-144f) : __builtin_inff();
 }
 
 // The step weight exponent j(s) = ceil(log2(n + 1 - s)) of step s < n: 2^j >= n + 1 - s.

@@ -8,7 +8,7 @@
 // increasing h with fma (fp32 weights), then (G0 + G1) + (G2 + G3).
 //
 // Work decomposition: a 512-lane workgroup = 8 waves = 8 queries x a block of 256 keys.  The key block is
-// staged once in LDS (64 KiB, zero rows past T) behind the kernel's only barrier; from there each wave runs
+// staged once in LDS (64 KiB; rows past T unused) behind the kernel's only barrier; from there each wave runs
 // independently.  A wave keeps its query's rows in VGPRs as MFMA A-fragments and walks the block in
 // 16-key tiles with v_mfma_f32_16x16x32_bf16 (M = 16 heads, N = 16 keys, 4 k-steps), issuing the next
 // tile's MFMAs before the current tile's epilogue.  LDS rows use a 16-byte XOR swizzle (chunk c of row r
@@ -331,7 +331,7 @@ indexer_scores_kernel(
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
     int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats, int xcd_pk,
     float *__restrict__ bounds, float *__restrict__ kmax, uint32_t *__restrict__ row_counts,
-    const float *__restrict__ ksc) {
+    const float *__restrict__ ksc, float bound_r) {
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
   static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
@@ -394,21 +394,24 @@ indexer_scores_kernel(
   const int kt = tid & (kKR - 1);
   const bool kin = kt < nk;
   const int kst = kin ? kt : nk - 1;  // nk >= 1: the grid covers T with key blocks
-  const float kn_v = kn[krow0 + kst];
-  const int32_t ks_v = ksp[krow0 + kst];
+  // (loads at 32-bit unsigned offsets from workgroup-uniform bases: one address instruction each)
+  const float *__restrict__ knb = kn + krow0;
+  const float kn_v = knb[static_cast<uint32_t>(kst)];
+  const int32_t ks_v = (ksp + krow0)[static_cast<uint32_t>(kst)];
   // every wave reads the whole block's key norms (keys lane + 64 j), so that it forms the block's norm maximum,
   // and with it the interval half-widths, without waiting for the other waves
   float kn4[kKR / 64];
 #pragma unroll
   for (int j = 0; j < kKR / 64; ++j) {
     const int kj = lane + 64 * j;
-    kn4[j] = kn[krow0 + (kj < nk ? kj : nk - 1)];
+    kn4[j] = knb[static_cast<uint32_t>(kj < nk ? kj : nk - 1)];
   }
   const int hl = lane & (H - 1);
-  const int64_t hrow = qrow0 + hl;
-  const float qn_v = qn[hrow];
-  const int32_t qs_v = qsp[hrow];
-  const float w_v = WBF ? bf16_to_f32(static_cast<const uint16_t *>(w)[hrow]) : static_cast<const float *>(w)[hrow];
+  const uint32_t hlu = static_cast<uint32_t>(hl);
+  const float qn_v = (qn + qrow0)[hlu];
+  const int32_t qs_v = (qsp + qrow0)[hlu];
+  const float w_v = WBF ? bf16_to_f32((static_cast<const uint16_t *>(w) + qrow0)[hlu])
+                        : (static_cast<const float *>(w) + qrow0)[hlu];
   constexpr int kKL = kKR * kC / kThreads;  // 16-byte key chunks per thread (F8: kKL / 2 loads of 16 codes)
   constexpr int kKV = F8 ? kKL / 2 : kKL;
   uint4 kv[kKV];
@@ -423,7 +426,7 @@ indexer_scores_kernel(
       ksv[it] = ksc[row];
     } else {
       const int kr = lin / kC, ch = lin % kC;
-      kv[it] = *reinterpret_cast<const uint4 *>(k + (krow0 + (kr < nk ? kr : nk - 1)) * KD + ch * 8);
+      kv[it] = *reinterpret_cast<const uint4 *>(k + krow0 * KD + static_cast<uint32_t>((kr < nk ? kr : nk - 1) * KD + ch * 8));
     }
   }
   // Every wave's key-block loads are queued ahead of every q load: the memory pipeline serves a CU's loads in
@@ -442,7 +445,7 @@ indexer_scores_kernel(
   for (int kk = 0; kk < KD / 32; ++kk)
 #pragma unroll
     for (int m = 0; m < HT; ++m)
-      qa[m][kk] = *reinterpret_cast<const uint4 *>(q + (qrow0 + 16 * m + l16) * KD + 32 * kk + 8 * g);
+      qa[m][kk] = *reinterpret_cast<const uint4 *>(q + qrow0 * KD + static_cast<uint32_t>((16 * m + l16) * KD + 32 * kk + 8 * g));
   auto abs8 = [](uint4 v) {  // |x| of 8 packed bf16
     return make_uint4(v.x & 0x7FFF7FFFu, v.y & 0x7FFF7FFFu, v.z & 0x7FFF7FFFu, v.w & 0x7FFF7FFFu);
   };
@@ -457,10 +460,10 @@ indexer_scores_kernel(
   L.qnorm[wave][hl] = qn_v;
   // per-head data formed once per head (lane h), not by each of the 16 lanes that use it.  PDD (the exact kernel
   // at 16 heads): per-dot half-widths from the MFMA sum of the magnitudes, dl then holds their additive part
-  L.dl[wave][hl] = PDD ? step_halfwidth_add(qn_v, knm, bound_c, KD) : dot_halfwidth(qn_v, knm, bound_c);
+  L.dl[wave][hl] = PDD ? step_halfwidth_add(qn_v, knm, bound_r) : dot_halfwidth(qn_v, knm, bound_c);
   if constexpr (BOUND) L.wup[wave][hl] = bf16_abs_round_up(w_v);
   L.w[wave][hl] = w_v;
-  // the workgroup's whole key block into LDS (zero rows past T)
+  // the workgroup's whole key block into LDS
   if constexpr (F8) {
     // one conversion form for the whole wave: the one-instruction form when every scale it holds allows it
     bool p2 = true;
@@ -484,15 +487,14 @@ indexer_scores_kernel(
     else
       stage(std::false_type{});
   } else {
+    // (rows past T hold copies of the last key, loaded from the clamped row: finite operands whose columns are
+    // neither stored nor listed)
 #pragma unroll
     for (int it = 0; it < kKL; ++it) {
       const int lin = it * kThreads + tid;
       const int kr = lin / kC, ch = lin % kC;
-      // zero rows past T by a mask, not a select: a select lets the compiler move the load behind a branch and
-      // below the barrier that orders the key-block loads before the q loads
-      const uint32_t msk = kr < nk ? 0xFFFFFFFFu : 0u;
-      L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = make_uint4(kv[it].x & msk, kv[it].y & msk, kv[it].z & msk, kv[it].w & msk);
-      if constexpr (PDD) L.kstep[kr][ch] = static_cast<uint16_t>(step_exponent_pow2(kv[it]) & msk);
+      L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = kv[it];
+      if constexpr (PDD) L.kstep[kr][ch] = static_cast<uint16_t>(step_exponent_pow2(kv[it]));
     }
   }
   if constexpr (COUNT) {  // this wave's lower-end counts start at zero
@@ -632,7 +634,7 @@ indexer_scores_kernel(
       for (int m = 0; m < HT; ++m) acc[m] = mfma16(qa[m][kk], bv[kk], acc[m]);
   };
 
-  const float dsc = PDD ? step_halfwidth_scale(bound_c, KD) : 0.f;
+  const float dsc = PDD ? step_halfwidth_scale(bound_r) : 0.f;
   // the exact kernel's interval test (the tile epilogue's, below) on the 16 keys of a resolution round: pl, ph and the
   // ballot of the lanes holding a near-tie dot.  (The tile epilogue keeps its own copy: sharing this lambda with
   // the bound kernels' epilogue made the compiler spill registers in their tile loop.)
@@ -735,7 +737,7 @@ indexer_scores_kernel(
       outv = WBF ? round_score_bf16(tot) : tot;
       if (g == 0 && kvalid) orow[key] = (full || key < limit32) ? outv : -INFINITY;
     }
-    // keys past T are zero rows and, in the exact kernel, keys past the causal limit are -inf: neither is deferred
+    // keys past T are not stored and, in the exact kernel, keys past the causal limit are -inf: neither is deferred
     // (the bound kernel stores bound 0 past the limit, below)
     if constexpr (!full) anyr &= __builtin_amdgcn_ballot_w64(BOUND ? kvalid : (kvalid && key < limit32));
     const uint32_t km = key_mask(anyr);
@@ -926,6 +928,7 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
                      float *bounds, float *kmax, uint32_t *row_counts, const float *ksc, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
+  const float bound_r = bound_c / score_bound_c(KD);  // the per-dot half-widths' scale (16-head exact kernel)
   // XCD tiling (Pq x Pk = 8) that minimises the L2 fills: each query group's rows are read by Pk XCDs,
   // each key block by Pq; 0 keeps the launch order (slice not a multiple of 8 or no tiling divides it)
   int xcd_pk = 0;
@@ -951,11 +954,11 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
       if (row_counts != nullptr) {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, true, true>), grid, dim3(kThreads), 0, stream, q,
                            k, w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio,
-                           bound_c, stats, xcd_pk, bounds, kmax, row_counts, ksc);
+                           bound_c, stats, xcd_pk, bounds, kmax, row_counts, ksc, bound_r);
       } else {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, false, true>), grid, dim3(kThreads), 0, stream,
                            q, k, w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio,
-                           bound_c, stats, xcd_pk, bounds, kmax, nullptr, ksc);
+                           bound_c, stats, xcd_pk, bounds, kmax, nullptr, ksc, bound_r);
       }
     } else {
       return fail(KS_ERR_INVALID, "indexer scores: FP8 keys need H = 64 and D = 128");
@@ -967,11 +970,11 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
       if (row_counts != nullptr) {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, true>), grid, dim3(kThreads), 0, stream, q, k, w,
                            qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
-                           stats, xcd_pk, bounds, kmax, row_counts, nullptr);
+                           stats, xcd_pk, bounds, kmax, row_counts, nullptr, bound_r);
       } else {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, false>), grid, dim3(kThreads), 0, stream, q, k,
                            w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
-                           stats, xcd_pk, bounds, kmax, nullptr, nullptr);
+                           stats, xcd_pk, bounds, kmax, nullptr, nullptr, bound_r);
       }
     } else {
       return fail(KS_ERR_INVALID, "indexer scores: score bounds need H = 64");
@@ -979,11 +982,11 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
   } else if (w_bf16) {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp,
                        kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk,
-                       nullptr, nullptr, nullptr, nullptr);
+                       nullptr, nullptr, nullptr, nullptr, bound_r);
   } else {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn,
                        qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats,
-                       xcd_pk, nullptr, nullptr, nullptr, nullptr);
+                       xcd_pk, nullptr, nullptr, nullptr, nullptr, bound_r);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;

@@ -487,13 +487,17 @@ indexer_scores_kernel(
     else
       stage(std::false_type{});
   } else {
-    // (rows past T hold copies of the last key, loaded from the clamped row: finite operands whose columns are
-    // neither stored nor listed)
+    // Rows past T hold copies of the last key, loaded from the clamped row: finite operands whose columns are
+    // neither stored nor listed.  The 32- and 64-head kernels still zero them: with the loaded values used only by
+    // the LDS stores, the compiler sinks their loads below the q loads (and the load-ordering barrier above),
+    // which the mask's use of them prevents (a CPU test checks the placement in the compiled code).
+    constexpr bool kMask = HT > 1;
 #pragma unroll
     for (int it = 0; it < kKL; ++it) {
       const int lin = it * kThreads + tid;
       const int kr = lin / kC, ch = lin % kC;
-      L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = kv[it];
+      const uint32_t msk = (!kMask || kr < nk) ? 0xFFFFFFFFu : 0u;
+      L.k[kr * kC + (ch ^ (kr & (kC - 1)))] = make_uint4(kv[it].x & msk, kv[it].y & msk, kv[it].z & msk, kv[it].w & msk);
       if constexpr (PDD) L.kstep[kr][ch] = static_cast<uint16_t>(step_exponent_pow2(kv[it]));
     }
   }

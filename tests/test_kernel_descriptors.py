@@ -13,6 +13,12 @@ LDS-fed MFMA) also waits for them: one pointer rebuilt from an integer, which th
 turned a sparse-attention kernel's index prefetch into flat loads that stalled each chunk's LDS reads.  The
 same compile checks that no kernel contains a flat memory instruction.
 
+The score kernels issue their key-block loads before a barrier that orders them ahead of every wave's q loads (a
+CU serves its loads in issue order, so waves whose key-block share queued behind the other waves' q rows would
+hold up the block's staging).  Whether the compiler keeps the loads there depends on how their values are used:
+with the values feeding only LDS stores it sank them below the q loads, and the 64-head bound kernel went from 60
+to 64 us at config 4.  The same compile checks that the loads precede the barrier.
+
 Some kernels' speed rests on their register, scratch and LDS budgets, which a small source change can break
 silently (a lambda shared between two epilogues made the bound score kernel's tile loop reload spilled registers
 every iteration: config 4's score kernel went from 61 to 76 us).  The same compile checks those budgets."""
@@ -122,6 +128,45 @@ def test_no_dispatch_packet_reads_or_flat_memory(compiled):
            for k in dispatch_ptr_kernels(asm)]
     bad += [f"{os.path.basename(src)}: {k} (flat memory instruction)" for src, asm in compiled.items()
             for k in flat_memory_kernels(asm)]
+    assert bad == [], "\n".join(bad)
+
+
+def loads_before_first_barrier(asm: str):
+    """{kernel name: 16-byte global loads ahead of the kernel's first s_barrier}."""
+    out = {}
+    for m in re.finditer(r"^(\w+):[^\n]*\n(.*?)^\.Lfunc_end", asm, re.S | re.M):
+        body = m.group(2)
+        cut = re.search(r"^\s+s_barrier\b", body, re.M)
+        if cut is not None:
+            out[m.group(1)] = len(re.findall(r"^\s+global_load_dwordx4\b", body[:cut.start()], re.M))
+    return out
+
+
+def test_checker_pins_load_order():
+    code = ("_Za:\n\tglobal_load_dwordx4 v[0:3], v[4:5], off\n\tglobal_load_dword v6, v[4:5], off\n\ts_barrier\n"
+            "\tglobal_load_dwordx4 v[0:3], v[4:5], off\n.Lfunc_end0:\n"
+            "_Zb:\n\ts_barrier\n\tglobal_load_dwordx4 v[0:3], v[4:5], off\n.Lfunc_end1:\n")
+    assert loads_before_first_barrier(code) == {"_Za": 1, "_Zb": 0}
+
+
+# (mangled-name fragment, 16-byte key-block loads per thread that must precede the first barrier)
+LOAD_ORDER = [
+    ("indexer_scores_kernelILi4ELi128ELb0ELb1ELb0ELb0E", 8),  # bound, config 4
+    ("indexer_scores_kernelILi4ELi128ELb0ELb1ELb1ELb0E", 8),  # bound and counting, config 2
+    ("indexer_scores_kernelILi4ELi128ELb0ELb0ELb0ELb0E", 8),  # exact, 64 heads
+    ("indexer_scores_kernelILi1ELi64ELb1ELb0ELb0ELb0E", 4),   # exact, the drop-in shape
+]
+
+
+def test_key_block_loads_precede_the_ordering_barrier(compiled):
+    found = {}
+    for asm in compiled.values():
+        found.update(loads_before_first_barrier(asm))
+    bad = []
+    for frag, n in LOAD_ORDER:
+        hits = [(k, v) for k, v in found.items() if frag in k]
+        assert hits, f"no kernel matches {frag}"
+        bad += [f"{k}: {v} key-block loads before the barrier, {n} expected" for k, v in hits if v < n]
     assert bad == [], "\n".join(bad)
 
 

@@ -171,16 +171,43 @@ __device__ __forceinline__ void chunk_stats(uint4 v, float &ss, int &lsb) {
   }
 }
 
-// Sum and minimum over the CPR lanes of a row (CPR in {8, 16}: an aligned lane group) with DPP exchanges.
-template <int CPR>
+// The same statistics with the LSB exponent taken from the smallest nonzero magnitude: mmin accumulates, as packed
+// 16-bit halves, the magnitudes minus one (a zero wraps to 0xFFFF and drops out of the minimum); magnitudes order
+// like their exponent fields, so the smallest nonzero one carries the smallest exponent.  Fold with lsb_of_min.
+__device__ __forceinline__ void chunk_stats_packed(uint4 v, float &ss, uint32_t &mmin) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  u16x2 acc = __builtin_bit_cast(u16x2, mmin);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float lo = bf16_to_f32(static_cast<uint16_t>(w[p] & 0xFFFFu));
+    const float hi = bf16_to_f32(static_cast<uint16_t>(w[p] >> 16));
+    ss = __builtin_fmaf(lo, lo, ss);  // a bound (the norm is rounded up by 2^-12 at the end): any order
+    ss = __builtin_fmaf(hi, hi, ss);
+    const u16x2 m = __builtin_bit_cast(u16x2, w[p] & 0x7FFF7FFFu) - u16x2{1, 1};
+    acc = __builtin_elementwise_min(acc, m);
+  }
+  mmin = __builtin_bit_cast(uint32_t, acc);
+}
+// The smallest LSB exponent (bf16_lsb_exponent) of the nonzero elements accumulated in mmin; 1 << 20 if none.
+__device__ __forceinline__ int lsb_of_min(uint32_t mmin) {
+  const uint32_t m1 = min(mmin & 0xFFFFu, mmin >> 16);
+  return m1 == 0xFFFFu ? (1 << 20) : max(static_cast<int>((m1 + 1u) >> 7), 1) - 134;
+}
+
+// Sum and minimum over the N lanes of a row (N in {4, 8, 16}: an aligned lane group) with DPP exchanges.
+template <int N>
 __device__ __forceinline__ void row_reduce(float &ss, int &lsb) {
+  static_assert(N == 4 || N == 8 || N == 16, "row lanes");
 #define KS_STEP(S)                                                                 \
   ss += __builtin_bit_cast(float, lane_xor<S>(__builtin_bit_cast(uint32_t, ss)));  \
   lsb = min(lsb, static_cast<int>(lane_xor<S>(static_cast<uint32_t>(lsb))));
   KS_STEP(1)
   KS_STEP(2)
-  KS_STEP(4)
-  if constexpr (CPR == 16) {
+  if constexpr (N >= 8) {
+    KS_STEP(4)
+  }
+  if constexpr (N == 16) {
     KS_STEP(8)
   }
 #undef KS_STEP

@@ -6,9 +6,10 @@
 // bf16 (RNE).  Canonical order: y0 = fl(x0*c) - fl(x1*s), y1 = fl(x0*s) + fl(x1*c) (the library is built
 // with -ffp-contract=off, so the products are rounded separately, exactly like the CPU oracle).
 //
-// Each lane owns 8 consecutive elements (one 16-byte load and store), so a row of D = 128 is 16 lanes and
-// a wave covers 4 rows with fully coalesced accesses.  In stats mode the D/8 lanes of a row also reduce
-// the row's squared norm and its smallest nonzero-element LSB exponent:
+// A lane owns 16-byte chunks of 8 consecutive elements: one in the generic form; two of one row in stats mode
+// (chunks j and j + D/16 of the row's D/16 lanes, so a wave's loads and stores cover whole rows, coalesced).  In
+// stats mode the lanes of a row also reduce the row's squared norm and its smallest nonzero-element LSB
+// exponent:
 //   norm  >= ||row||_2 (rounded up),   span = ceil(log2 norm) - min_lsb_exponent.
 // The score kernel uses norm for its MFMA error bound and span to prove that a double-precision
 // recomputation of a dot product is exact.
@@ -46,15 +47,19 @@ RowJobK kernel_job(const RowJob &j) {
   return k;
 }
 
-// One thread per 16-byte chunk; blocks [0, blocks0) take job 0 and the rest job 1 (a uniform choice, so
-// each field is selected separately from the kernel arguments, never through a pointer to them).
-// CPR: chunks per row, 8 or 16 with statistics (0: any D, no statistics).  The grid's threads also clear
+// Threads own 16-byte chunks: one each in the generic form (CPR 0: any D, no statistics), two of the same row in
+// the statistics forms (CPR = chunks per row, 8 or 16: lane j of the row's CPR / 2 lanes holds chunks j and
+// j + CPR / 2), so that the row and position arithmetic, the statistics' final steps and the weight scaling are
+// shared by twice the bytes.  Blocks [0, blocks0) take job 0 and the rest job 1 (a uniform choice, so each field is
+// selected separately from the kernel arguments, never through a pointer to them).  The grid's threads also clear
 // zero16 16-byte words at zero (grid-strided).
 template <int CPR>
 __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, uint32_t blocks0,
                                                        const float *__restrict__ freqs, int D, FastDiv cpr,
                                                        int rope_start, uint4 *__restrict__ zero, uint32_t zero16,
                                                        WeightScale wsc) {
+  constexpr int NC = CPR == 0 ? 1 : 2;  // chunks per thread
+  constexpr int LPR = CPR / NC;         // lanes per row (statistics forms)
   const bool second = blockIdx.x >= blocks0;
 #define KS_PICK(f) (second ? j1.f : j0.f)
   const uint16_t *__restrict__ src = KS_PICK(src);
@@ -72,28 +77,48 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, 
     row = cpr.div(c);
     j = c - row * cpr.d;
   } else {
-    row = c / CPR;  // power of two: a shift
-    j = c % CPR;
+    row = c / LPR;  // powers of two: shifts
+    j = c % LPR;
   }
   const bool live = row < rows;
   const uint32_t rb = live ? rpb.div(row) : 0, rr = live ? row - rb * rpb.d : 0;
   const int64_t srow = static_cast<int64_t>(rb) * sbr + rr;
-  uint4 v = make_uint4(0, 0, 0, 0);
-  if (live) v = *reinterpret_cast<const uint4 *>(src + srow * D + 8 * j);
-  const int e0 = 8 * static_cast<int>(j);
-  if (live && rope_dim > 0 && e0 >= rope_start && e0 < rope_start + rope_dim) {
+  // both chunks' loads go out before any use
+  uint4 v[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    v[i] = make_uint4(0, 0, 0, 0);
+    if (live) v[i] = *reinterpret_cast<const uint4 *>(src + srow * D + 8 * (j + i * LPR));
+  }
+  bool any_rot = false;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int e0 = 8 * static_cast<int>(j + i * LPR);
+    any_rot = any_rot || (rope_dim > 0 && e0 >= rope_start && e0 < rope_start + rope_dim);
+  }
+  if (live && any_rot) {
     const uint32_t t = Hd.div(rr);
     const int64_t pos = pos0 + (t - Sd.div(t) * Sd.d);
-    const float2 *cs = reinterpret_cast<const float2 *>(freqs) + pos * (rope_dim / 2) + (e0 - rope_start) / 2;
-    v = rope_chunk(v, cs);
+    const float2 *cs0 = reinterpret_cast<const float2 *>(freqs) + pos * (rope_dim / 2);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int e0 = 8 * static_cast<int>(j + i * LPR);
+      if (e0 >= rope_start && e0 < rope_start + rope_dim) v[i] = rope_chunk(v[i], cs0 + (e0 - rope_start) / 2);
+    }
   }
-  if (live && dst != nullptr) *reinterpret_cast<uint4 *>(dst + static_cast<int64_t>(row) * D + 8 * j) = v;
+  if (live && dst != nullptr) {
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+      *reinterpret_cast<uint4 *>(dst + static_cast<int64_t>(row) * D + 8 * (j + i * LPR)) = v[i];
+  }
   if constexpr (CPR != 0) {
-    // the CPR lanes of a row are an aligned group of the wave
+    // the LPR lanes of a row are an aligned group of the wave
     float ss = 0.f;
-    int lsb = 1 << 20;
-    chunk_stats(v, ss, lsb);
-    row_reduce<CPR>(ss, lsb);
+    uint32_t mmin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) chunk_stats_packed(v[i], ss, mmin);
+    int lsb = lsb_of_min(mmin);
+    row_reduce<LPR>(ss, lsb);
     if (live && j == 0) {
       float *norm = second ? j1.norm : j0.norm;
       int32_t *span = second ? j1.span : j0.span;
@@ -119,7 +144,9 @@ int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs,
                      hipStream_t stream, void *zero, int64_t zero16, const WeightScale *wscale) {
   KS_CHECK_ARG(zero16 >= 0 && zero16 < (int64_t(1) << 31) && (zero16 == 0 || aligned(zero, 16)),
                "rope rows: clear range of %lld words", (long long)zero16);
-  const int64_t c0 = job0.rows * (D / 8), c1 = job1.rows * (D / 8);
+  const bool stats = job0.norm != nullptr;
+  const int64_t tpr = stats ? D / 16 : D / 8;  // threads per row: two chunks each with statistics, else one
+  const int64_t c0 = job0.rows * tpr, c1 = job1.rows * tpr;
   KS_CHECK_ARG(c0 + c1 + 512 < (int64_t(1) << 31), "rope rows: %lld + %lld chunks exceed the 32-bit grid",
                (long long)c0, (long long)c1);
   KS_CHECK_ARG(job0.rows_per_batch >= 1 && job1.rows_per_batch >= 1 && job0.H >= 1 && job1.H >= 1 &&
@@ -130,7 +157,6 @@ int launch_rope_rows(const RowJob &job0, const RowJob &job1, const float *freqs,
   const int64_t b0 = ceil_div(c0, 256), b1 = ceil_div(c1, 256);
   KS_CHECK_ARG(b0 + b1 > 0 || zero16 == 0, "rope rows: a clear range needs rows");
   if (b0 + b1 == 0) return KS_OK;
-  const bool stats = job0.norm != nullptr;
   KS_CHECK_ARG((job1.rows == 0 || (job1.norm != nullptr) == stats) && (!stats || D == 64 || D == 128),
                "rope rows: statistics need D in {64, 128} and both jobs alike");
   const dim3 grid(static_cast<unsigned>(b0 + b1));

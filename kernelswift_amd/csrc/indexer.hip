@@ -113,7 +113,8 @@ struct Fp8Direct {
 int indexer_select(const char *fn, const IndexerWs &ws, const void *w, int32_t w_bf16, int64_t k_top, int32_t causal,
                    int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64, int64_t B, int64_t S,
                    int64_t H, int64_t D, int64_t T, hipStream_t st, float bound_c, uint32_t *stats, int path,
-                   const Fp8Direct &f8 = Fp8Direct{}) {
+                   const Fp8Direct &f8 = Fp8Direct{}, const uint16_t *q_unrot = nullptr, int rot_lo = 0,
+                   int rot_hi = 0) {
   const int64_t kk = k_top < T ? k_top : T;
   const bool can_bound = takes_bounded(k_top, w_bf16, H, D, T, 0);
   KS_CHECK_ARG(path < 2 || can_bound,
@@ -137,8 +138,13 @@ int indexer_select(const char *fn, const IndexerWs &ws, const void *w, int32_t w
     return ks::launch_indexer_topk_bounded(ws.scores, T, B, S, T, kk, causal ? 1 : 0, start_pos, ratio, offset, out,
                                            out_i64 ? 1 : 0, trc, st);
   }
-  rc = ks::launch_indexer_scores(ws.q_rot, ws.k_rot, w, w_bf16 ? 1 : 0, ws.q_norm, ws.q_span, ws.k_norm, ws.k_span,
-                                 ws.scores, B, S, H, D, T, T, causal ? 1 : 0, start_pos, ratio, bound_c, stats, st);
+  // q_unrot: the caller's q rows, whose dims outside [rot_lo, rot_hi) the row preparation did not copy (ws.q_rot
+  // then holds only the rotated dims; rot_lo == rot_hi: nothing rotated, all of q from the caller's rows)
+  const ks::QSplit qs{rot_hi > rot_lo ? ws.q_rot : nullptr, rot_lo, rot_hi};
+  rc = ks::launch_indexer_scores(q_unrot != nullptr ? q_unrot : ws.q_rot, ws.k_rot, w, w_bf16 ? 1 : 0, ws.q_norm,
+                                 ws.q_span, ws.k_norm, ws.k_span, ws.scores, B, S, H, D, T, T, causal ? 1 : 0,
+                                 start_pos, ratio, bound_c, stats, st, nullptr, nullptr, nullptr, nullptr,
+                                 q_unrot != nullptr ? &qs : nullptr);
   if (rc != KS_OK) return rc;
   return ks_indexer_topk(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, st);
 }
@@ -169,9 +175,13 @@ int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int rd = static_cast<int>(rope_dim);
   // q rows at positions start_pos + s; k rows of every batch (stride k_batch_stride) at positions t
-  const ks::RowJob qjob{q, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H, H, S, start_pos, rd};
-  const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
   const bool bounded = takes_bounded(k_top, w_bf16, H, D, T, path);
+  // the exact path with a 32-aligned rotated range (or none) reads q's other dims from the caller's rows, so the row
+  // preparation writes only the rotated dims of q (half of q's bytes at the drop-in indexer's shape)
+  const bool split = !bounded && rope_start % 32 == 0 && rd % 32 == 0;
+  ks::RowJob qjob{q, ws.q_rot, ws.q_norm, ws.q_span, B * S * H, B * S * H, B * S * H, H, S, start_pos, rd};
+  qjob.rotated_only = split ? 1 : 0;
+  const ks::RowJob kjob{k, ws.k_rot, ws.k_norm, ws.k_span, B * T, T, k_batch_stride, 1, T, 0, rope_k ? rd : 0};
   // w_scale != 1: the row preparation also writes the scaled weights (one per q row), which the later launches read
   const bool scaled = w_scale != 1.0f;
   const ks::WeightScale wsc{w, ws.w_scaled, w_scale, w_bf16 ? 1 : 0};
@@ -180,7 +190,8 @@ int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_
                             bounded ? count_words16(ws, B, S, T) : 0, scaled ? &wsc : nullptr);
   if (rc != KS_OK) return rc;
   return indexer_select("ks_indexer", ws, scaled ? ws.w_scaled : w, w_bf16, k_top, causal, start_pos, ratio, offset,
-                        out, out_i64, B, S, H, D, T, st, bound_c, stats, path);
+                        out, out_i64, B, S, H, D, T, st, bound_c, stats, path, Fp8Direct{}, split ? q : nullptr,
+                        static_cast<int>(rope_start), static_cast<int>(rope_start) + rd);
 }
 
 int indexer_fp8_impl(const uint8_t *q, const float *q_scale, const uint8_t *k, const float *k_scale, const void *w,

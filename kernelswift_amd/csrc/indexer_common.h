@@ -250,6 +250,7 @@ struct RowJob {
   int64_t rows, rows_per_batch, src_batch_rows;
   int64_t H, S, pos0;
   int rope_dim;  // 0: copy / statistics only
+  int rotated_only = 0;  // 1: dst receives only the chunks of the rotated dims (the others stay unwritten)
 };
 
 // Both jobs in one launch (job1.rows may be 0); rows of D in {64, 128} for statistics, any multiple of 8
@@ -302,11 +303,19 @@ constexpr int kScoreKeyBlock = 256;
 // by the selection's own histogram launch instead.
 constexpr int64_t kScoreCountGrid = 256;
 bool scores_count_rows(int64_t B, int64_t S, int64_t T);
+// q rows split over two buffers (the exact path when the row preparation wrote only the rotated dims): dims
+// [lo, hi) (32-aligned) from rot, the others from the q argument; rot == nullptr: all of q from the argument.
+struct QSplit {
+  const uint16_t *rot;
+  int lo, hi;
+};
+
 int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
                           int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds = nullptr,
-                          float *kmax = nullptr, uint32_t *row_counts = nullptr, const float *ksc = nullptr);
+                          float *kmax = nullptr, uint32_t *row_counts = nullptr, const float *ksc = nullptr,
+                          const QSplit *qsplit = nullptr);
 
 // Sorted exact top-k of rows of bounded scores (the bound-emitting score kernel's output): a threshold from the
 // lower ends, exact recomputation of the scores that may reach the top k (interval test with the score kernel's

@@ -28,6 +28,7 @@ struct RowJobK {
   int64_t src_batch_rows, pos0;
   uint32_t rows;
   int rope_dim;
+  int rotated_only;
   FastDiv rpb, H, S;
 };
 
@@ -41,6 +42,7 @@ RowJobK kernel_job(const RowJob &j) {
   k.pos0 = j.pos0;
   k.rows = static_cast<uint32_t>(j.rows);
   k.rope_dim = j.rope_dim;
+  k.rotated_only = j.rotated_only;
   k.rpb = FastDiv(static_cast<uint32_t>(j.rows_per_batch));
   k.H = FastDiv(static_cast<uint32_t>(j.H));
   k.S = FastDiv(static_cast<uint32_t>(j.S));
@@ -68,6 +70,7 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, 
   const int64_t sbr = KS_PICK(src_batch_rows);
   const int64_t pos0 = KS_PICK(pos0);
   const int rope_dim = KS_PICK(rope_dim);
+  const bool rotated_only = KS_PICK(rotated_only) != 0;
   const FastDiv rpb = KS_PICK(rpb), Hd = KS_PICK(H), Sd = KS_PICK(S);
 #undef KS_PICK
   const uint32_t blk = second ? blockIdx.x - blocks0 : blockIdx.x;
@@ -108,8 +111,11 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RowJobK j0, RowJobK j1, 
   }
   if (live && dst != nullptr) {
 #pragma unroll
-    for (int i = 0; i < NC; ++i)
-      *reinterpret_cast<uint4 *>(dst + static_cast<int64_t>(row) * D + 8 * (j + i * LPR)) = v[i];
+    for (int i = 0; i < NC; ++i) {
+      const int e0 = 8 * static_cast<int>(j + i * LPR);
+      if (!rotated_only || (e0 >= rope_start && e0 < rope_start + rope_dim))
+        *reinterpret_cast<uint4 *>(dst + static_cast<int64_t>(row) * D + e0) = v[i];
+    }
   }
   if constexpr (CPR != 0) {
     // the LPR lanes of a row are an aligned group of the wave

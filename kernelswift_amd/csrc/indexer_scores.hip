@@ -147,7 +147,7 @@ __device__ __forceinline__ uint32_t entry_mask(const KeyEntry<HT> &en, int gg) {
 template <int HT, int KD, bool WBF>
 __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
                               const uint4 (&qa)[HT][KD / 32], int64_t qrow0, float *orow, int64_t limit, int T, int kb0,
-                              const float (&wv)[HT][4], uint32_t &n_exact, uint32_t &n_unres) {
+                              const float (&wv)[HT][4], uint32_t &n_exact, uint32_t &n_unres, QSplit qsp) {
   KeyEntry<HT> *E = L.ent[wave];
   uint32_t *D = L.dots[wave];
   const int g = lane >> 4, l16 = lane & 15;
@@ -203,6 +203,9 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
       // 16-byte chunks 4c + sub, which lane h + 16 sub holds as its A-fragment qa[0][c] (read with ds_bpermute);
       // more heads: the chunks kLC sub + c, read from global memory (L2-resident).
       const uint32_t dcur = D[min(b0 + dq, nd - 1)];
+      // the q rows this lane reads from memory: its quarter (elements KD/4 sub ..) lies wholly on one side of a
+      // split (QSplit boundaries are 32-aligned)
+      const uint16_t *qsrc = (qsp.rot != nullptr && (KD / 4) * sub >= qsp.lo && (KD / 4) * sub < qsp.hi) ? qsp.rot : q;
       const int h = static_cast<int>(dcur >> 24), kl = static_cast<int>((dcur >> 16) & 255u);
       uint4 qcur[kLC], kcur[kLC];
       if constexpr (HT == 1) {
@@ -214,7 +217,7 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
           kcur[c] = L.k[kl * kC + ((4 * c + sub) ^ (kl & (kC - 1)))];
         }
       } else {
-        const uint4 *qp = reinterpret_cast<const uint4 *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
+        const uint4 *qp = reinterpret_cast<const uint4 *>(qsrc + (qrow0 + h) * KD + (KD / 4) * sub);
 #pragma unroll
         for (int c = 0; c < kLC; ++c) qcur[c] = qp[c];
 #pragma unroll
@@ -252,7 +255,7 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
         const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
         double hi = 0.0, lo = 0.0;
         // rare path, kept register-light: one dword of q and k per step, re-read from memory
-        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(q + (qrow0 + h) * KD + (KD / 4) * sub);
+        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qsrc + (qrow0 + h) * KD + (KD / 4) * sub);
 #pragma unroll 1
         for (int j = 0; j < 4 * kLC; ++j) {
           const uint32_t qw = q32[j];
@@ -267,7 +270,7 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
       }
       if (scur > 84) {
         // wider still (the whole quad takes this branch): the integer accumulator, any range
-        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(q + (qrow0 + h) * KD);
+        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qsrc + (qrow0 + h) * KD);  // part `sub` of it
         r = exact_dot_wide_bf16<KD, 4>(
             [&](int j) { return q32[j]; },
             [&](int j) {
@@ -331,7 +334,8 @@ indexer_scores_kernel(
     const int32_t *__restrict__ ksp, float *__restrict__ scores, int64_t S, int T, int64_t kbs, int causal,
     int64_t start_pos, int ratio, float bound_c, uint32_t *__restrict__ stats, int xcd_pk,
     float *__restrict__ bounds, float *__restrict__ kmax, uint32_t *__restrict__ row_counts,
-    const float *__restrict__ ksc, float bound_r) {
+    const float *__restrict__ ksc, float bound_r, const uint16_t *__restrict__ qsplit_rot, int qsplit_lo,
+    int qsplit_hi) {
   constexpr int H = HT * 16;
   constexpr int kC = KD / 8;  // 16-byte chunks per key row
   static_assert(!BOUND || (HT == 4 && !WBF), "the bound-emitting variant is built for 64 heads, fp32 weights");
@@ -445,7 +449,12 @@ indexer_scores_kernel(
   for (int kk = 0; kk < KD / 32; ++kk)
 #pragma unroll
     for (int m = 0; m < HT; ++m)
-      qa[m][kk] = *reinterpret_cast<const uint4 *>(q + qrow0 * KD + static_cast<uint32_t>((16 * m + l16) * KD + 32 * kk + 8 * g));
+    {
+      // (the exact kernel may read its q rows from two buffers, QSplit: the rotated dims from qsplit_rot)
+      const uint16_t *qsrc =
+          (!BOUND && qsplit_rot != nullptr && 32 * kk >= qsplit_lo && 32 * kk < qsplit_hi) ? qsplit_rot : q;
+      qa[m][kk] = *reinterpret_cast<const uint4 *>(qsrc + qrow0 * KD + static_cast<uint32_t>((16 * m + l16) * KD + 32 * kk + 8 * g));
+    }
   auto abs8 = [](uint4 v) {  // |x| of 8 packed bf16
     return make_uint4(v.x & 0x7FFF7FFFu, v.y & 0x7FFF7FFFu, v.z & 0x7FFF7FFFu, v.w & 0x7FFF7FFFu);
   };
@@ -895,7 +904,8 @@ indexer_scores_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (nent > 0)
-          flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qa, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres);
+          flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qa, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres,
+                                     QSplit{qsplit_rot, qsplit_lo, qsplit_hi});
         nent = 0;
       }
     }
@@ -929,7 +939,9 @@ template <int HT, int KD>
 int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_bf16, const float *qn,
                      const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                      int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c, uint32_t *stats,
-                     float *bounds, float *kmax, uint32_t *row_counts, const float *ksc, hipStream_t stream) {
+                     float *bounds, float *kmax, uint32_t *row_counts, const float *ksc, hipStream_t stream,
+                     const QSplit *qsplit) {
+  const QSplit qs = qsplit != nullptr ? *qsplit : QSplit{nullptr, 0, 0};
   dim3 grid(static_cast<unsigned>(ceil_div(T, kKR)), static_cast<unsigned>(ceil_div(S, kQW)),
             static_cast<unsigned>(B));
   const float bound_r = bound_c / score_bound_c(KD);  // the per-dot half-widths' scale (16-head exact kernel)
@@ -958,11 +970,11 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
       if (row_counts != nullptr) {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, true, true>), grid, dim3(kThreads), 0, stream, q,
                            k, w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio,
-                           bound_c, stats, xcd_pk, bounds, kmax, row_counts, ksc, bound_r);
+                           bound_c, stats, xcd_pk, bounds, kmax, row_counts, ksc, bound_r, qs.rot, qs.lo, qs.hi);
       } else {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, false, true>), grid, dim3(kThreads), 0, stream,
                            q, k, w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio,
-                           bound_c, stats, xcd_pk, bounds, kmax, nullptr, ksc, bound_r);
+                           bound_c, stats, xcd_pk, bounds, kmax, nullptr, ksc, bound_r, qs.rot, qs.lo, qs.hi);
       }
     } else {
       return fail(KS_ERR_INVALID, "indexer scores: FP8 keys need H = 64 and D = 128");
@@ -974,11 +986,11 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
       if (row_counts != nullptr) {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, true>), grid, dim3(kThreads), 0, stream, q, k, w,
                            qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
-                           stats, xcd_pk, bounds, kmax, row_counts, nullptr, bound_r);
+                           stats, xcd_pk, bounds, kmax, row_counts, nullptr, bound_r, qs.rot, qs.lo, qs.hi);
       } else {
         hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, true, false>), grid, dim3(kThreads), 0, stream, q, k,
                            w, qn, qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c,
-                           stats, xcd_pk, bounds, kmax, nullptr, nullptr, bound_r);
+                           stats, xcd_pk, bounds, kmax, nullptr, nullptr, bound_r, qs.rot, qs.lo, qs.hi);
       }
     } else {
       return fail(KS_ERR_INVALID, "indexer scores: score bounds need H = 64");
@@ -986,11 +998,11 @@ int launch_scores_ht(const uint16_t *q, const uint16_t *k, const void *w, int w_
   } else if (w_bf16) {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, true, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn, qsp,
                        kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats, xcd_pk,
-                       nullptr, nullptr, nullptr, nullptr, bound_r);
+                       nullptr, nullptr, nullptr, nullptr, bound_r, qs.rot, qs.lo, qs.hi);
   } else {
     hipLaunchKernelGGL((indexer_scores_kernel<HT, KD, false, false>), grid, dim3(kThreads), 0, stream, q, k, w, qn,
                        qsp, kn, ksp, scores, S, static_cast<int>(T), kbs, causal, start_pos, ratio, bound_c, stats,
-                       xcd_pk, nullptr, nullptr, nullptr, nullptr, bound_r);
+                       xcd_pk, nullptr, nullptr, nullptr, nullptr, bound_r, qs.rot, qs.lo, qs.hi);
   }
   KS_CHECK_LAUNCH("indexer_scores_kernel");
   return KS_OK;
@@ -1001,17 +1013,17 @@ int launch_scores_d(const uint16_t *q, const uint16_t *k, const void *w, int w_b
                     const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B, int64_t S,
                     int64_t H, int64_t T, int64_t kbs, int causal, int64_t start_pos, int ratio, float bound_c,
                     uint32_t *stats, float *bounds, float *kmax, uint32_t *row_counts, const float *ksc,
-                    hipStream_t stream) {
+                    hipStream_t stream, const QSplit *qsplit) {
   switch (H) {
     case 16:
       return launch_scores_ht<1, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream, qsplit);
     case 32:
       return launch_scores_ht<2, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream, qsplit);
     case 64:
       return launch_scores_ht<4, KD>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, T, kbs, causal, start_pos,
-                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream);
+                                     ratio, bound_c, stats, bounds, kmax, row_counts, ksc, stream, qsplit);
     default:
       return fail(KS_ERR_INVALID, "indexer scores: H=%lld, supported: 16, 32, 64", (long long)H);
   }
@@ -1027,13 +1039,13 @@ int launch_indexer_scores(const uint16_t *q, const uint16_t *k, const void *w, i
                           const int32_t *qsp, const float *kn, const int32_t *ksp, float *scores, int64_t B,
                           int64_t S, int64_t H, int64_t D, int64_t T, int64_t kbs, int causal, int64_t start_pos,
                           int ratio, float bound_c, uint32_t *stats, hipStream_t stream, float *bounds,
-                          float *kmax, uint32_t *row_counts, const float *ksc) {
+                          float *kmax, uint32_t *row_counts, const float *ksc, const QSplit *qsplit) {
   if (D == 128)
     return launch_scores_d<128>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                                bound_c, stats, bounds, kmax, row_counts, ksc, stream);
+                                bound_c, stats, bounds, kmax, row_counts, ksc, stream, qsplit);
   if (D == 64)
     return launch_scores_d<64>(q, k, w, w_bf16, qn, qsp, kn, ksp, scores, B, S, H, T, kbs, causal, start_pos, ratio,
-                               bound_c, stats, bounds, kmax, row_counts, ksc, stream);
+                               bound_c, stats, bounds, kmax, row_counts, ksc, stream, qsplit);
   return fail(KS_ERR_INVALID, "indexer scores: D=%lld, supported: 64, 128", (long long)D);
 }
 

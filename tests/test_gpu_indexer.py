@@ -700,3 +700,32 @@ def test_indexer_16_heads_rope_layouts(device, D, rs, rd, rope_k, w_bf16, causal
     print(f"[case] indexer 16 heads D={D} rope=[{rs},{rs + rd}) rope_k={rope_k} w_bf16={w_bf16} causal={causal}",
           flush=True)
     _indexer_vs_oracle(q, k, w, tab, 96, causal, start, 1, 0 if causal else 5, rs, rd, rope_k, T)
+
+
+@pytest.mark.parametrize("D,rs,rd", [(64, 32, 32), (128, 64, 64)])
+def test_indexer_16_heads_split_rows_wide_range(device, D, rs, rd):
+    # the fused indexer's exact path with a 32-aligned rotated range: the row preparation writes only q's rotated
+    # dims and the score kernel reads the others from the caller's rows.  Cubed normals (row spans past the double-
+    # precision paths) send near-tie dots through the wide-range and integer-accumulator recomputations, which read
+    # q from memory on both sides of the split; every index must be the oracle's
+    g = torch.Generator().manual_seed(D + 7)
+    B, S, H, T = 1, 24, 16, 600
+    q = (torch.randn(B, S, H, D, generator=g) ** 3).bfloat16()
+    k = (torch.randn(B, T, D, generator=g) ** 3).bfloat16()
+    w = torch.randn(B, S, H, generator=g) / 8
+    tab = workloads.freqs_table(rd, 1024)
+    k_top, start = 64, T - S
+    qd, kd, wd, td = q.to("cuda"), k.to("cuda"), w.to("cuda"), tab.to("cuda")
+    ws = torch.empty(ops.indexer_workspace_size(B, S, H, D, T), dtype=torch.uint8, device="cuda")
+    out = torch.empty(B, S, k_top, dtype=torch.int32, device="cuda")
+    st = torch.zeros(2, dtype=torch.int32, device="cuda")
+    print(f"[case] indexer 16 heads split rows D={D} rope=[{rs},{rs + rd}) cubed normals", flush=True)
+    _lib.check(_lib.load().ks_dbg_indexer(qd.data_ptr(), kd.data_ptr(), wd.data_ptr(), 0, td.data_ptr(), tab.shape[0],
+                                          rs, rd, 0, k_top, 1, start, 1, 0, out.data_ptr(), 0, B, S, H, D, T, T,
+                                          ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream,
+                                          BOUND_C, st.data_ptr(), 1), "ks_dbg_indexer")
+    torch.cuda.synchronize()
+    want = oracle.indexer(_u16(q), _u16(k), w.numpy(), tab.numpy(), k_top, True, start, 1, 0, rs, rd, False)
+    print(f"[info] exact dots {int(st[0])}, integer-accumulator dots {int(st[1])}", flush=True)
+    assert st[1] > 0
+    np.testing.assert_array_equal(out.cpu().numpy().astype(np.int64), want)

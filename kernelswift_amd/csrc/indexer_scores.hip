@@ -75,7 +75,7 @@ struct ScoresLds {
                                               // each 16-byte chunk: a chunk is one accumulation step)
   uint8_t klist[kQW][kKR];           // per wave: block rows of the keys holding a near-tie dot (a wave's tiles
                                      // defer at most every key of the block)
-  KeyEntry<HT> ent[kQW][kEntCap];
+  KeyEntry<HT> ent[HT == 1 ? 0 : kQW][kEntCap];  // 16 heads: the resolution keeps its keys' values in registers
   uint32_t dots[kQW][kDotCap];       // near-tie dots: head << 24 | key row << 16 | pair << 4 | slot,
                                      // pair = 4 entry + group
   int32_t kspan[kKR];                // row statistics of the key block and of each wave's query rows, for
@@ -143,6 +143,92 @@ __device__ __forceinline__ uint32_t entry_mask(const KeyEntry<HT> &en, int gg) {
   return m;
 }
 
+// The exact value (RNE to bf16, before the ReLU) of the dot of head h's q row and key row kl of the block,
+// computed by a quad of lanes (this lane: quarter `sub`); every lane of the wave calls it together (the path
+// choices are ballots).  16 heads: quarter `sub` takes the 16-byte chunks 4c + sub, which lane h + 16 sub holds as
+// its A-fragment qa[0][c] (read with ds_bpermute); more heads: the chunks kLC sub + c, read from global memory
+// (L2-resident).  scur: the span sum that decided the path (> 84: the integer accumulator).
+template <int HT, int KD>
+__device__ __forceinline__ uint16_t quad_exact_dot(ScoresLds<KD, HT> &L, int wave, int sub, int h, int kl,
+                                                   const uint16_t *__restrict__ q, QSplit qsp,
+                                                   const uint4 (&qa)[HT][KD / 32], int64_t qrow0, int &scur) {
+  constexpr int kC = KD / 8, kLC = KD / 32;  // 16-byte chunks per key row; chunks per lane
+  // the q rows this lane reads from memory: its quarter (elements KD/4 sub ..) lies wholly on one side of a
+  // split (QSplit boundaries are 32-aligned)
+  const uint16_t *qsrc = (qsp.rot != nullptr && (KD / 4) * sub >= qsp.lo && (KD / 4) * sub < qsp.hi) ? qsp.rot : q;
+  uint4 qcur[kLC], kcur[kLC];
+  if constexpr (HT == 1) {
+    const int src = 4 * (h + 16 * sub);
+    auto bp = [&](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(v))); };
+#pragma unroll
+    for (int c = 0; c < kLC; ++c) {
+      qcur[c] = make_uint4(bp(qa[0][c].x), bp(qa[0][c].y), bp(qa[0][c].z), bp(qa[0][c].w));
+      kcur[c] = L.k[kl * kC + ((4 * c + sub) ^ (kl & (kC - 1)))];
+    }
+  } else {
+    const uint4 *qp = reinterpret_cast<const uint4 *>(qsrc + (qrow0 + h) * KD + (KD / 4) * sub);
+#pragma unroll
+    for (int c = 0; c < kLC; ++c) qcur[c] = qp[c];
+#pragma unroll
+    for (int c = 0; c < kLC; ++c) kcur[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
+  }
+  scur = L.qspan[wave][h] + L.kspan[kl];
+  uint16_t r;
+  if (__builtin_amdgcn_ballot_w64(scur > 52) == 0ull) {
+    // every partial sum is a multiple of the smallest product LSB and below 2^53 of it: exact doubles
+    // in any order
+    double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+    for (int c = 0; c < kLC; ++c) {
+      const uint32_t qw[4] = {qcur[c].x, qcur[c].y, qcur[c].z, qcur[c].w};
+      const uint32_t kw[4] = {kcur[c].x, kcur[c].y, kcur[c].z, kcur[c].w};
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        a0 = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), a0);
+        a1 = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), a1);
+      }
+    }
+    const double sum = quad_sum_f64(a0 + a1);
+    const bool outside = sum != 0.0 && !(fabs(sum) >= 0x1p-126 && fabs(sum) < 0x1p127);
+    if (__builtin_amdgcn_ballot_w64(outside) == 0ull) {
+      r = round_to_bf16_fast(sum);
+    } else {
+      r = round_dir_to_bf16(sum, 0);
+    }
+  } else {
+    // wide dynamic range: products above / below 2^(top - 38) accumulate separately, each exactly
+    const int span_sum = scur;
+    const int top_sum = frexp_exp(L.qnorm[wave][h]) + frexp_exp(L.knorm[kl]);
+    const bool split = span_sum > 52;
+    const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
+    double hi = 0.0, lo = 0.0;
+    // rare path, kept register-light: one dword of q and k per step, re-read from memory
+    const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qsrc + (qrow0 + h) * KD + (KD / 4) * sub);
+#pragma unroll 1
+    for (int j = 0; j < 4 * kLC; ++j) {
+      const uint32_t qw = q32[j];
+      const uint32_t kw =
+          reinterpret_cast<const uint32_t *>(&L.k[kl * kC + ((kLC * sub + (j >> 2)) ^ (kl & (kC - 1)))])[j & 3];
+      const double p0 = static_cast<double>(unpack_lo(qw)) * static_cast<double>(unpack_lo(kw));
+      const double p1 = static_cast<double>(unpack_hi(qw)) * static_cast<double>(unpack_hi(kw));
+      if (!split || fabs(p0) >= thr) hi += p0; else lo += p0;
+      if (!split || fabs(p1) >= thr) hi += p1; else lo += p1;
+    }
+    r = round2_to_bf16(quad_sum_f64(hi), quad_sum_f64(lo));
+  }
+  if (scur > 84) {
+    // wider still (the whole quad takes this branch): the integer accumulator, any range
+    const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qsrc + (qrow0 + h) * KD);  // part `sub` of it
+    r = exact_dot_wide_bf16<KD, 4>(
+        [&](int j) { return q32[j]; },
+        [&](int j) {
+          return reinterpret_cast<const uint32_t *>(&L.k[kl * kC + ((j >> 2) ^ (kl & (kC - 1)))])[j & 3];
+        },
+        sub);
+  }
+  return r;
+}
+
 // Exact recomputation of the deferred near-tie dots of one wave, then of the affected scores.
 template <int HT, int KD, bool WBF>
 __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent, const uint16_t *__restrict__ q,
@@ -198,86 +284,12 @@ __device__ void flush_entries(ScoresLds<KD, HT> &L, int wave, int lane, int nent
     const int nd = min(kDotCap, ndots - base);
     const int dq = lane >> 2, sub = lane & 3;
     for (int b0 = 0; b0 < nd; b0 += 16) {
-      // list entry of this quad (idle quads repeat the last one; the result is identical), its quarter of the q
-      // row and of the key row (LDS), and the span sum that decides the path.  16 heads: quarter `sub` takes the
-      // 16-byte chunks 4c + sub, which lane h + 16 sub holds as its A-fragment qa[0][c] (read with ds_bpermute);
-      // more heads: the chunks kLC sub + c, read from global memory (L2-resident).
+      // list entry of this quad (idle quads repeat the last one; the result is identical)
       const uint32_t dcur = D[min(b0 + dq, nd - 1)];
-      // the q rows this lane reads from memory: its quarter (elements KD/4 sub ..) lies wholly on one side of a
-      // split (QSplit boundaries are 32-aligned)
-      const uint16_t *qsrc = (qsp.rot != nullptr && (KD / 4) * sub >= qsp.lo && (KD / 4) * sub < qsp.hi) ? qsp.rot : q;
       const int h = static_cast<int>(dcur >> 24), kl = static_cast<int>((dcur >> 16) & 255u);
-      uint4 qcur[kLC], kcur[kLC];
-      if constexpr (HT == 1) {
-        const int src = 4 * (h + 16 * sub);
-        auto bp = [&](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(v))); };
-#pragma unroll
-        for (int c = 0; c < kLC; ++c) {
-          qcur[c] = make_uint4(bp(qa[0][c].x), bp(qa[0][c].y), bp(qa[0][c].z), bp(qa[0][c].w));
-          kcur[c] = L.k[kl * kC + ((4 * c + sub) ^ (kl & (kC - 1)))];
-        }
-      } else {
-        const uint4 *qp = reinterpret_cast<const uint4 *>(qsrc + (qrow0 + h) * KD + (KD / 4) * sub);
-#pragma unroll
-        for (int c = 0; c < kLC; ++c) qcur[c] = qp[c];
-#pragma unroll
-        for (int c = 0; c < kLC; ++c) kcur[c] = L.k[kl * kC + ((kLC * sub + c) ^ (kl & (kC - 1)))];
-      }
-      const int scur = L.qspan[wave][h] + L.kspan[kl];
       const int pr = static_cast<int>((dcur >> 4) & 255u), slot = static_cast<int>(dcur & 15u);
-      uint16_t r;
-      if (__builtin_amdgcn_ballot_w64(scur > 52) == 0ull) {
-        // every partial sum is a multiple of the smallest product LSB and below 2^53 of it: exact doubles
-        // in any order
-        double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-        for (int c = 0; c < kLC; ++c) {
-          const uint32_t qw[4] = {qcur[c].x, qcur[c].y, qcur[c].z, qcur[c].w};
-          const uint32_t kw[4] = {kcur[c].x, kcur[c].y, kcur[c].z, kcur[c].w};
-#pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            a0 = __builtin_fma(static_cast<double>(unpack_lo(qw[p])), static_cast<double>(unpack_lo(kw[p])), a0);
-            a1 = __builtin_fma(static_cast<double>(unpack_hi(qw[p])), static_cast<double>(unpack_hi(kw[p])), a1);
-          }
-        }
-        const double sum = quad_sum_f64(a0 + a1);
-        const bool outside = sum != 0.0 && !(fabs(sum) >= 0x1p-126 && fabs(sum) < 0x1p127);
-        if (__builtin_amdgcn_ballot_w64(outside) == 0ull) {
-          r = round_to_bf16_fast(sum);
-        } else {
-          r = round_dir_to_bf16(sum, 0);
-        }
-      } else {
-        // wide dynamic range: products above / below 2^(top - 38) accumulate separately, each exactly
-        const int span_sum = scur;
-        const int top_sum = frexp_exp(L.qnorm[wave][h]) + frexp_exp(L.knorm[kl]);
-        const bool split = span_sum > 52;
-        const double thr = split ? ldexp(1.0, top_sum - 38) : 0.0;
-        double hi = 0.0, lo = 0.0;
-        // rare path, kept register-light: one dword of q and k per step, re-read from memory
-        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qsrc + (qrow0 + h) * KD + (KD / 4) * sub);
-#pragma unroll 1
-        for (int j = 0; j < 4 * kLC; ++j) {
-          const uint32_t qw = q32[j];
-          const uint32_t kw =
-              reinterpret_cast<const uint32_t *>(&L.k[kl * kC + ((kLC * sub + (j >> 2)) ^ (kl & (kC - 1)))])[j & 3];
-          const double p0 = static_cast<double>(unpack_lo(qw)) * static_cast<double>(unpack_lo(kw));
-          const double p1 = static_cast<double>(unpack_hi(qw)) * static_cast<double>(unpack_hi(kw));
-          if (!split || fabs(p0) >= thr) hi += p0; else lo += p0;
-          if (!split || fabs(p1) >= thr) hi += p1; else lo += p1;
-        }
-        r = round2_to_bf16(quad_sum_f64(hi), quad_sum_f64(lo));
-      }
-      if (scur > 84) {
-        // wider still (the whole quad takes this branch): the integer accumulator, any range
-        const uint32_t *q32 = reinterpret_cast<const uint32_t *>(qsrc + (qrow0 + h) * KD);  // part `sub` of it
-        r = exact_dot_wide_bf16<KD, 4>(
-            [&](int j) { return q32[j]; },
-            [&](int j) {
-              return reinterpret_cast<const uint32_t *>(&L.k[kl * kC + ((j >> 2) ^ (kl & (kC - 1)))])[j & 3];
-            },
-            sub);
-      }
+      int scur;
+      const uint16_t r = quad_exact_dot<HT, KD>(L, wave, sub, h, kl, q, qsp, qa, qrow0, scur);
       const uint32_t rv = (r & 0x8000) ? 0u : r;  // ReLU (also maps -0 to +0)
       if (sub == 0 && b0 + dq < nd) {
         uint16_t *half = reinterpret_cast<uint16_t *>(&E[pr >> 2].pl[pr & 3][slot >> 1]) + (slot & 1);
@@ -878,42 +890,110 @@ indexer_scores_kernel(
       for (int t = 0; t < nlive; ++t) (void)epilogue(std::true_type{}, std::false_type{}, std::false_type{}, t, acc, accs);
     }
     // resolution, 16 listed keys at a time: the same MFMAs and interval test on their rows (the same operands, so
-    // the same interval ends), all four groups' ends of each key saved as a deferred entry, and the entries'
-    // near-tie dots computed exactly and their scores rewritten whenever another 16 could overflow the entries
+    // the same interval ends)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    for (int base = 0; base < nlist; base += 16) {
-      const int key_l = klist[min(base + l16, nlist - 1)];
-      tile_mfma(key_l, acc, accs);
-      uint32_t pl[2 * HT], ph[2 * HT];
-      // every listed key is in range and before the causal limit; lanes past the list repeat its last key
-      const uint32_t km = key_mask(interval_ends(acc, accs, pl, ph) &
-                                   __builtin_amdgcn_ballot_w64(base + l16 < nlist));
-      if ((km >> l16) & 1u) {
-        const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
-        KeyEntry<HT> &en = L.ent[wave][e];
-#pragma unroll
-        for (int p = 0; p < 2 * HT; ++p) {
-          en.pl[g][p] = pl[p];
-          en.ph[g][p] = ph[p];
+    if constexpr (HT == 1) {
+      // 16 heads: each round keeps its 16 keys' interval ends in registers (lane (g, l16): heads 4 g .. 4 g + 3 of
+      // key l16), lists the round's near-tie dots (lane and head bit, 16 bits each; at most 256) in the wave's dot list,
+      // computes them exactly 16 at a time, patches the exact relu'd values (through the list's patch slots, one
+      // per lane and head bit) into its own ends and stores the round's scores.
+      const QSplit qsp{qsplit_rot, qsplit_lo, qsplit_hi};
+      // a round holds at most 16 keys x 16 heads = 256 near-tie dots: [0, 256) the list, [256, 512) the patches
+      static_assert(2 * 256 * sizeof(uint16_t) <= sizeof(L.dots[0]), "dot list and patches of one round");
+      uint16_t *Dl = reinterpret_cast<uint16_t *>(L.dots[wave]);
+      uint16_t *Pt = Dl + 256;
+      const int dq = lane >> 2, sub = lane & 3;
+      for (int base = 0; base < nlist; base += 16) {
+        const int key_l = klist[min(base + l16, nlist - 1)];
+        tile_mfma(key_l, acc, accs);
+        uint32_t pl[2], ph[2];
+        (void)interval_ends(acc, accs, pl, ph);
+        // this lane's near-tie dots: bit b = head 4 g + b (half b & 1 of pl[b >> 1]); lanes past the list none
+        uint32_t m = 0;
+        if (base + l16 < nlist) {
+          const uint32_t d0 = pl[0] ^ ph[0], d1 = pl[1] ^ ph[1];
+          m = ((d0 & 0xFFFFu) ? 1u : 0u) | ((d0 >> 16) ? 2u : 0u) | ((d1 & 0xFFFFu) ? 4u : 0u) | ((d1 >> 16) ? 8u : 0u);
         }
-        if (g == 0) en.key = kb0 + key_l;
-      }
-      nent += __builtin_popcount(km);
-      if (nent + 16 > kEntCap || base + 16 >= nlist) {
+        uint32_t nd_u;
+        uint32_t pos = wave_excl_scan_bits<3>(static_cast<uint32_t>(__builtin_popcount(m)), nd_u);
+        for (uint32_t mm = m; mm != 0u; mm &= mm - 1u) Dl[pos++] = static_cast<uint16_t>((lane << 2) | __builtin_ctz(mm));
+        n_exact += nd_u;
+        const int nd = static_cast<int>(nd_u);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (nent > 0)
-          flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qa, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres,
-                                     QSplit{qsplit_rot, qsplit_lo, qsplit_hi});
-        nent = 0;
+        for (int b0 = 0; b0 < nd; b0 += 16) {
+          // the quad's dot (idle quads repeat the last one; the result is identical): lane sl's head bit
+          const int dcur = Dl[min(b0 + dq, nd - 1)];
+          const int sl = dcur >> 2;
+          const int h = 4 * (sl >> 4) + (dcur & 3);
+          const int kl = klist[base + (sl & 15)];
+          int scur;
+          const uint16_t r = quad_exact_dot<HT, KD>(L, wave, sub, h, kl, q, qsp, qa, qrow0, scur);
+          if (sub == 0 && b0 + dq < nd) {
+            Pt[dcur] = (r & 0x8000) ? 0u : r;  // ReLU (also maps -0 to +0)
+            if (scur > 84) ++n_unres;  // counted: dots that needed the integer accumulator
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (m != 0u) {
+#pragma unroll
+          for (int bit = 0; bit < 4; ++bit)
+            if ((m >> bit) & 1u) {
+              const uint32_t v = Pt[(lane << 2) | bit];
+              uint32_t &w2 = pl[bit >> 1];
+              w2 = (bit & 1) ? ((w2 & 0xFFFFu) | (v << 16)) : ((w2 & 0xFFFF0000u) | v);
+            }
+        }
+        // the round's scores from the patched values (every listed key is in range and before the causal limit)
+        const float G = group_sum<HT, WBF>([&](int i) { return pl[i]; }, wv);
+        const float tot = combine_groups(G);
+        if (g == 0 && base + l16 < nlist) orow[static_cast<uint32_t>(kb0 + key_l)] = WBF ? round_score_bf16(tot) : tot;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    } else {
+      // all four groups' ends of each key saved as a deferred entry, and the entries' near-tie dots computed
+      // exactly and their scores rewritten whenever another 16 could overflow the entries
+      for (int base = 0; base < nlist; base += 16) {
+        const int key_l = klist[min(base + l16, nlist - 1)];
+        tile_mfma(key_l, acc, accs);
+        uint32_t pl[2 * HT], ph[2 * HT];
+        // every listed key is in range and before the causal limit; lanes past the list repeat its last key
+        const uint32_t km = key_mask(interval_ends(acc, accs, pl, ph) &
+                                     __builtin_amdgcn_ballot_w64(base + l16 < nlist));
+        if ((km >> l16) & 1u) {
+          const int e = nent + __builtin_popcount(km & ((1u << l16) - 1u));
+          KeyEntry<HT> &en = L.ent[wave][e];
+#pragma unroll
+          for (int p = 0; p < 2 * HT; ++p) {
+            en.pl[g][p] = pl[p];
+            en.ph[g][p] = ph[p];
+          }
+          if (g == 0) en.key = kb0 + key_l;
+        }
+        nent += __builtin_popcount(km);
+        if (nent + 16 > kEntCap || base + 16 >= nlist) {
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          if (nent > 0)
+            flush_entries<HT, KD, WBF>(L, wave, lane, nent, q, qa, qrow0, orow, limit, T, kb0, wv, n_exact, n_unres,
+                                       QSplit{qsplit_rot, qsplit_lo, qsplit_hi});
+          nent = 0;
+        }
       }
     }
   }
-  // masked tiles (at or past the causal limit)
-  for (int t = nlive; t < ntiles; ++t) {
-    const int key_l = 16 * t + l16;
-    if (g == 0 && key_l < nk) orow[kb0 + key_l] = -INFINITY;
+  // masked tiles (at or past the causal limit); the exact kernel stores with every lane (the bound kernel keeps
+  // its tile form, which its register allocation was tuned with)
+  if constexpr (BOUND) {
+    for (int t = nlive; t < ntiles; ++t) {
+      const int key_l = 16 * t + l16;
+      if (g == 0 && key_l < nk) orow[kb0 + key_l] = -INFINITY;
+    }
+  } else {
+    for (int key_l = 16 * nlive + lane; key_l < nk; key_l += 64) orow[static_cast<uint32_t>(kb0 + key_l)] = -INFINITY;
   }
   if constexpr (COUNT) {
     // the wave's counts into its row's histogram (only the nonzero buckets: a block of 256 keys fills a few

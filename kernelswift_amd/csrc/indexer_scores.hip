@@ -333,7 +333,7 @@ struct ScoresLdsBound {
 // Waves per SIMD a kernel form is built for.  The non-counting bound kernel runs grids of several workgroups per
 // CU: at most 168 VGPRs (three waves per SIMD) let the next workgroup start as soon as one wave per SIMD of the
 // current one has finished.  The exact kernel at 16 heads of 64 dims (the drop-in shape: 4 dots per lane and tile,
-// a tile one chain of dependent steps) at 128 VGPRs and 72 KiB of LDS holds two workgroups per CU: four waves per
+// a tile one chain of dependent steps) at up to 128 VGPRs and 57 KiB of LDS holds two workgroups per CU: four waves per
 // SIMD hide each other's tile latency, and one workgroup's prologue loads overlap the other's tiles.
 template <int HT, int KD, bool BOUND, bool COUNT>
 constexpr int score_waves() { return (BOUND && !COUNT) ? 3 : (!BOUND && HT == 1 && KD == 64) ? 4 : 1; }

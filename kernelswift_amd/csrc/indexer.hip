@@ -146,7 +146,9 @@ int indexer_select(const char *fn, const IndexerWs &ws, const void *w, int32_t w
                                  start_pos, ratio, bound_c, stats, st, nullptr, nullptr, nullptr, nullptr,
                                  q_unrot != nullptr ? &qs : nullptr);
   if (rc != KS_OK) return rc;
-  return ks_indexer_topk(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, st);
+  // bf16 weights: the exact scores are rounded to bf16, so the top-k may take them as bf16 values
+  return ks::indexer_topk_impl(ws.scores, T, B, S, T, kk, causal, start_pos, ratio, offset, out, out_i64, st,
+                               w_bf16 ? 1 : 0);
 }
 
 int indexer_impl(const uint16_t *q, const uint16_t *k, const void *w, int32_t w_bf16, const float *freqs,

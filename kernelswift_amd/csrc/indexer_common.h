@@ -354,6 +354,12 @@ int64_t topk_bounded_part_capacity(int64_t rows, int64_t T);
 // ([rows][4] 32-bit), kTopkCountWords 32-bit words per row in all, to be cleared before the score kernel.
 constexpr int64_t kTopkCountWords = 2048 + 4;
 uint32_t *topk_bounded_counts(uint64_t *part, int64_t rows, int64_t T);
+// ks_indexer_topk with the caller's guarantee that every score is a bf16 value (bf16_vals = 1), which spares the
+// one-wave-per-row form its check of the keys' low halves.
+int indexer_topk_impl(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k, int32_t causal,
+                      int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64, void *stream,
+                      int bf16_vals);
+
 int launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k, int causal,
                                 int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64,
                                 const TopkRecompute &rc, hipStream_t stream);

@@ -389,7 +389,7 @@ template <int KPT>
 __global__ __launch_bounds__(kWaveThreads) void topk_wave_kernel(const float *__restrict__ scores, int64_t ld,
                                                                 int64_t rows, int64_t S, int T, int k, int causal,
                                                                 int64_t start_pos, int ratio, int64_t offset,
-                                                                void *__restrict__ out, int out_i64) {
+                                                                void *__restrict__ out, int out_i64, int bf16_vals) {
   __shared__ uint32_t hist[kWaveRows][256];
   __shared__ uint64_t cand[kWaveRows][128];
   // the row index in scalar registers (rows < 2^31, checked by the caller): its remainder by S is a 32-bit scalar
@@ -415,15 +415,20 @@ __global__ __launch_bounds__(kWaveThreads) void topk_wave_kernel(const float *__
     f[j] = src[col < n_valid ? col : 0];
   }
   uint32_t key[KPT];
-  bool odd_low = false;  // a valid key whose low 16 bits do not follow from its sign
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    key[j] = 64 * j + lane < n_valid ? score_key(f[j]) : 0u;
-    const uint32_t low = key[j] & 0xFFFFu;
-    odd_low = odd_low || (key[j] != 0u && low != ((key[j] >> 31) ? 0u : 0xFFFFu));
+  for (int j = 0; j < KPT; ++j) key[j] = 64 * j + lane < n_valid ? score_key(f[j]) : 0u;
+  // every key fixed by its top 16 bits (uniform): checked, unless the caller's scores are bf16 values by
+  // construction (bf16_vals: the fused indexer's scores with bf16 weights, rounded to bf16)
+  bool top16 = bf16_vals != 0;
+  if (!top16) {
+    bool odd_low = false;  // a valid key whose low 16 bits do not follow from its sign
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const uint32_t low = key[j] & 0xFFFFu;
+      odd_low = odd_low || (key[j] != 0u && low != ((key[j] >> 31) ? 0u : 0xFFFFu));
+    }
+    top16 = __builtin_amdgcn_ballot_w64(odd_low) == 0ull;
   }
-  // every key fixed by its top 16 bits (uniform)
-  const bool top16 = __builtin_amdgcn_ballot_w64(odd_low) == 0ull;
   if (k_sel > 0) {  // uniform
     uint32_t *h = hist[wave];
     uint32_t prefix = 0, mask = 0, k_rem = static_cast<uint32_t>(k_sel), eq_total = 0;
@@ -537,10 +542,11 @@ __global__ __launch_bounds__(kWaveThreads) void topk_wave_kernel(const float *__
 
 template <int KPT>
 int launch_topk_wave(const float *scores, int64_t ld, int64_t rows, int64_t S, int T, int k, int causal,
-                     int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream) {
+                     int64_t start_pos, int ratio, int64_t offset, void *out, int out_i64, hipStream_t stream,
+                     int bf16_vals) {
   hipLaunchKernelGGL(topk_wave_kernel<KPT>, dim3(static_cast<unsigned>(ceil_div(rows, kWaveRows))),
                      dim3(kWaveThreads), 0, stream, scores, ld, rows, S, T, k, causal, start_pos, ratio, offset, out,
-                     out_i64);
+                     out_i64, bf16_vals);
   KS_CHECK_LAUNCH("topk_wave_kernel");
   return KS_OK;
 }
@@ -1232,10 +1238,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_collected_kernel(const floa
 }  // namespace
 }  // namespace ks
 
-extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
-                               int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out,
-                               int32_t out_i64, void *stream) {
-  ks::last_error().clear();
+// bf16_vals: every score is a bf16 value (the caller's guarantee; the wave form then skips its check of the keys'
+// low halves)
+int ks::indexer_topk_impl(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k, int32_t causal,
+                          int64_t start_pos, int32_t ratio, int64_t offset, void *out, int32_t out_i64, void *stream,
+                          int bf16_vals) {
   KS_CHECK_ARG(B >= 0 && S >= 0, "ks_indexer_topk: negative B or S");
   KS_CHECK_ARG(T >= 1 && T <= 65536, "ks_indexer_topk: T=%lld must be in [1, 65536]", (long long)T);
   KS_CHECK_ARG(k >= 1 && k <= T && k <= ks::kTopkMaxK, "ks_indexer_topk: k=%lld must be in [1, min(T, %d)]",
@@ -1252,12 +1259,12 @@ extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64
   const int Ti = static_cast<int>(T), ki = static_cast<int>(k);
   const int c = causal ? 1 : 0, o = out_i64 ? 1 : 0;
   if (T <= 1024 && k <= 128) {  // short rows: one wave per row
-    if (T <= 64) return ks::launch_topk_wave<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
-    if (T <= 128) return ks::launch_topk_wave<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
-    if (T <= 256) return ks::launch_topk_wave<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
-    if (T <= 512) return ks::launch_topk_wave<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
-    if (T <= 768) return ks::launch_topk_wave<12>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
-    return ks::launch_topk_wave<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+    if (T <= 64) return ks::launch_topk_wave<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st, bf16_vals);
+    if (T <= 128) return ks::launch_topk_wave<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st, bf16_vals);
+    if (T <= 256) return ks::launch_topk_wave<4>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st, bf16_vals);
+    if (T <= 512) return ks::launch_topk_wave<8>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st, bf16_vals);
+    if (T <= 768) return ks::launch_topk_wave<12>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st, bf16_vals);
+    return ks::launch_topk_wave<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st, bf16_vals);
   }
   if (T <= 1024) return ks::launch_topk<1>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   if (T <= 2048) return ks::launch_topk<2>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
@@ -1266,6 +1273,13 @@ extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64
   if (T <= 16384) return ks::launch_topk<16>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   if (T <= 32768) return ks::launch_topk<32>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
   return ks::launch_topk<64>(scores, ld, rows, S, Ti, ki, c, start_pos, ratio, offset, out, o, st);
+}
+
+extern "C" int ks_indexer_topk(const float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,
+                               int32_t causal, int64_t start_pos, int32_t ratio, int64_t offset, void *out,
+                               int32_t out_i64, void *stream) {
+  ks::last_error().clear();
+  return ks::indexer_topk_impl(scores, ld, B, S, T, k, causal, start_pos, ratio, offset, out, out_i64, stream, 0);
 }
 
 int ks::launch_indexer_topk_bounded(float *scores, int64_t ld, int64_t B, int64_t S, int64_t T, int64_t k,

@@ -12,13 +12,20 @@ import torch
 import torch.nn as nn
 
 
+_OPS = None
+
+
 def _ops():
-    """torch.ops.ks_mi355x (libkswift_torch.so), loaded on first use like the reference wrappers' extension."""
-    root = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
-    if root not in sys.path:
-        sys.path.insert(0, root)
-    from kernelswift_amd import _lib
-    return _lib.torch_ops()
+    """torch.ops.ks_mi355x (libkswift_torch.so), loaded on first use like the reference wrappers' extension, then
+    kept (a forward's first call into the library should not pay an import lookup)."""
+    global _OPS
+    if _OPS is None:
+        root = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+        if root not in sys.path:
+            sys.path.insert(0, root)
+        from kernelswift_amd import _lib
+        _OPS = _lib.torch_ops()
+    return _OPS
 
 
 class ModelNew(nn.Module):

@@ -394,6 +394,22 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
                         "cache": ("warm (the 2 MiB kv fits in L2)" if cfg == 3
                                   else "kv 2.25 GiB: gathered rows come from HBM")},
            "gathered_GBps": round(gathered / (op_us * 1e-6) / 1e9, 1)}
+    if cfg == 3:
+        # the reference's dense count-mask formulation (optimized/sparse_attention/design.md:46-69) on the MFMA at
+        # this shape: every query scores every key, the top-k list as per-key counts (a diagnostic kernel; the op
+        # dispatches to the gather kernel, which is faster here)
+        lib = _lib.load()
+        out_c = torch.empty(B, M, H, dv, dtype=torch.bfloat16, device="cuda")
+        N = t["kv"].shape[1]
+        strm = torch.cuda.current_stream().cuda_stream
+
+        def dense():
+            _lib.check(lib.ks_dbg_sparse_attn_count(t["q"].data_ptr(), t["kv"].data_ptr(), t["sink"].data_ptr(),
+                                                    t["idx"].data_ptr(), out_c.data_ptr(), B, M, H, N, K, p["scale"],
+                                                    ws.data_ptr(), ws_n, strm), "ks_dbg_sparse_attn_count")
+        dense_us = _events_avg(dense, steps, warmup)
+        res["dense_count_mask_us"] = round(dense_us, 3)
+        res["dense_count_mask_frac_of_sparse_flops"] = round(flops / (dense_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4)
     if do_cpu:
         from oracle import torch_ref
         torch.set_num_threads(_cpu_threads())

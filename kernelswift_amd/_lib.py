@@ -61,6 +61,8 @@ DEBUG_SIGNATURES = {
                                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_p, _c_p,
                                                    _c_p, _c_i64]),
     "ks_dbg_topk_bounded_slots": (ctypes.c_int64, [_c_i64, _c_i64]),
+    "ks_dbg_sparse_attn_count": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                                _c_f, _c_p, _c_sz, _c_p]),
     "ks_dbg_indexer": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i64, _c_i32,
                                       _c_i64, _c_i32, _c_i64, _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                       _c_i64, _c_p, _c_sz, _c_p, _c_f, _c_p, _c_i32]),

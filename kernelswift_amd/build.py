@@ -32,10 +32,21 @@ COMMON = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 
+# Per-file flags.  sparse_attn.hip: MFMA builtins in their VGPR form (accumulators in VGPRs).  The count-mask kernel
+# rescales its O accumulators in a rarely taken branch; with AGPR accumulators the compiler moved all 64 of them
+# to VGPRs and back on every chunk.  The file's other kernels keep AGPR accumulators through inline assembly
+# (MLA) or fit in VGPRs either way.
+FILE_FLAGS = {"sparse_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
+def flags(src: str) -> list:
+    """hipcc flags of one source file (the common set plus its own)."""
+    return [*COMMON, *FILE_FLAGS.get(os.path.basename(src), [])]
+
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *COMMON, "-c", src, "-o", obj]
+    cmd = [HIPCC, *flags(src), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -1416,6 +1416,378 @@ int launch_sa_dense(const uint16_t *q, const uint16_t *kv, const float *sink, co
   return run(sparse_attn_dense_kernel<2, 4, PD>);
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Dense top-k lists over larger kv sets (Dqk = Dv = 128, K >= N / 4): the count-mask form over key splits.  At
+// 25% density the gather kernel spends each 32-key chunk on one query's 16 heads, a short chain of dependent
+// QK -> softmax -> PV with ~16 MFMAs, and gathers every row for every query.  Here every query scores every key of
+// its split on the MFMA, and the top-k list only says how often each key counts (the reference's dense design,
+// optimized/sparse_attention/design.md:46-69, there for N = 32).  That is 4x the MFMA work at 25% density, done
+// as long streams of 32 x 32 x 16 MFMAs on key chunks shared by the workgroup's waves.
+//   workgroup  128 consecutive (query, head) rows of one batch (4 waves x 32 rows; H divides 128) x one key split
+//              of KR keys; one wave per SIMD (registers: 4 x 16 O^T accumulators, 8 q fragments, two S^T tiles)
+//   counts     the workgroup's index rows read once (all loads in flight together) and counted into LDS with
+//              ds_add: invalid indices count nowhere, duplicates with multiplicity
+//   chunks     32 keys x 128 dims, DMA'd into a 3-buffer ring in the gather kernel's swizzled layout; at chunk c
+//              chunk c + 1 has landed and chunk c + 2 is in flight (one barrier per chunk)
+//   QK^T       S^T = K Q^T (M = 32 keys, N = 32 rows, K = 16 dims); lane (row l%32, half h = l/32) receives keys
+//              8j + 4h + r (j, r = 0..3).  Chunk c + 1's QK is issued before chunk c's softmax.
+//   softmax    p = 2^(s + log2(count) - m) with the lazily updated reference max of the gather kernel (the counts
+//              become log2 weights in LDS, -inf for keys counted nowhere); a row's keys are split over lanes l and
+//              l ^ 32, which share the max through v_permlane32_swap
+//   PV         O^T = V^T P^T (M = 32 dv, N = 32 rows, K = 16 keys): the k order of a step is the lane's own key
+//              order (keys 16s + 4h + e, then 16s + 8 + 4h + e), so P^T is the lane's probabilities as they
+//              are, and the matching V^T fragment is two ds_read_b64_tr_b16 reads.  O^T keeps one row per lane,
+//              so a rescale needs no exchange.
+// Partial ranges (O in bf16, max, sum) go through sparse_attn_combine_kernel; one split finalises in place.
+constexpr int kCntRows = 128;       // (query, head) rows per workgroup
+constexpr int kCntMaxKR = 2048;     // keys per split (LDS counts: 128 / H queries x KR x 4 bytes)
+constexpr int kCntBufs = 3;         // chunk ring
+constexpr int kCntTargetWgs = 256;  // one workgroup per CU
+constexpr int kCntIdxBatch = 16;    // index loads in flight per thread while counting
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                  0, 0, 0);
+}
+
+__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void sparse_attn_count_kernel(
+    const uint16_t *__restrict__ q, const uint16_t *__restrict__ kv, const float *__restrict__ sink,
+    const int32_t *__restrict__ idx, uint16_t *__restrict__ out, uint16_t *__restrict__ part_o,
+    float *__restrict__ part_ml, int64_t M, int H, int N, int K, int NS, int KR, int64_t tgb, float scale_log2,
+    int idx_vec) {
+  using Sh = SaShape<128, 128, 1>;                // the swizzle of 16-unit rows
+  constexpr int D = 128, BUF = 32 * D;            // bf16 elements per chunk buffer
+  extern __shared__ uint4 smem_cnt[];
+  uint16_t *kb = reinterpret_cast<uint16_t *>(smem_cnt);               // [kCntBufs][BUF]
+  uint32_t *cnt = reinterpret_cast<uint32_t *>(kb + kCntBufs * BUF);   // [128 / H][KR]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31, h2 = lane >> 5;
+  // the splits of one row block are dealt to one XCD (workgroup i runs on XCD i mod 8): they share its index rows
+  const int64_t nblk = gridDim.x;
+  const int64_t lb = (nblk % 8 == 0) ? (blockIdx.x % 8) * (nblk / 8) + blockIdx.x / 8 : blockIdx.x;
+  const int s = static_cast<int>(lb % NS);
+  const int64_t tg = (lb / NS) % tgb;
+  const int64_t b = lb / (static_cast<int64_t>(NS) * tgb);
+  const int64_t MH = M * H;
+  const int64_t row0 = tg * kCntRows;  // the workgroup's first row of batch b (a multiple of H)
+  const int QW = kCntRows / H;
+  const int64_t m0 = row0 / H;
+  const int qv = static_cast<int>(M - m0 < QW ? M - m0 : QW);  // queries of the workgroup inside the batch
+  const int k_lo = s * KR, k_hi = k_lo + KR < N ? k_lo + KR : N;
+  const int nch = (k_hi - k_lo + 31) / 32;  // >= 1: the host plan leaves no split empty
+  const global_ptr<const uint16_t> kvb = uniform_ptr(kv + b * static_cast<int64_t>(N) * D);
+  const uint32_t kb_lds = __builtin_amdgcn_readfirstlane(lds_addr(kb));
+
+  // ---- chunk DMA: slot 64 (wave + 4 i) + lane of a buffer holds unit (slot % 16) ^ swz(key) of key slot / 16
+  int dkey[2], doff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int sl = 64 * (wave + 4 * i) + lane;
+    dkey[i] = sl / 16;
+    doff[i] = ((sl % 16) ^ Sh::swz(dkey[i])) * 16;
+  }
+  auto dma_chunk = [&](int c, int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      int key = k_lo + 32 * c + dkey[i];
+      key = key < N ? key : N - 1;  // past the split's end: a real row, counted nowhere
+      dma16((const void *)kvb, static_cast<uint32_t>(key) * (D * 2) + doff[i],
+            kb_lds + (buf * BUF + 64 * (wave + 4 * i) * 8) * 2);
+    }
+  };
+  dma_chunk(0, 0);
+  if (nch > 1) dma_chunk(1, 1);
+
+  // ---- q B-fragments: row (wave's 32 rows, lane c32), dims 16j + 8h .. +7; rows past the batch read its last row
+  const int64_t qrow = row0 + 32 * wave + c32;
+  const bool row_ok = qrow < MH;
+  const uint16_t *qp = q + (b * MH + (row_ok ? qrow : MH - 1)) * D + 8 * h2;
+  uint4 qf[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) qf[j] = *reinterpret_cast<const uint4 *>(qp + 16 * j);
+
+  // ---- key counts of the workgroup's queries over [k_lo, k_hi)
+  for (int i = tid * 4; i < QW * KR; i += 1024) *reinterpret_cast<uint4 *>(cnt + i) = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  {
+    const int32_t *ib = idx + (b * M + m0) * static_cast<int64_t>(K);  // qv consecutive index rows
+    auto count = [&](int e, int32_t v) {
+      if (v >= k_lo && v < k_hi) atomicAdd(&cnt[(e / K) * KR + (v - k_lo)], 1u);
+    };
+    const int tot = qv * K;
+    if (idx_vec) {  // K % 4 == 0 and 16-byte aligned rows
+      const int4 *ib4 = reinterpret_cast<const int4 *>(ib);
+      const int n4 = tot >> 2;
+      for (int base = 0; base < n4; base += 256 * kCntIdxBatch) {
+        int4 v[kCntIdxBatch];
+#pragma unroll
+        for (int j = 0; j < kCntIdxBatch; ++j) {
+          const int u = base + 256 * j + tid;
+          v[j] = ib4[u < n4 ? u : n4 - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < kCntIdxBatch; ++j) {
+          const int u = base + 256 * j + tid;
+          if (u < n4) {
+            count(4 * u, v[j].x);
+            count(4 * u, v[j].y);
+            count(4 * u, v[j].z);
+            count(4 * u, v[j].w);
+          }
+        }
+      }
+    } else {
+      for (int base = 0; base < tot; base += 256 * kCntIdxBatch) {
+        int32_t v[kCntIdxBatch];
+#pragma unroll
+        for (int j = 0; j < kCntIdxBatch; ++j) {
+          const int e = base + 256 * j + tid;
+          v[j] = ib[e < tot ? e : tot - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < kCntIdxBatch; ++j) {
+          const int e = base + 256 * j + tid;
+          if (e < tot) count(e, v[j]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // counts -> log2 weights: p = 2^(s + log2(count) - m); -inf for keys counted nowhere
+  for (int i = tid * 4; i < QW * KR; i += 1024) {
+    uint4 *w = reinterpret_cast<uint4 *>(cnt + i);
+    const uint4 c = *w;
+    auto lw = [](uint32_t n) { return __float_as_uint(n == 0u ? -INFINITY : __log2f(static_cast<float>(n))); };
+    *w = make_uint4(lw(c.x), lw(c.y), lw(c.z), lw(c.w));
+  }
+  wait_dma();
+  __syncthreads();  // weights complete, chunks 0 and 1 visible
+
+  // ---- per-lane LDS element offsets.  QK: key c32, unit 2j + h (swizzled per j).  PV (transpose reads): lane
+  // 16R + 4e + jj addresses key 4(R >> 1) + e (+ 8, + 16 s), columns 32 ct + 16 (R & 1) + 4 jj .. +3
+  int qk_off[8], pv_off[4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) qk_off[j] = Sh::slot(c32, 0, 2 * j + h2) * 8;
+  {
+    const int R = lane >> 4, e = (lane >> 2) & 3, jj = lane & 3;
+    const int key = 4 * (R >> 1) + e;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) pv_off[ct] = Sh::slot(key, 0, 4 * ct + 2 * (R & 1) + (jj >> 1)) * 8 + 4 * (jj & 1);
+  }
+  const int qi = (32 * wave + c32) / H;  // the lane's query in the workgroup's count rows
+  const float *crow = reinterpret_cast<const float *>(cnt) + qi * KR + 4 * h2;  // log2 weights
+
+  // LDS reads of a chunk: the lane's 8 K fragments, its 4 x 2 V^T fragments (two transpose reads each) and the
+  // log2 weights of its 16 keys
+  auto kfrags = [&](int buf, uint4(&kf)[8]) {
+    const uint16_t *kbp = kb + buf * BUF;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kf[j] = *reinterpret_cast<const uint4 *>(kbp + qk_off[j]);
+  };
+  auto vfrags = [&](int buf, uint4(&vf)[4][2]) {
+    const uint16_t *kbp = kb + buf * BUF;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const uint2 v0 = lds_read_tr16(kbp + pv_off[ct] + (16 * s2) * 16 * 8);
+        const uint2 v1 = lds_read_tr16(kbp + pv_off[ct] + (16 * s2 + 8) * 16 * 8);
+        vf[ct][s2] = make_uint4(v0.x, v0.y, v1.x, v1.y);
+      }
+  };
+  auto weights = [&](int c, float (&w)[16]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 v = *reinterpret_cast<const float4 *>(crow + 32 * c + 8 * j);
+      w[4 * j] = v.x, w[4 * j + 1] = v.y, w[4 * j + 2] = v.z, w[4 * j + 3] = v.w;
+    }
+  };
+  // t = s + log2(weight) and its row max over the chunk (lanes l and l ^ 32 hold the row's two key halves)
+  auto scores = [&](const f32x16_t &sc, const float (&w)[16], float (&t)[16]) {
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      t[i] = fmaf(sc[i], scale_log2, w[i]);
+      cmax = fmaxf(cmax, t[i]);
+    }
+    float a = cmax, bb = cmax;
+    swap32(a, bb);
+    return fmaxf(a, bb);
+  };
+
+  float m_ref = -INFINITY, l_run = 0.f;  // per row (lanes l and l ^ 32 hold the same values)
+  f32x16_t o[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) o[ct] = f32x16_t{};
+  // u: the current chunk's exponents t - m_ref (-inf for keys counted nowhere)
+  float u[16];
+  {
+    uint4 kf[8];
+    float w[16], t[16];
+    kfrags(0, kf);
+    weights(0, w);
+    f32x16_t sc = {};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sc = mfma32(kf[j], qf[j], sc);
+    m_ref = scores(sc, w, t);
+    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;  // no counted key: every t is -inf, p = 0
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u[i] = t[i] - m_use;
+  }
+
+  // Two stages per chunk c: (A) chunk c + 1's QK MFMAs beside chunk c's exponentials and bf16 packing, (B) chunk
+  // c's PV MFMAs beside chunk c + 1's scores and row max.  A rescale for chunk c + 1 (rare) then scales O, which
+  // holds chunk c, and the sum.  On the last chunk the "next" buffer and weights are stale and unused.
+  for (int c = 0; c < nch; ++c) {
+    if (c + 1 < nch) wait_dma();  // this thread's part of chunk c + 1
+    __syncthreads();              // chunk c + 1 visible; every wave is done with chunk c - 1's buffer
+    if (c + 2 < nch) dma_chunk(c + 2, (c + 2) % kCntBufs);
+    uint4 kf[8], vf[4][2];
+    float w[16];
+    kfrags((c + 1) % kCntBufs, kf);
+    vfrags(c % kCntBufs, vf);
+    weights(c + 1 < nch ? c + 1 : c, w);
+    // (A)
+    f32x16_t sn = {};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sn = mfma32(kf[j], qf[j], sn);
+    float p[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      p[i] = fast_exp2(u[i]);
+      l_run += p[i];
+    }
+    uint4 pb[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+      pb[s2] = make_uint4(pack_bf16x2(p[8 * s2], p[8 * s2 + 1]), pack_bf16x2(p[8 * s2 + 2], p[8 * s2 + 3]),
+                          pack_bf16x2(p[8 * s2 + 4], p[8 * s2 + 5]), pack_bf16x2(p[8 * s2 + 6], p[8 * s2 + 7]));
+    // (B)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) o[ct] = mfma32(vf[ct][s2], pb[s2], o[ct]);
+    float t[16];
+    const float cmax = scores(sn, w, t);
+    const float m_use = m_ref == -INFINITY ? 0.f : m_ref;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) u[i] = t[i] - m_use;
+    const bool need = cmax > m_ref + kRescaleTau;  // false for cmax = -inf; true for a first counted chunk
+    if (c + 1 < nch && __builtin_amdgcn_ballot_w64(need) != 0ull) {
+      const float m_new = need ? cmax : m_ref;
+      const float alpha = need ? (m_ref == -INFINITY ? 0.f : fast_exp2(m_ref - m_new)) : 1.f;
+      l_run *= alpha;
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) o[ct] *= alpha;
+      m_ref = m_new;
+      const float m_use2 = m_ref == -INFINITY ? 0.f : m_ref;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) u[i] = t[i] - m_use2;
+    }
+  }
+
+  // ---- finalise: lane holds row qrow, dv columns 32 ct + 8 (i / 4) + 4h + i % 4
+  {
+    float a = l_run, bb = l_run;
+    swap32(a, bb);
+    l_run = a + bb;
+  }
+  if (!row_ok) return;
+  const int64_t m = qrow / H;
+  const int h = static_cast<int>(qrow % H);
+  const int64_t qm = b * M + m;
+  if (NS == 1) {
+    const float sk = sink[h] * kLog2e;
+    const float z = fmaxf(m_ref, sk);
+    float so = 0.f;
+    if (z != -INFINITY) {
+      const float e = m_ref == -INFINITY ? 0.f : exp2f(m_ref - z);
+      const float den = l_run * e + exp2f(sk - z);
+      so = den > 0.f ? e / den : 0.f;
+    }
+    uint16_t *orow = out + (qm * H + h) * D + 4 * h2;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        *reinterpret_cast<uint2 *>(orow + 32 * ct + 8 * jj) =
+            make_uint2(pack_bf16x2(o[ct][4 * jj] * so, o[ct][4 * jj + 1] * so),
+                       pack_bf16x2(o[ct][4 * jj + 2] * so, o[ct][4 * jj + 3] * so));
+  } else {
+    const int64_t pr = (qm * NS + s) * H + h;
+    uint16_t *po = part_o + pr * D + 4 * h2;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        *reinterpret_cast<uint2 *>(po + 32 * ct + 8 * jj) = make_uint2(pack_bf16x2(o[ct][4 * jj], o[ct][4 * jj + 1]),
+                                                                       pack_bf16x2(o[ct][4 * jj + 2], o[ct][4 * jj + 3]));
+    if (h2 == 0) {
+      part_ml[pr * 2] = m_ref;
+      part_ml[pr * 2 + 1] = l_run;
+    }
+  }
+}
+
+constexpr size_t kCntMaxShmem = 64 * 1024;  // dynamic LDS without a per-kernel attribute
+inline size_t count_shmem(int64_t H, int64_t kr) {
+  return static_cast<size_t>(kCntBufs) * 32 * 128 * 2 + static_cast<size_t>(kCntRows / H) * kr * 4;
+}
+
+struct CntPlan {
+  int ns, kr;
+  int64_t tgb;  // row blocks per batch
+};
+
+// The count-mask kernel takes dense lists (K >= N / 4) over kv sets past the small-kv kernel's, with whole
+// 128-row blocks (M H >= 128, H dividing 128).  Splits: about one workgroup per CU, at most kCntMaxKR keys each,
+// and no more ranges than the gather plan's, whose workspace size the caller was given (the workspace query does
+// not see N).
+inline bool count_plan(int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, const void *out, CntPlan &p) {
+  if (N <= kDenseMaxN || K * 4 < N || kCntRows % H != 0 || M * H < kCntRows || !aligned(out, 8)) return false;
+  const int64_t tgb = ceil_div(M * H, kCntRows);
+  int64_t ns = ceil_div(kCntTargetWgs, B * tgb);
+  const int64_t ns_min = ceil_div(N, kCntMaxKR);
+  const int64_t ns_max = ceil_div(N, 4 * 32) > ns_min ? ceil_div(N, 4 * 32) : ns_min;  // >= 4 chunks per split
+  ns = ns < ns_min ? ns_min : ns > ns_max ? ns_max : ns;
+  const SaSplit sp = split_plan(B, M, H, K);
+  if (ns > sp.ns) ns = sp.ns;
+  if (ns < ns_min) return false;
+  const int64_t kr = ceil_div(ceil_div(N, ns), 32) * 32;
+  ns = ceil_div(N, kr);  // no empty split (and no more than before)
+  if (count_shmem(H, kr) > kCntMaxShmem) return false;
+  if (B * tgb * ns >= (int64_t(1) << 31)) return false;
+  p = CntPlan{static_cast<int>(ns), static_cast<int>(kr), tgb};
+  return true;
+}
+
+int launch_sa_count(const CntPlan &p, const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx,
+                    uint16_t *out, int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws,
+                    hipStream_t stream) {
+  float *part_ml = nullptr;
+  uint16_t *part_o = nullptr;
+  if (p.ns > 1) {
+    part_ml = static_cast<float *>(ws);
+    part_o = reinterpret_cast<uint16_t *>(part_ml + B * M * p.ns * H * 2);
+  }
+  const size_t shmem = count_shmem(H, p.kr);
+  const int idx_vec = (K % 4 == 0 && aligned(idx, 16)) ? 1 : 0;
+  const int64_t wgs = B * p.tgb * p.ns;
+  hipLaunchKernelGGL(sparse_attn_count_kernel, dim3(static_cast<unsigned>(wgs)), dim3(256), shmem, stream, q, kv, sink,
+                     idx, out, part_o, part_ml, M, static_cast<int>(H), static_cast<int>(N), static_cast<int>(K), p.ns,
+                     p.kr, p.tgb, scale * kLog2e, idx_vec);
+  KS_CHECK_LAUNCH("sparse_attn_count_kernel");
+  if (p.ns > 1) {
+    const int64_t rows = B * M * H;
+    hipLaunchKernelGGL((sparse_attn_combine_kernel<128>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
+                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), p.ns);
+    KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
+  }
+  return KS_OK;
+}
+
 template <int DQK, int DV>
 int launch_sa(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
               int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
@@ -1467,6 +1839,28 @@ extern "C" int ks_sparse_attn(const uint16_t *q, const uint16_t *kv, const float
   if (d128) return ks::launch_sa<128, 128>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
   if (ks::use_mla(Dqk, Dv, H, K)) return ks::launch_mla(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
   return ks::launch_sa<576, 512>(q, kv, sink, idx, out, B, M, H, N, K, scale, workspace, st);
+}
+
+// Diagnostic export (not in include/kswift.h): ks_sparse_attn's contract on the count-mask kernel, for the shapes its
+// plan takes (Dqk = Dv = 128, K >= N / 4, N > 64, H dividing 128, M H >= 128).  ks_sparse_attn does not dispatch to
+// it: at every density measured it was slower than the gather kernel.  Kept to time the dense formulation beside
+// the gather kernel and to keep its parity tested.
+extern "C" int ks_dbg_sparse_attn_count(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx,
+                                        uint16_t *out, int64_t B, int64_t M, int64_t H, int64_t N, int64_t K,
+                                        float scale, void *workspace, size_t workspace_bytes, void *stream) {
+  ks::last_error().clear();
+  KS_CHECK_ARG(B >= 1 && M >= 1 && N >= 1 && K >= 1 && H >= 1 && M < 65536 && B < 65536 && K < (int64_t(1) << 31) &&
+                   N * 256 < (int64_t(1) << 32),
+               "ks_dbg_sparse_attn_count: bad sizes");
+  KS_CHECK_ARG(q && kv && sink && idx && out && ks::aligned(q, 16) && ks::aligned(kv, 16),
+               "ks_dbg_sparse_attn_count: null or misaligned pointer");
+  ks::CntPlan cp;
+  KS_CHECK_ARG(ks::count_plan(B, M, H, N, K, out, cp), "ks_dbg_sparse_attn_count: shape outside the kernel's plan");
+  const size_t need = ks::sa_workspace(B, M, H, 128, K, 128);
+  KS_CHECK_ARG(need == 0 || (workspace != nullptr && workspace_bytes >= need && ks::aligned(workspace, 16)),
+               "ks_dbg_sparse_attn_count: workspace of %zu bytes required", need);
+  return ks::launch_sa_count(cp, q, kv, sink, idx, out, B, M, H, N, K, scale, workspace,
+                             static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------- the entry point that allocates nothing

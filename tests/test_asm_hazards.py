@@ -59,7 +59,7 @@ def test_mla_kernels_have_no_mfma_hazards(tmp_path):
     from kernelswift_amd import build as ksbuild
     src = os.path.join(REPO, "kernelswift_amd", "csrc", "sparse_attn.hip")
     out = tmp_path / "sparse_attn.s"
-    cmd = [ksbuild.HIPCC, *ksbuild.COMMON, "--cuda-device-only", "-S", src, "-o", str(out)]
+    cmd = [ksbuild.HIPCC, *ksbuild.flags(src), "--cuda-device-only", "-S", src, "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
     asm = out.read_text()
@@ -100,7 +100,7 @@ def test_lds_dma_kernels_use_m0_only_for_the_dma(tmp_path):
     from kernelswift_amd import build as ksbuild
     src = os.path.join(REPO, "kernelswift_amd", "csrc", "sparse_attn.hip")
     out = tmp_path / "sparse_attn_m0.s"
-    r = subprocess.run([ksbuild.HIPCC, *ksbuild.COMMON, "--cuda-device-only", "-S", src, "-o", str(out)],
+    r = subprocess.run([ksbuild.HIPCC, *ksbuild.flags(src), "--cuda-device-only", "-S", src, "-o", str(out)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
     asm = out.read_text()

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import oracle
-from kernelswift_amd import ops, workloads
+from kernelswift_amd import _lib, ops, workloads
 
 pytestmark = pytest.mark.gpu
 bits = workloads.bf16_bits
@@ -182,3 +182,42 @@ def test_sparse_attn_mla_leading_invalid(device):
     got = _run(q.to(device), kv.to(device), sink.to(device), idx.to(device), 576 ** -0.5, 512, "mla-leading-invalid")
     want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), idx.numpy(), 576 ** -0.5, 512)
     np.testing.assert_allclose(got, want, **TOL)
+
+
+# The count-mask kernel (ks_dbg_sparse_attn_count: the dense formulation over key splits, timed beside the gather
+# kernel by bench.py; ks_sparse_attn does not dispatch to it): one split finalised in place or several merged by the
+# combine kernel; N not a multiple of the 32-key chunk; the last 128-row block of a batch partly past the batch;
+# every head count; K above N (many duplicates); K not a multiple of 4 (the scalar count path); invalid indices on
+# both sides; an all-invalid row; config 3's shape.
+def _run_count(q, kv, sink, idx, scale, tag):
+    print(f"[case] sparse_attn_count {tag}", flush=True)
+    B, M, H, _ = q.shape
+    N, K = kv.shape[1], idx.shape[-1]
+    lib = _lib.load()
+    need = lib.ks_sparse_attn_workspace_size(B, M, H, 128, 128, K)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    out = torch.empty(B, M, H, 128, dtype=torch.bfloat16, device=q.device)
+    rc = lib.ks_dbg_sparse_attn_count(q.data_ptr(), kv.data_ptr(), sink.data_ptr(), idx.data_ptr(), out.data_ptr(), B, M,
+                                      H, N, K, scale, ws.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "ks_dbg_sparse_attn_count")
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("H,B,M,N,K", [(16, 2, 9, 300, 100), (32, 1, 40, 1000, 600), (64, 2, 6, 2500, 1000),
+                                       (128, 1, 3, 4100, 1200), (64, 1, 521, 200, 64), (16, 1, 16, 100, 300),
+                                       (16, 1, 16, 100, 301), (16, 3, 24, 4096, 1024), (16, 1, 128, 8192, 2048)])
+def test_sparse_attn_count_mask(device, H, B, M, N, K):
+    g = torch.Generator().manual_seed(H * 13 + N + K)
+    q = torch.randn(B, M, H, 128, generator=g).bfloat16()
+    kv = torch.randn(B, N, 128, generator=g).bfloat16()
+    idx = torch.randint(-3, N + 3, (B, M, K), generator=g, dtype=torch.int32)  # invalid: < 0 and >= N
+    idx[0, 0] = -1  # an all-invalid row -> output 0
+    idx[-1, -1, : K // 3] = N - 1  # duplicates count with multiplicity (the last key of the last split)
+    sink = torch.randn(H, generator=g)
+    got = _run_count(q.to(device), kv.to(device), sink.to(device), idx.to(device), 128 ** -0.5,
+                     f"H={H} B={B} M={M} N={N} K={K}")
+    ok = (idx >= 0) & (idx < N)
+    want = oracle.sparse_attn(bits(q), bits(kv), sink.numpy(), torch.where(ok, idx, -1).numpy(), 128 ** -0.5, 128)
+    np.testing.assert_allclose(got, want, **TOL)
+    assert np.all(got[0, 0] == 0)

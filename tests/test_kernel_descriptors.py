@@ -114,7 +114,7 @@ def compiled(tmp_path_factory):
 
     def compile_one(src):
         out = tmp / (os.path.basename(src) + ".s")
-        r = subprocess.run([ksbuild.HIPCC, *ksbuild.COMMON, "--cuda-device-only", "-S", src, "-o", str(out)],
+        r = subprocess.run([ksbuild.HIPCC, *ksbuild.flags(src), "--cuda-device-only", "-S", src, "-o", str(out)],
                            capture_output=True, text=True)
         assert r.returncode == 0, r.stderr[-2000:]
         return src, out.read_text()

@@ -1439,6 +1439,8 @@ int launch_sa_dense(const uint16_t *q, const uint16_t *kv, const float *sink, co
 //              are, and the matching V^T fragment is two ds_read_b64_tr_b16 reads.  O^T keeps one row per lane,
 //              so a rescale needs no exchange.
 // Partial ranges (O in bf16, max, sum) go through sparse_attn_combine_kernel; one split finalises in place.
+// Measured slower than the gather kernel at every density tried (config 3: 27 against 15 us; at 100% density 19
+// against 15 us), so ks_sparse_attn does not dispatch to it; ks_dbg_sparse_attn_count exposes it for timing.
 constexpr int kCntRows = 128;       // (query, head) rows per workgroup
 constexpr int kCntMaxKR = 2048;     // keys per split (LDS counts: 128 / H queries x KR x 4 bytes)
 constexpr int kCntBufs = 3;         // chunk ring

@@ -1427,8 +1427,8 @@ int launch_sa_dense(const uint16_t *q, const uint16_t *kv, const float *sink, co
 //              of KR keys; one wave per SIMD (registers: 4 x 16 O^T accumulators, 8 q fragments, two S^T tiles)
 //   counts     the workgroup's index rows read once (all loads in flight together) and counted into LDS with
 //              ds_add: invalid indices count nowhere, duplicates with multiplicity
-//   chunks     32 keys x 128 dims, DMA'd into a 3-buffer ring in the gather kernel's swizzled layout; at chunk c
-//              chunk c + 1 has landed and chunk c + 2 is in flight (one barrier per chunk)
+//   chunks     32 keys x 128 dims, DMA'd into a 4-buffer ring in a swizzled row-major layout; at chunk c
+//              chunk c + 1 has landed and chunks c + 2, c + 3 are in flight (one barrier per chunk)
 //   QK^T       S^T = K Q^T (M = 32 keys, N = 32 rows, K = 16 dims); lane (row l%32, half h = l/32) receives keys
 //              8j + 4h + r (j, r = 0..3).  Chunk c + 1's QK is issued before chunk c's softmax.
 //   softmax    p = 2^(s + log2(count) - m) with the lazily updated reference max of the gather kernel (the counts
@@ -1443,7 +1443,7 @@ int launch_sa_dense(const uint16_t *q, const uint16_t *kv, const float *sink, co
 // against 15 us), so ks_sparse_attn does not dispatch to it; ks_dbg_sparse_attn_count exposes it for timing.
 constexpr int kCntRows = 128;       // (query, head) rows per workgroup
 constexpr int kCntMaxKR = 2048;     // keys per split (LDS counts: 128 / H queries x KR x 4 bytes)
-constexpr int kCntBufs = 3;         // chunk ring
+constexpr int kCntBufs = 4;         // chunk ring: chunks c + 1 and c + 2 in flight while chunk c is computed
 constexpr int kCntTargetWgs = 256;  // one workgroup per CU
 constexpr int kCntIdxBatch = 16;    // index loads in flight per thread while counting
 
@@ -1458,7 +1458,6 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     const int32_t *__restrict__ idx, uint16_t *__restrict__ out, uint16_t *__restrict__ part_o,
     float *__restrict__ part_ml, int64_t M, int H, int N, int K, int NS, int KR, int64_t tgb, float scale_log2,
     int idx_vec) {
-  using Sh = SaShape<128, 128, 1>;                // the swizzle of 16-unit rows
   constexpr int D = 128, BUF = 32 * D;            // bf16 elements per chunk buffer
   extern __shared__ uint4 smem_cnt[];
   uint16_t *kb = reinterpret_cast<uint16_t *>(smem_cnt);               // [kCntBufs][BUF]
@@ -1482,13 +1481,18 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
   const global_ptr<const uint16_t> kvb = uniform_ptr(kv + b * static_cast<int64_t>(N) * D);
   const uint32_t kb_lds = __builtin_amdgcn_readfirstlane(lds_addr(kb));
 
-  // ---- chunk DMA: slot 64 (wave + 4 i) + lane of a buffer holds unit (slot % 16) ^ swz(key) of key slot / 16
+  // ---- chunk layout: unit u of key k in slot 16 k + (u ^ swz(k)), swz(k) = 4 (k & 3) + 2 ((k >> 2) & 1).  The QK
+  // reads (8 keys, one unit) and the PV transpose reads (per 32 lanes 4 keys x 4 units, or 4 units + 2 for keys
+  // 4..7 of an 8-key group) then hit distinct banks.  DMA slot 64 (wave + 4 i) + lane holds unit (slot % 16) ^
+  // swz(key) of key slot / 16.
+  auto swz = [](int k) { return 4 * (k & 3) + 2 * ((k >> 2) & 1); };
+  auto cslot = [&](int k, int u) { return 16 * k + (u ^ swz(k)); };
   int dkey[2], doff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int sl = 64 * (wave + 4 * i) + lane;
     dkey[i] = sl / 16;
-    doff[i] = ((sl % 16) ^ Sh::swz(dkey[i])) * 16;
+    doff[i] = ((sl % 16) ^ swz(dkey[i])) * 16;
   }
   auto dma_chunk = [&](int c, int buf) {
 #pragma unroll
@@ -1499,8 +1503,9 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
             kb_lds + (buf * BUF + 64 * (wave + 4 * i) * 8) * 2);
     }
   };
-  dma_chunk(0, 0);
-  if (nch > 1) dma_chunk(1, 1);
+#pragma unroll
+  for (int i = 0; i < kCntBufs - 1; ++i)
+    if (i < nch) dma_chunk(i, i);
 
   // ---- q B-fragments: row (wave's 32 rows, lane c32), dims 16j + 8h .. +7; rows past the batch read its last row
   const int64_t qrow = row0 + 32 * wave + c32;
@@ -1515,11 +1520,20 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
   __syncthreads();
   {
     const int32_t *ib = idx + (b * M + m0) * static_cast<int64_t>(K);  // qv consecutive index rows
-    auto count = [&](int e, int32_t v) {
-      if (v >= k_lo && v < k_hi) atomicAdd(&cnt[(e / K) * KR + (v - k_lo)], 1u);
+    // row of element e of the qv x K index block (the float quotient is within one of e / K: qv <= 8)
+    const float inv_k = 1.f / static_cast<float>(K);
+    auto row_of = [&](int e) {
+      int r = static_cast<int>(static_cast<float>(e) * inv_k);
+      r -= static_cast<int64_t>(r) * K > e ? 1 : 0;
+      r += static_cast<int64_t>(r + 1) * K <= e ? 1 : 0;
+      return r;
+    };
+    const uint32_t span = static_cast<uint32_t>(k_hi - k_lo);
+    auto count = [&](int rbase, int32_t v) {  // rbase = row * KR - k_lo
+      if (static_cast<uint32_t>(v - k_lo) < span) atomicAdd(&cnt[rbase + v], 1u);
     };
     const int tot = qv * K;
-    if (idx_vec) {  // K % 4 == 0 and 16-byte aligned rows
+    if (idx_vec) {  // K % 4 == 0 and 16-byte aligned rows: the four indices of an int4 share a row
       const int4 *ib4 = reinterpret_cast<const int4 *>(ib);
       const int n4 = tot >> 2;
       for (int base = 0; base < n4; base += 256 * kCntIdxBatch) {
@@ -1533,10 +1547,11 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
         for (int j = 0; j < kCntIdxBatch; ++j) {
           const int u = base + 256 * j + tid;
           if (u < n4) {
-            count(4 * u, v[j].x);
-            count(4 * u, v[j].y);
-            count(4 * u, v[j].z);
-            count(4 * u, v[j].w);
+            const int rb = row_of(4 * u) * KR - k_lo;
+            count(rb, v[j].x);
+            count(rb, v[j].y);
+            count(rb, v[j].z);
+            count(rb, v[j].w);
           }
         }
       }
@@ -1551,7 +1566,7 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
 #pragma unroll
         for (int j = 0; j < kCntIdxBatch; ++j) {
           const int e = base + 256 * j + tid;
-          if (e < tot) count(e, v[j]);
+          if (e < tot) count(row_of(e) * KR - k_lo, v[j]);
         }
       }
     }
@@ -1565,18 +1580,18 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
     *w = make_uint4(lw(c.x), lw(c.y), lw(c.z), lw(c.w));
   }
   wait_dma();
-  __syncthreads();  // weights complete, chunks 0 and 1 visible
+  __syncthreads();  // weights complete, chunks 0 to 2 visible
 
   // ---- per-lane LDS element offsets.  QK: key c32, unit 2j + h (swizzled per j).  PV (transpose reads): lane
   // 16R + 4e + jj addresses key 4(R >> 1) + e (+ 8, + 16 s), columns 32 ct + 16 (R & 1) + 4 jj .. +3
   int qk_off[8], pv_off[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) qk_off[j] = Sh::slot(c32, 0, 2 * j + h2) * 8;
+  for (int j = 0; j < 8; ++j) qk_off[j] = cslot(c32, 2 * j + h2) * 8;
   {
     const int R = lane >> 4, e = (lane >> 2) & 3, jj = lane & 3;
     const int key = 4 * (R >> 1) + e;
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) pv_off[ct] = Sh::slot(key, 0, 4 * ct + 2 * (R & 1) + (jj >> 1)) * 8 + 4 * (jj & 1);
+    for (int ct = 0; ct < 4; ++ct) pv_off[ct] = cslot(key, 4 * ct + 2 * (R & 1) + (jj >> 1)) * 8 + 4 * (jj & 1);
   }
   const int qi = (32 * wave + c32) / H;  // the lane's query in the workgroup's count rows
   const float *crow = reinterpret_cast<const float *>(cnt) + qi * KR + 4 * h2;  // log2 weights
@@ -1642,10 +1657,12 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
   // Two stages per chunk c: (A) chunk c + 1's QK MFMAs beside chunk c's exponentials and bf16 packing, (B) chunk
   // c's PV MFMAs beside chunk c + 1's scores and row max.  A rescale for chunk c + 1 (rare) then scales O, which
   // holds chunk c, and the sum.  On the last chunk the "next" buffer and weights are stale and unused.
+  static_assert(kCntBufs == 4, "the waits below keep one chunk (two DMA instructions per thread) in flight");
   for (int c = 0; c < nch; ++c) {
-    if (c + 1 < nch) wait_dma();  // this thread's part of chunk c + 1
-    __syncthreads();              // chunk c + 1 visible; every wave is done with chunk c - 1's buffer
-    if (c + 2 < nch) dma_chunk(c + 2, (c + 2) % kCntBufs);
+    if (c + 2 < nch) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");  // this thread's part of chunk c + 1
+    else if (c + 1 < nch) wait_dma();
+    __syncthreads();  // chunk c + 1 visible; every wave is done with chunk c - 1's buffer
+    if (c + 3 < nch) dma_chunk(c + 3, (c + 3) % kCntBufs);
     uint4 kf[8], vf[4][2];
     float w[16];
     kfrags((c + 1) % kCntBufs, kf);
@@ -1749,6 +1766,7 @@ struct CntPlan {
 // not see N).
 inline bool count_plan(int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, const void *out, CntPlan &p) {
   if (N <= kDenseMaxN || K * 4 < N || kCntRows % H != 0 || M * H < kCntRows || !aligned(out, 8)) return false;
+  if (K * (kCntRows / H) >= (int64_t(1) << 31)) return false;  // the workgroup's index block is int-indexed
   const int64_t tgb = ceil_div(M * H, kCntRows);
   int64_t ns = ceil_div(kCntTargetWgs, B * tgb);
   const int64_t ns_min = ceil_div(N, kCntMaxKR);

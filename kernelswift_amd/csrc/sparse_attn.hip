@@ -1031,8 +1031,9 @@ __global__ __launch_bounds__(256) void sparse_attn_mla_combine_kernel(const uint
 }
 
 // Merge the NS partial ranges of one (query, head) row with the sink: one wave per row, lane s reads
-// range s's (max, sum); every lane then accumulates DV/64 columns over the ranges.
-template <int DV>
+// range s's (max, sum); every lane then accumulates DV/64 columns over the ranges.  The first PRE ranges'
+// columns are loaded ahead of the reduction (PRE >= NS where NS <= 8, so no load is spent on a clamped range).
+template <int DV, int PRE>
 __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const uint16_t *__restrict__ part_o,
                                                                  const float *__restrict__ part_ml,
                                                                  const float *__restrict__ sink,
@@ -1050,7 +1051,7 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const uint16_t
   const int h = static_cast<int>(row % H);
   // every load of the first kPre ranges goes out before the first wait: the sink, the ranges' (max, sum)
   // (lane s: range min(s, NS - 1), masked below) and their O columns, which do not depend on them
-  constexpr int kPre = 8;
+  constexpr int kPre = PRE;
   const float sk_raw = sink[h];
   const float *ml = part_ml + ((qm * NS + (lane < NS ? lane : NS - 1)) * H + h) * 2;
   const float m_raw = ml[0], l_raw = ml[1];
@@ -1107,6 +1108,20 @@ __global__ __launch_bounds__(256) void sparse_attn_combine_kernel(const uint16_t
     *reinterpret_cast<uint32_t *>(orow + i) = pack_bf16x2(acc[i] * inv, acc[i + 1] * inv);
 }
 
+template <int DV>
+int launch_combine(const uint16_t *part_o, const float *part_ml, const float *sink, uint16_t *out, int64_t rows, int H,
+                   int NS, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(rows, 4))), block(256);
+  if (NS <= 2)
+    hipLaunchKernelGGL((sparse_attn_combine_kernel<DV, 2>), grid, block, 0, stream, part_o, part_ml, sink, out, rows, H, NS);
+  else if (NS <= 4)
+    hipLaunchKernelGGL((sparse_attn_combine_kernel<DV, 4>), grid, block, 0, stream, part_o, part_ml, sink, out, rows, H, NS);
+  else
+    hipLaunchKernelGGL((sparse_attn_combine_kernel<DV, 8>), grid, block, 0, stream, part_o, part_ml, sink, out, rows, H, NS);
+  KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
+  return KS_OK;
+}
+
 template <int DQK, int DV, int GW>
 int launch_sa_gw(const uint16_t *q, const uint16_t *kv, const float *sink, const int32_t *idx, uint16_t *out,
                  int64_t B, int64_t M, int64_t H, int64_t N, int64_t K, float scale, void *ws, hipStream_t stream) {
@@ -1129,12 +1144,7 @@ int launch_sa_gw(const uint16_t *q, const uint16_t *kv, const float *sink, const
   // one-wave groups merge the ranges of a workgroup in LDS when a workgroup holds whole ranges of a query
   const bool merged = GW == 1 && Sh::GROUPS > 1 && sp.ns % Sh::GROUPS == 0;
   const int ns_left = merged ? sp.ns / Sh::GROUPS : sp.ns;
-  if (ns_left > 1) {
-    const int64_t rows = B * M * H;
-    hipLaunchKernelGGL((sparse_attn_combine_kernel<DV>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
-                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), ns_left);
-    KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
-  }
+  if (ns_left > 1) return launch_combine<DV>(part_o, part_ml, sink, out, B * M * H, static_cast<int>(H), ns_left, stream);
   return KS_OK;
 }
 
@@ -1801,9 +1811,8 @@ int launch_sa_count(const CntPlan &p, const uint16_t *q, const uint16_t *kv, con
   KS_CHECK_LAUNCH("sparse_attn_count_kernel");
   if (p.ns > 1) {
     const int64_t rows = B * M * H;
-    hipLaunchKernelGGL((sparse_attn_combine_kernel<128>), dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256),
-                       0, stream, part_o, part_ml, sink, out, rows, static_cast<int>(H), p.ns);
-    KS_CHECK_LAUNCH("sparse_attn_combine_kernel");
+    const int rc = launch_combine<128>(part_o, part_ml, sink, out, rows, static_cast<int>(H), p.ns, stream);
+    if (rc != KS_OK) return rc;
   }
   return KS_OK;
 }

@@ -388,7 +388,7 @@ def run_sparse(cfg, steps, warmup, do_cpu, cpu_budget):
            "roofline": {"bound": "mfma", "kernel": ("sparse_attn_kernel" if cfg == 3 else "sparse_attn_mla_kernel")
                         + " (+ combine)", "achieved": round(achieved, 2),
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                        "traffic": (_traffic("sparse_attn_kernel<128, 128, 1>@3", "sparse_attn_combine_kernel<128>@3")
+                        "traffic": (_traffic("sparse_attn_kernel<128, 128, 1>@3", "sparse_attn_combine_kernel<128, 2>@3")
                                     if cfg == 3 else
                                     _traffic("sparse_attn_mla_kernel<4, 3>@5", "sparse_attn_mla_combine_kernel@5")),
                         "cache": ("warm (the 2 MiB kv fits in L2)" if cfg == 3
